@@ -1,0 +1,79 @@
+"""Build the gfx950 HIP library `libvgo.so` in-tree with hipcc.
+
+Every `csrc/*.hip` file is compiled to an object under `_build/` and linked
+into one shared library next to this file.  The library exports only the
+`extern "C"` entry points declared in `include/vgo.h`.
+"""
+from __future__ import annotations
+
+import concurrent.futures
+import os
+import shutil
+import subprocess
+from pathlib import Path
+
+PACKAGE_DIR = Path(__file__).resolve().parent
+CSRC = PACKAGE_DIR / "csrc"
+BUILD_DIR = PACKAGE_DIR / "_build"
+LIBRARY = PACKAGE_DIR / "libvgo.so"
+OFFLOAD_ARCH = "gfx950"
+
+# Packed fp32 VALU forms are switched off for every device compile.
+COMMON_FLAGS = [
+    f"--offload-arch={OFFLOAD_ARCH}",
+    "-O3",
+    "-fPIC",
+    "-std=c++17",
+    # IEEE operation order as written: fused multiply-adds only where fmaf() is
+    # spelled out, so reductions reproduce the reference's separate mul/add.
+    "-ffp-contract=off",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def hipcc() -> str:
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    candidate = Path(rocm) / "bin" / "hipcc"
+    if candidate.exists():
+        return str(candidate)
+    found = shutil.which("hipcc")
+    if not found:
+        raise RuntimeError("hipcc not found: the vgo HIP library cannot be built")
+    return found
+
+
+def _compile(source: Path) -> Path:
+    obj = BUILD_DIR / (source.stem + ".o")
+    cmd = [hipcc(), *COMMON_FLAGS, "-c", str(source), "-o", str(obj)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {source.name}:\n{proc.stderr}")
+    return obj
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compile every kernel for gfx950 and link `libvgo.so`; returns its path."""
+    BUILD_DIR.mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    if not sources:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    jobs = jobs or min(len(sources), max(1, (os.cpu_count() or 2) // 2), 16)
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
+        objects = list(pool.map(_compile, sources))
+    tmp = LIBRARY.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC",
+           *map(str, objects), "-o", str(tmp)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc link failed:\n{proc.stderr}")
+    os.replace(tmp, LIBRARY)
+    if verbose:
+        print(f"built {LIBRARY}")
+    return LIBRARY
+
+
+if __name__ == "__main__":
+    build(verbose=True)

@@ -1,0 +1,218 @@
+// Top-4 convex projection (unmerge), the restore step of a merge plan:
+//   out[i,:] = sum_{c<4} w[i,c] * table[index[i,c],:]
+//
+// Work of vggt_omega/models/token_merging.py:387-414 (WeightedBilinearTokenPlan.
+// restore: `parent = value[:, parent]; (parent * w.to(value.dtype)).sum(2)`) and
+// :193-196 (TokenPlan.restore, the one-hot case).  The reference materialises
+// [M,4,C] and sums it; here one wave streams one output row: its four gathers
+// are issued back to back (16 B per lane each), products are rounded to the
+// value type exactly as the reference's elementwise multiply does, summed in
+// fp32, and the row is written with non-temporal stores so the gathered table
+// keeps the L2/MALL.  HBM-bound: per output row it moves dim*s bytes of output
+// plus the 32 bytes of (index, weight); the table is compulsory traffic once.
+#include "vgo_common.h"
+
+namespace vgo {
+namespace {
+
+constexpr int kWaves = 4;  // waves per work-group; one output row per wave
+
+template <typename T>
+struct Vec16;  // 16 bytes of T
+template <>
+struct Vec16<float> {
+  typedef f32x4 type;
+  static constexpr int n = 4;
+};
+template <>
+struct Vec16<bf16_t> {
+  typedef bf16x8 type;
+  static constexpr int n = 8;
+};
+template <>
+struct Vec16<f16_t> {
+  typedef f16x8 type;
+  static constexpr int n = 8;
+};
+
+template <typename T>
+__device__ __forceinline__ float weight_as_value(float w) {
+  return to_f32(from_f32<T>(w));
+}
+template <>
+__device__ __forceinline__ float weight_as_value<float>(float w) {
+  return w;
+}
+
+// Product rounded to the value type (bf16/f16 multiply semantics), fp32 as is.
+template <typename T>
+__device__ __forceinline__ float rounded_product(float y, float w) {
+  return to_f32(from_f32<T>(y * w));
+}
+template <>
+__device__ __forceinline__ float rounded_product<float>(float y, float w) {
+  return __fmul_rn(y, w);
+}
+
+// CH = 16-byte chunks per lane kept in flight for each of the four gathers.
+template <typename T, int CH>
+__global__ __launch_bounds__(kWaves * 64) void top4_project_kernel(
+    const T* __restrict__ table, int64_t table_stride, const int32_t* __restrict__ index,
+    const float* __restrict__ weight, T* __restrict__ out, int64_t out_stride, int64_t n_rows,
+    int64_t table_rows, int dim) {
+  typedef typename Vec16<T>::type V;
+  constexpr int VN = Vec16<T>::n;
+  const int lane = lane_id();
+  const int64_t row = __builtin_amdgcn_readfirstlane(
+      static_cast<int>(blockIdx.x) * kWaves + static_cast<int>(threadIdx.x >> 6));
+  if (row >= n_rows) return;
+
+  const i32x4 id = *reinterpret_cast<const i32x4*>(index + 4 * row);
+  const f32x4 wt = *reinterpret_cast<const f32x4*>(weight + 4 * row);
+  bool use[4];
+  bool bad = false;
+  float wq[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    use[c] = wt[c] != 0.0f;
+    if (use[c] && static_cast<uint32_t>(id[c]) >= static_cast<uint64_t>(table_rows)) {
+      bad = true;
+      use[c] = false;
+    }
+    wq[c] = weight_as_value<T>(wt[c]);
+  }
+
+  T* orow = out + row * out_stride;
+  for (int base = 0; base < dim; base += CH * 64 * VN) {
+    V y[4][CH];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (use[c]) {
+        const T* trow = table + static_cast<int64_t>(id[c]) * table_stride;
+#pragma unroll
+        for (int ch = 0; ch < CH; ++ch) {
+          const int e = base + (ch * 64 + lane) * VN;
+          if (e < dim) y[c][ch] = *reinterpret_cast<const V*>(trow + e);
+        }
+      }
+    }
+#pragma unroll
+    for (int ch = 0; ch < CH; ++ch) {
+      const int e = base + (ch * 64 + lane) * VN;
+      if (e >= dim) continue;
+      float acc[VN];
+#pragma unroll
+      for (int j = 0; j < VN; ++j) acc[j] = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (use[c]) {
+#pragma unroll
+          for (int j = 0; j < VN; ++j)
+            acc[j] = __fadd_rn(acc[j], rounded_product<T>(to_f32(y[c][ch][j]), wq[c]));
+        }
+      }
+      V o;
+#pragma unroll
+      for (int j = 0; j < VN; ++j) o[j] = from_f32<T>(bad ? __builtin_nanf("") : acc[j]);
+      __builtin_nontemporal_store(o, reinterpret_cast<V*>(orow + e));
+    }
+  }
+}
+
+// Fallback for rows whose byte size is not a multiple of 16: one element per lane.
+template <typename T>
+__global__ __launch_bounds__(256) void top4_project_scalar_kernel(
+    const T* __restrict__ table, int64_t table_stride, const int32_t* __restrict__ index,
+    const float* __restrict__ weight, T* __restrict__ out, int64_t out_stride, int64_t n_rows,
+    int64_t table_rows, int dim) {
+  const int64_t row = blockIdx.y;
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (row >= n_rows || e >= dim) return;
+  float acc = 0.0f;
+  bool bad = false;
+  for (int c = 0; c < 4; ++c) {
+    const float w = weight[4 * row + c];
+    if (w == 0.0f) continue;
+    const int32_t id = index[4 * row + c];
+    if (static_cast<uint32_t>(id) >= static_cast<uint64_t>(table_rows)) {
+      bad = true;
+      continue;
+    }
+    acc = __fadd_rn(acc, rounded_product<T>(to_f32(table[id * table_stride + e]),
+                                            weight_as_value<T>(w)));
+  }
+  out[row * out_stride + e] = from_f32<T>(bad ? __builtin_nanf("") : acc);
+}
+
+template <typename T>
+int launch_project(const void* table, int64_t table_stride, const int32_t* index,
+                   const float* weight, void* out, int64_t out_stride, int64_t n_rows,
+                   int64_t table_rows, int64_t dim, hipStream_t stream) {
+  const T* tb = static_cast<const T*>(table);
+  T* ob = static_cast<T*>(out);
+  constexpr int VN = Vec16<T>::n;
+  const bool vec_ok = (dim % VN == 0) && (table_stride % VN == 0) && (out_stride % VN == 0) &&
+                      aligned(table, 16) && aligned(out, 16);
+  if (vec_ok) {
+    const int64_t blocks = (n_rows + kWaves - 1) / kWaves;
+    VGO_REQUIRE(blocks <= 0x7fffffff, "top4_project: too many rows");
+    const int row_chunks = static_cast<int>((dim + 64 * VN - 1) / (64 * VN));
+    if (row_chunks >= 4) {
+      hipLaunchKernelGGL((top4_project_kernel<T, 4>), dim3(blocks), dim3(kWaves * 64), 0, stream,
+                         tb, table_stride, index, weight, ob, out_stride, n_rows, table_rows,
+                         static_cast<int>(dim));
+    } else if (row_chunks == 2 || row_chunks == 3) {
+      hipLaunchKernelGGL((top4_project_kernel<T, 2>), dim3(blocks), dim3(kWaves * 64), 0, stream,
+                         tb, table_stride, index, weight, ob, out_stride, n_rows, table_rows,
+                         static_cast<int>(dim));
+    } else {
+      hipLaunchKernelGGL((top4_project_kernel<T, 1>), dim3(blocks), dim3(kWaves * 64), 0, stream,
+                         tb, table_stride, index, weight, ob, out_stride, n_rows, table_rows,
+                         static_cast<int>(dim));
+    }
+  } else {
+    VGO_REQUIRE(n_rows <= 65535 * 1024LL, "top4_project: too many rows for the unaligned path");
+    dim3 grid(static_cast<unsigned>((dim + 255) / 256), 1, 1);
+    // Rows go on grid.y in slabs of 65535 (the y limit).
+    for (int64_t r0 = 0; r0 < n_rows; r0 += 65535) {
+      const int64_t nr = (n_rows - r0) < 65535 ? (n_rows - r0) : 65535;
+      grid.y = static_cast<unsigned>(nr);
+      hipLaunchKernelGGL((top4_project_scalar_kernel<T>), grid, dim3(256), 0, stream, tb,
+                         table_stride, index + 4 * r0, weight + 4 * r0, ob + r0 * out_stride,
+                         out_stride, nr, table_rows, static_cast<int>(dim));
+    }
+  }
+  return check_launch("top4_project");
+}
+
+}  // namespace
+}  // namespace vgo
+
+extern "C" int vgo_top4_project(const void* table, int64_t table_row_stride, const int32_t* index,
+                                const float* weight, void* out, int64_t out_row_stride,
+                                int64_t n_rows, int64_t table_rows, int64_t dim, int dtype,
+                                void* stream) {
+  using namespace vgo;
+  VGO_REQUIRE(n_rows >= 0 && table_rows >= 0 && dim >= 0, "top4_project: negative size");
+  if (n_rows == 0 || dim == 0) return VGO_OK;
+  VGO_REQUIRE(index && weight && out, "top4_project: null pointer");
+  VGO_REQUIRE(table || table_rows == 0, "top4_project: null table");
+  VGO_REQUIRE(dim <= 0x7fffffff, "top4_project: dim too large");
+  VGO_REQUIRE(table_row_stride >= dim && out_row_stride >= dim, "top4_project: row stride < dim");
+  VGO_REQUIRE(aligned(index, 16) && aligned(weight, 16),
+              "top4_project: index/weight must be 16-byte aligned [n,4] arrays");
+  hipStream_t s = as_stream(stream);
+  switch (dtype) {
+    case VGO_F32:
+      return launch_project<float>(table, table_row_stride, index, weight, out, out_row_stride,
+                                   n_rows, table_rows, dim, s);
+    case VGO_BF16:
+      return launch_project<bf16_t>(table, table_row_stride, index, weight, out, out_row_stride,
+                                    n_rows, table_rows, dim, s);
+    case VGO_F16:
+      return launch_project<f16_t>(table, table_row_stride, index, weight, out, out_row_stride,
+                                   n_rows, table_rows, dim, s);
+    default:
+      return fail(VGO_EINVAL, "top4_project: unknown dtype");
+  }
+}

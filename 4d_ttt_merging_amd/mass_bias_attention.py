@@ -1,0 +1,88 @@
+"""Mass-bias attention on gfx950: softmax(QK^T/sqrt(d) + log_key_mass) V.
+
+Drop-in for `vggt_omega.models.mass_bias_attention.mass_bias_attention`
+(reference vggt_omega/models/mass_bias_attention.py:85-129): same argument
+meaning, same autocast cast, same exception types and messages, same output
+allocation.  The arithmetic runs in the hand-written HIP kernel
+`vgo_mass_bias_attn_fwd` (csrc/attention.hip); there is no CPU path.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def _attention_into(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                    bias: torch.Tensor | None, out: torch.Tensor) -> torch.Tensor:
+    """Run the kernel on [B,H,N,64] views (any batch/head/token strides) into `out`."""
+    lib = _lib.load()
+    _lib.require_gpu(q, k, v, bias, out)
+    if not (q.dtype == k.dtype == v.dtype == out.dtype):
+        raise ValueError("q, k, v and the output must share one dtype")
+    if bias is not None:
+        if bias.dtype != q.dtype:
+            raise ValueError("the log-mass bias must be rounded to the query dtype")
+        bias = bias.contiguous()
+    views = []
+    for t in (q, k, v):
+        if t.stride(-1) != 1:
+            t = t.contiguous()
+        views.append(t)
+    q, k, v = views
+    if out.stride(-1) != 1:
+        raise ValueError("output channel stride must be 1")
+    batch, heads, n_query, head_dim = q.shape
+    status = lib.vgo_mass_bias_attn_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.ptr(bias), out.data_ptr(),
+        batch, heads, n_query, k.shape[-2], head_dim,
+        _lib.strides3(q), _lib.strides3(k), _lib.strides3(v), _lib.strides3(out),
+        _lib.dtype_code(q.dtype), _lib.stream_of(q),
+    )
+    _lib.check(status)
+    return out
+
+
+def mass_bias_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                        log_key_mass: torch.Tensor) -> torch.Tensor:
+    """Compute softmax(QK^T/sqrt(d) + log_key_mass)V exactly.
+
+    q, k, v: [batch, heads, tokens, 64] on the GPU; log_key_mass: Nk values
+    shared by every batch and head.  Under CUDA/HIP bf16 autocast fp32 inputs
+    are cast to bf16 first, as autocast SDPA would
+    (reference mass_bias_attention.py:96-107).  The bias is rounded to the
+    query dtype (reference :109).
+    """
+    try:
+        _lib.load()
+    except _lib.ExtensionUnavailable as error:
+        raise RuntimeError(str(error)) from error
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError("q, k and v must be [batch, heads, tokens, channels]")
+    if q.shape[-1] != 64 or k.shape[-1] != 64 or v.shape[-1] != 64:
+        raise ValueError("the initial fused kernel supports head_dim=64 only")
+    if k.shape != v.shape or q.shape[:2] != k.shape[:2]:
+        raise ValueError("incompatible q/k/v shapes")
+    autocast_bf16 = bool(
+        torch.is_autocast_enabled("cuda") and q.dtype == torch.float32
+        and torch.get_autocast_dtype("cuda") == torch.bfloat16
+    )
+    if autocast_bf16:
+        q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+    output_dtype = q.dtype
+    if output_dtype not in _lib.DTYPE_CODE:
+        raise ValueError(f"unsupported dtype {output_dtype}")
+    k, v = k.to(output_dtype), v.to(output_dtype)
+    bias = log_key_mass.reshape(-1).to(q.dtype)
+    if bias.numel() != k.shape[-2]:
+        raise ValueError("log_key_mass length does not match key tokens")
+    output = torch.empty(q.shape, device=q.device, dtype=output_dtype)
+    return _attention_into(q, k, v, bias, output)
+
+
+def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    """Unbiased attention (the dense special-query pass), same kernel, no bias."""
+    if q.shape[-1] != 64:
+        raise ValueError("the initial fused kernel supports head_dim=64 only")
+    output = torch.empty(q.shape, device=q.device, dtype=q.dtype)
+    return _attention_into(q, k.to(q.dtype), v.to(q.dtype), None, output)

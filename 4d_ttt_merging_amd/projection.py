@@ -1,0 +1,45 @@
+"""Top-4 convex projection (unmerge) on gfx950.
+
+`top4_project(table, index, weight)` returns out[i] = sum_c weight[i,c] *
+table[index[i,c]] with the reference's rounding: weights rounded to the value
+dtype, each product rounded to the value dtype, fp32 sum, result in the value
+dtype (reference vggt_omega/models/token_merging.py:408-413).  It is the kernel
+behind every plan `restore`.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def top4_project(table: torch.Tensor, index: torch.Tensor, weight: torch.Tensor, *,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """Gather four rows of `table` [M, D] per output row and take their weighted sum.
+
+    index: [N, 4] int32, weight: [N, 4] float32 (both contiguous).  Zero weights
+    skip their gather; an out-of-range index with a non-zero weight yields a NaN
+    row (the kernel never reads outside the table).
+    """
+    lib = _lib.load()
+    _lib.require_gpu(table, index, weight, out)
+    if table.ndim != 2 or index.ndim != 2 or index.shape[1] != 4 or weight.shape != index.shape:
+        raise ValueError("top4_project requires table [M,D], index [N,4] and weight [N,4]")
+    if index.dtype != torch.int32 or weight.dtype != torch.float32:
+        raise ValueError("top4_project requires int32 indices and float32 weights")
+    index = index.contiguous()
+    weight = weight.contiguous()
+    if table.stride(-1) != 1:
+        table = table.contiguous()
+    n_rows, dim = index.shape[0], table.shape[1]
+    if out is None:
+        out = torch.empty((n_rows, dim), device=table.device, dtype=table.dtype)
+    elif out.shape != (n_rows, dim) or out.dtype != table.dtype or out.stride(-1) != 1:
+        raise ValueError("top4_project output must be [N, D] of the table dtype")
+    status = lib.vgo_top4_project(
+        table.data_ptr(), table.stride(0), index.data_ptr(), weight.data_ptr(), out.data_ptr(),
+        out.stride(0), n_rows, table.shape[0], dim, _lib.dtype_code(table.dtype),
+        _lib.stream_of(table),
+    )
+    _lib.check(status)
+    return out

@@ -1,0 +1,70 @@
+"""The C ABI library loads and exports every entry point include/vgo.h declares.
+
+CPU only: nothing here launches a kernel.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from tests.conftest import ROOT, import_package
+
+HEADER = ROOT / "include" / "vgo.h"
+
+
+def declared_symbols() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(vgo_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = declared_symbols()
+    assert "vgo_mass_bias_attn_fwd" in names and "vgo_top4_project" in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib_mod = import_package("_lib")
+    lib = lib_mod.load()
+    missing = [name for name in declared_symbols() if not hasattr(lib, name)]
+    assert not missing, f"libvgo.so lacks {missing}"
+    # The binding declares a signature for each of them, too.
+    assert set(declared_symbols()) <= set(lib_mod.SIGNATURES)
+
+
+def test_abi_version_matches_header():
+    lib = import_package("_lib").load()
+    version = int(re.search(r"#define VGO_ABI_VERSION (\d+)", HEADER.read_text()).group(1))
+    assert lib.vgo_abi_version() == version
+
+
+def test_argument_errors_raise_value_error_without_a_gpu():
+    # Validation happens on the host before any launch, so this runs on CPU.
+    lib_mod = import_package("_lib")
+    lib = lib_mod.load()
+    strides = lib_mod.strides3
+    status = lib.vgo_mass_bias_attn_fwd(None, None, None, None, None, 1, 1, 1, 1, 32,
+                                        (ctypes.c_int64 * 3)(), (ctypes.c_int64 * 3)(),
+                                        (ctypes.c_int64 * 3)(), (ctypes.c_int64 * 3)(), 1, None)
+    assert status == lib_mod.VGO_EINVAL
+    assert "head_dim=64" in lib_mod.last_error()
+    with pytest.raises(ValueError, match="head_dim=64"):
+        lib_mod.check(status)
+    del strides
+
+
+def test_cpu_tensors_are_rejected():
+    vgo = import_package()
+    import torch
+    q = torch.zeros(1, 1, 4, 64)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        vgo.mass_bias_attention(q, q, q, torch.zeros(4))
+
+
+def test_library_symbols_are_only_the_c_abi():
+    # The shared object exports the vgo_* C entry points and no C++ kernel API.
+    lib_path = import_package("_lib").LIBRARY_PATH
+    assert Path(lib_path).exists()
