@@ -1,0 +1,173 @@
+"""Typed wrappers over the merge-path entry points of `libvgo.so`.
+
+Each wrapper validates shapes/dtypes on the host, allocates outputs and
+workspaces with torch (device memory only), and launches on torch's current
+stream.  No wrapper synchronises the device.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+
+def _c(ptr_or_tensor):
+    if ptr_or_tensor is None:
+        return None
+    return ptr_or_tensor.data_ptr()
+
+
+def normalize_rows(x: torch.Tensor, rows: torch.Tensor | None, eps: float,
+                   out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """out[r] = x[rows[r]] / max(||x[rows[r]]||, eps) for a 2-D x (unit column stride)."""
+    lib = _lib.load()
+    _lib.require_gpu(x, rows)
+    if x.ndim != 2 or x.stride(-1) != 1:
+        x = x.reshape(-1, x.shape[-1]).contiguous()
+    if rows is not None:
+        rows = rows.to(torch.int64).contiguous()
+    n = x.shape[0] if rows is None else rows.numel()
+    out = torch.empty((n, x.shape[1]), device=x.device, dtype=out_dtype)
+    status = lib.vgo_normalize_rows(
+        x.data_ptr(), x.stride(0), x.shape[0], _lib.dtype_code(x.dtype), _c(rows), n, x.shape[1],
+        float(eps), out.data_ptr(), out.stride(0), _lib.dtype_code(out_dtype), _lib.stream_of(x))
+    _lib.check(status)
+    return out
+
+
+def similarity_topk(src: torch.Tensor, dictionary: torch.Tensor, topk: int, *,
+                    src_rows: torch.Tensor | None = None,
+                    n_src_device: torch.Tensor | None = None, n_src: int | None = None,
+                    dict_ranges: tuple[int, int, int] | None = None,
+                    index_map: torch.Tensor | None = None, want_values: bool = True,
+                    index_dtype: torch.dtype = torch.int64,
+                    scores: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Top-K bf16 cosine matches of every source row against a dictionary.
+
+    dict_ranges = (n0, off1, n_dict): dictionary position j reads row j for
+    j < n0 and row off1 + j - n0 otherwise (default: all rows).  Returns
+    (values [n, K] fp32, indices [n, K]) with ties going to the lower position.
+    """
+    lib = _lib.load()
+    _lib.require_gpu(src, dictionary, src_rows, n_src_device, index_map, scores)
+    if src.dtype != torch.bfloat16 or dictionary.dtype != torch.bfloat16:
+        raise ValueError("similarity_topk expects bf16 operands")
+    if src.stride(-1) != 1:
+        src = src.contiguous()
+    if dictionary.stride(-1) != 1:
+        dictionary = dictionary.contiguous()
+    if dict_ranges is None:
+        dict_ranges = (dictionary.shape[0], 0, dictionary.shape[0])
+    n0, off1, n_dict = dict_ranges
+    if n_src is None:
+        n_src = src.shape[0] if src_rows is None else src_rows.numel()
+    if src_rows is not None:
+        src_rows = src_rows.to(torch.int64).contiguous()
+    parts = ctypes.c_int(0)
+    need = ctypes.c_size_t(0)
+    _lib.check(lib.vgo_similarity_topk_workspace(n_src, n_dict, topk, ctypes.byref(parts),
+                                                 ctypes.byref(need)))
+    workspace = torch.empty(max(1, need.value // 8), device=src.device, dtype=torch.int64)
+    values = torch.empty((n_src, topk), device=src.device, dtype=torch.float32) if want_values else None
+    index = torch.empty((n_src, topk), device=src.device, dtype=index_dtype)
+    idx64 = index if index_dtype == torch.int64 else None
+    idx32 = index if index_dtype == torch.int32 else None
+    if index_map is not None:
+        index_map = index_map.to(torch.int64).contiguous()
+    status = lib.vgo_similarity_topk(
+        src.data_ptr(), src.stride(0), src.shape[0], _c(src_rows), _c(n_src_device), n_src,
+        dictionary.data_ptr(), dictionary.stride(0), dictionary.shape[0], n0, off1, n_dict,
+        src.shape[1], topk, workspace.data_ptr(), workspace.numel() * 8, _c(values), _c(idx64),
+        _c(idx32), _c(index_map), _c(scores), 0 if scores is None else scores.stride(0),
+        _lib.stream_of(src))
+    _lib.check(status)
+    return values, index
+
+
+def csr_build(keys: torch.Tensor, n_buckets: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Stable bucket order: (order [n] int32 item ids, offsets [n_buckets+1] int32)."""
+    lib = _lib.load()
+    _lib.require_gpu(keys)
+    keys = keys.to(torch.int32).contiguous()
+    n = keys.numel()
+    need = ctypes.c_size_t(0)
+    _lib.check(lib.vgo_csr_workspace(n, n_buckets, ctypes.byref(need)))
+    workspace = torch.empty(max(256, need.value + 256), device=keys.device, dtype=torch.uint8)
+    base = workspace.data_ptr()
+    pad = (-base) % 256
+    order = torch.empty(n, device=keys.device, dtype=torch.int32)
+    offsets = torch.empty(n_buckets + 1, device=keys.device, dtype=torch.int32)
+    status = lib.vgo_csr_build(keys.data_ptr(), n, n_buckets, base + pad, need.value,
+                               order.data_ptr(), offsets.data_ptr(), _lib.stream_of(keys))
+    _lib.check(status)
+    return order, offsets
+
+
+def segment_mass(offsets: torch.Tensor, segs_per_row: int, order: torch.Tensor,
+                 weights: torch.Tensor | None, rows: int, start: float,
+                 want_log: bool = True) -> tuple[torch.Tensor, torch.Tensor | None]:
+    lib = _lib.load()
+    device = offsets.device
+    mass = torch.empty(rows, device=device, dtype=torch.float32)
+    log_mass = torch.empty(rows, device=device, dtype=torch.float32) if want_log else None
+    if weights is not None:
+        weights = weights.to(torch.float32).contiguous()
+    status = lib.vgo_segment_mass(
+        offsets.data_ptr(), segs_per_row, order.data_ptr(), _c(weights),
+        0 if weights is None else weights.numel(), rows, float(start), mass.data_ptr(),
+        _c(log_mass), _lib.stream_of(offsets))
+    _lib.check(status)
+    return mass, log_mass
+
+
+def token_layout(t: torch.Tensor) -> tuple[int, int]:
+    """(token stride, head stride) of a [N, C] or [H, N, 64] view for vgo_compact."""
+    if t.ndim == 2:
+        if t.stride(1) != 1:
+            raise ValueError("channel stride must be 1")
+        return t.stride(0), 64
+    if t.ndim == 3 and t.shape[-1] == 64 and t.stride(-1) == 1:
+        return t.stride(1), t.stride(0)
+    raise ValueError("compaction operands must be [N, C] or [H, N, 64] views")
+
+
+def compact_into(x: torch.Tensor, out: torch.Tensor, *, base_rows: torch.Tensor | None,
+                 offsets: torch.Tensor, segs_per_row: int, items: torch.Tensor | None,
+                 item_shift: int, item_rows: torch.Tensor | None, weights: torch.Tensor | None,
+                 normalizer: torch.Tensor | None) -> torch.Tensor:
+    """Segmented weighted pooling; x/out are [N, C] or head-major [H, N, 64] views."""
+    lib = _lib.load()
+    _lib.require_gpu(x, out)
+    if x.dtype != out.dtype:
+        raise ValueError("compaction input and output dtypes differ")
+    xts, xhs = token_layout(x)
+    ots, ohs = token_layout(out)
+    n_rows_x = x.shape[0] if x.ndim == 2 else x.shape[1]
+    rows = out.shape[0] if out.ndim == 2 else out.shape[1]
+    dim = out.shape[1] if out.ndim == 2 else out.shape[0] * 64
+    status = lib.vgo_compact(
+        x.data_ptr(), xts, xhs, n_rows_x, _c(base_rows), offsets.data_ptr(), segs_per_row,
+        _c(items), item_shift, _c(item_rows), _c(weights), 0 if weights is None else weights.numel(),
+        _c(normalizer), rows, dim, out.data_ptr(), ots, ohs, _lib.dtype_code(x.dtype),
+        _lib.stream_of(x))
+    _lib.check(status)
+    return out
+
+
+def restore_map(total: int, *, device: torch.device, keep: torch.Tensor | None = None,
+                source: torch.Tensor | None = None, parent: torch.Tensor | None = None,
+                weight: torch.Tensor | None = None,
+                inverse: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Dense [total, 4] (int32 index, fp32 weight) rows consumed by top4_project."""
+    lib = _lib.load()
+    index_out = torch.zeros((total, 4), device=device, dtype=torch.int32)
+    weight_out = torch.zeros((total, 4), device=device, dtype=torch.float32)
+    n_keep = 0 if keep is None else keep.numel()
+    n_source = 0 if source is None else source.numel()
+    status = lib.vgo_restore_map(
+        _c(keep), n_keep, _c(source), _c(parent), _c(weight), n_source, _c(inverse), total,
+        index_out.data_ptr(), weight_out.data_ptr(), torch.cuda.current_stream(device).cuda_stream)
+    _lib.check(status)
+    return index_out, weight_out

@@ -42,6 +42,40 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "vgo_top4_project": (_c_int, [
         _c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_p,
     ]),
+    "vgo_normalize_rows": (_c_int, [
+        _c_p, _c_i64, _c_i64, _c_int, _c_p, _c_i64, _c_i64, _c_f32, _c_p, _c_i64, _c_int, _c_p,
+    ]),
+    "vgo_similarity_topk_workspace": (_c_int, [
+        _c_i64, _c_i64, _c_int, ctypes.POINTER(_c_int), ctypes.POINTER(_c_size),
+    ]),
+    "vgo_similarity_topk": (_c_int, [
+        _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+        _c_i64, _c_int, _c_p, _c_size, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p,
+    ]),
+    "vgo_fastvggt_assemble": (_c_int, [
+        _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p,
+    ]),
+    "vgo_sparse_convex_assemble": (_c_int, [
+        _c_p, _c_p, _c_p, _c_p, _c_p, _c_f32, _c_p, _c_i64, _c_i64, _c_f32, _c_p, _c_p, _c_p,
+        _c_p, _c_p, _c_p, _c_p,
+    ]),
+    "vgo_csr_workspace": (_c_int, [_c_i64, _c_i64, ctypes.POINTER(_c_size)]),
+    "vgo_csr_build": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_size, _c_p, _c_p, _c_p]),
+    "vgo_segment_mass": (_c_int, [
+        _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_f32, _c_p, _c_p, _c_p,
+    ]),
+    "vgo_compact": (_c_int, [
+        _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_int, _c_p, _c_p, _c_i64, _c_p,
+        _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_int, _c_p,
+    ]),
+    "vgo_restore_map": (_c_int, [
+        _c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p,
+    ]),
+    "vgo_convex_fit": (_c_int, [
+        _c_p, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_p, _c_p, _c_f32, _c_p, _c_p, _c_i64, _c_i64,
+        _c_f32, _c_f32, _c_p, _c_p, _c_p,
+    ]),
+    "vgo_failed_rows": (_c_int, [_c_p, _c_p, _c_f32, _c_i64, _c_f32, _c_p, _c_p, _c_p]),
 }
 
 _lock = threading.Lock()

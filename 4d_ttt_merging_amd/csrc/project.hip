@@ -51,11 +51,13 @@ __device__ __forceinline__ float rounded_product(float y, float w) {
 }
 template <>
 __device__ __forceinline__ float rounded_product<float>(float y, float w) {
-  return __fmul_rn(y, w);
+  return y * w;
 }
 
-// CH = 16-byte chunks per lane kept in flight for each of the four gathers.
-template <typename T, int CH>
+// Persistent waves: each wave owns R consecutive output rows per step and issues
+// the gathers of all R rows (4 corners x CH 16-byte chunks per lane each) before
+// reducing any of them, so a CU keeps hundreds of KB of gathers in flight.
+template <typename T, int R, int CH>
 __global__ __launch_bounds__(kWaves * 64) void top4_project_kernel(
     const T* __restrict__ table, int64_t table_stride, const int32_t* __restrict__ index,
     const float* __restrict__ weight, T* __restrict__ out, int64_t out_stride, int64_t n_rows,
@@ -63,58 +65,79 @@ __global__ __launch_bounds__(kWaves * 64) void top4_project_kernel(
   typedef typename Vec16<T>::type V;
   constexpr int VN = Vec16<T>::n;
   const int lane = lane_id();
-  const int64_t row = __builtin_amdgcn_readfirstlane(
+  const int64_t wave_gid = __builtin_amdgcn_readfirstlane(
       static_cast<int>(blockIdx.x) * kWaves + static_cast<int>(threadIdx.x >> 6));
-  if (row >= n_rows) return;
+  const int64_t step = static_cast<int64_t>(gridDim.x) * kWaves * R;
 
-  const i32x4 id = *reinterpret_cast<const i32x4*>(index + 4 * row);
-  const f32x4 wt = *reinterpret_cast<const f32x4*>(weight + 4 * row);
-  bool use[4];
-  bool bad = false;
-  float wq[4];
+  for (int64_t r0 = wave_gid * R; r0 < n_rows; r0 += step) {
+    int32_t id[R][4];
+    float wq[R][4];
+    bool use[R][4];
+    bool bad[R];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    use[c] = wt[c] != 0.0f;
-    if (use[c] && static_cast<uint32_t>(id[c]) >= static_cast<uint64_t>(table_rows)) {
-      bad = true;
-      use[c] = false;
+    for (int rr = 0; rr < R; ++rr) {
+      const int64_t row = r0 + rr;
+      bad[rr] = false;
+      i32x4 id4 = {0, 0, 0, 0};
+      f32x4 w4 = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (row < n_rows) {
+        id4 = *reinterpret_cast<const i32x4*>(index + 4 * row);
+        w4 = *reinterpret_cast<const f32x4*>(weight + 4 * row);
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        id[rr][c] = id4[c];
+        use[rr][c] = w4[c] != 0.0f;
+        if (use[rr][c] && static_cast<uint32_t>(id4[c]) >= static_cast<uint64_t>(table_rows)) {
+          bad[rr] = true;
+          use[rr][c] = false;
+        }
+        wq[rr][c] = weight_as_value<T>(w4[c]);
+      }
     }
-    wq[c] = weight_as_value<T>(wt[c]);
-  }
 
-  T* orow = out + row * out_stride;
-  for (int base = 0; base < dim; base += CH * 64 * VN) {
-    V y[4][CH];
+    for (int base = 0; base < dim; base += CH * 64 * VN) {
+      V y[R][4][CH];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      if (use[c]) {
-        const T* trow = table + static_cast<int64_t>(id[c]) * table_stride;
+      for (int rr = 0; rr < R; ++rr) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          if (use[rr][c]) {
+            const T* trow = table + static_cast<int64_t>(id[rr][c]) * table_stride;
+#pragma unroll
+            for (int ch = 0; ch < CH; ++ch) {
+              const int e = base + (ch * 64 + lane) * VN;
+              if (e < dim) y[rr][c][ch] = *reinterpret_cast<const V*>(trow + e);
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int rr = 0; rr < R; ++rr) {
+        const int64_t row = r0 + rr;
+        if (row >= n_rows) continue;
+        T* orow = out + row * out_stride;
 #pragma unroll
         for (int ch = 0; ch < CH; ++ch) {
           const int e = base + (ch * 64 + lane) * VN;
-          if (e < dim) y[c][ch] = *reinterpret_cast<const V*>(trow + e);
+          if (e >= dim) continue;
+          float acc[VN];
+#pragma unroll
+          for (int j = 0; j < VN; ++j) acc[j] = 0.0f;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            if (use[rr][c]) {
+#pragma unroll
+              for (int j = 0; j < VN; ++j)
+                acc[j] = acc[j] + rounded_product<T>(to_f32(y[rr][c][ch][j]), wq[rr][c]);
+            }
+          }
+          V o;
+#pragma unroll
+          for (int j = 0; j < VN; ++j) o[j] = from_f32<T>(bad[rr] ? __builtin_nanf("") : acc[j]);
+          __builtin_nontemporal_store(o, reinterpret_cast<V*>(orow + e));
         }
       }
-    }
-#pragma unroll
-    for (int ch = 0; ch < CH; ++ch) {
-      const int e = base + (ch * 64 + lane) * VN;
-      if (e >= dim) continue;
-      float acc[VN];
-#pragma unroll
-      for (int j = 0; j < VN; ++j) acc[j] = 0.0f;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        if (use[c]) {
-#pragma unroll
-          for (int j = 0; j < VN; ++j)
-            acc[j] = __fadd_rn(acc[j], rounded_product<T>(to_f32(y[c][ch][j]), wq[c]));
-        }
-      }
-      V o;
-#pragma unroll
-      for (int j = 0; j < VN; ++j) o[j] = from_f32<T>(bad ? __builtin_nanf("") : acc[j]);
-      __builtin_nontemporal_store(o, reinterpret_cast<V*>(orow + e));
     }
   }
 }
@@ -138,10 +161,34 @@ __global__ __launch_bounds__(256) void top4_project_scalar_kernel(
       bad = true;
       continue;
     }
-    acc = __fadd_rn(acc, rounded_product<T>(to_f32(table[id * table_stride + e]),
+    acc = acc + (rounded_product<T>(to_f32(table[id * table_stride + e]),
                                             weight_as_value<T>(w)));
   }
   out[row * out_stride + e] = from_f32<T>(bad ? __builtin_nanf("") : acc);
+}
+
+template <typename T, int R, int CH>
+void launch_vec(const T* tb, int64_t table_stride, const int32_t* index, const float* weight,
+                T* ob, int64_t out_stride, int64_t n_rows, int64_t table_rows, int dim,
+                int64_t blocks, hipStream_t stream) {
+  hipLaunchKernelGGL((top4_project_kernel<T, R, CH>), dim3(static_cast<unsigned>(blocks)),
+                     dim3(kWaves * 64), 0, stream, tb, table_stride, index, weight, ob, out_stride,
+                     n_rows, table_rows, dim);
+}
+
+// Work-groups resident per CU for the persistent launch (MI355X: 256 CUs).
+constexpr int64_t kProjectBlocksPerCu = 8;
+
+int device_cus() {
+  static thread_local int cached = 0;
+  if (cached > 0) return cached;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    cus = 256;
+  cached = cus;
+  return cached;
 }
 
 template <typename T>
@@ -154,24 +201,26 @@ int launch_project(const void* table, int64_t table_stride, const int32_t* index
   const bool vec_ok = (dim % VN == 0) && (table_stride % VN == 0) && (out_stride % VN == 0) &&
                       aligned(table, 16) && aligned(out, 16);
   if (vec_ok) {
-    const int64_t blocks = (n_rows + kWaves - 1) / kWaves;
-    VGO_REQUIRE(blocks <= 0x7fffffff, "top4_project: too many rows");
+    // 16-byte chunks per row per lane, and how many rows a wave gathers at once
+    // (about 32 chunks = 512 B in flight per lane).
     const int row_chunks = static_cast<int>((dim + 64 * VN - 1) / (64 * VN));
+    const int d = static_cast<int>(dim);
+    const int64_t cap = static_cast<int64_t>(device_cus()) * kProjectBlocksPerCu;
+    auto blocks_for = [&](int rows_per_wave) {
+      const int64_t need = (n_rows + kWaves * rows_per_wave - 1) / (kWaves * rows_per_wave);
+      return need < cap ? need : cap;
+    };
     if (row_chunks >= 4) {
-      hipLaunchKernelGGL((top4_project_kernel<T, 4>), dim3(blocks), dim3(kWaves * 64), 0, stream,
-                         tb, table_stride, index, weight, ob, out_stride, n_rows, table_rows,
-                         static_cast<int>(dim));
-    } else if (row_chunks == 2 || row_chunks == 3) {
-      hipLaunchKernelGGL((top4_project_kernel<T, 2>), dim3(blocks), dim3(kWaves * 64), 0, stream,
-                         tb, table_stride, index, weight, ob, out_stride, n_rows, table_rows,
-                         static_cast<int>(dim));
+      launch_vec<T, 2, 4>(tb, table_stride, index, weight, ob, out_stride, n_rows, table_rows, d,
+                          blocks_for(2), stream);
+    } else if (row_chunks >= 2) {
+      launch_vec<T, 4, 2>(tb, table_stride, index, weight, ob, out_stride, n_rows, table_rows, d,
+                          blocks_for(4), stream);
     } else {
-      hipLaunchKernelGGL((top4_project_kernel<T, 1>), dim3(blocks), dim3(kWaves * 64), 0, stream,
-                         tb, table_stride, index, weight, ob, out_stride, n_rows, table_rows,
-                         static_cast<int>(dim));
+      launch_vec<T, 8, 1>(tb, table_stride, index, weight, ob, out_stride, n_rows, table_rows, d,
+                          blocks_for(8), stream);
     }
   } else {
-    VGO_REQUIRE(n_rows <= 65535 * 1024LL, "top4_project: too many rows for the unaligned path");
     dim3 grid(static_cast<unsigned>((dim + 255) / 256), 1, 1);
     // Rows go on grid.y in slabs of 65535 (the y limit).
     for (int64_t r0 = 0; r0 < n_rows; r0 += 65535) {
@@ -197,7 +246,7 @@ extern "C" int vgo_top4_project(const void* table, int64_t table_row_stride, con
   if (n_rows == 0 || dim == 0) return VGO_OK;
   VGO_REQUIRE(index && weight && out, "top4_project: null pointer");
   VGO_REQUIRE(table || table_rows == 0, "top4_project: null table");
-  VGO_REQUIRE(dim <= 0x7fffffff, "top4_project: dim too large");
+  VGO_REQUIRE(dim <= 0x7fffffff && n_rows <= 0x7fffffff, "top4_project: size too large");
   VGO_REQUIRE(table_row_stride >= dim && out_row_stride >= dim, "top4_project: row stride < dim");
   VGO_REQUIRE(aligned(index, 16) && aligned(weight, 16),
               "top4_project: index/weight must be 16-byte aligned [n,4] arrays");

@@ -1,0 +1,411 @@
+// Deterministic segmented reductions of a merge plan: per-destination member
+// lists (CSR), mass / log-mass, Q/K/V compaction and the dense restore map.
+//
+// The reference groups plan members with one stable argsort + bincount per
+// corner (vggt_omega/models/token_merging.py:323-333, 40-59) so that every
+// reduction runs in a fixed source order; the default sparse-convex mass uses
+// atomic scatter_add_ (vggt_omega/models/sparse_convex.py:2448-2450), whose
+// float order is unspecified.  Here one stable LSD radix sort (8-bit digits,
+// wave-ballot ranking) orders all (destination, corner) pairs at once, and the
+// reductions walk those lists sequentially, reproducing the order of
+// `deterministic_weighted_normalizer` and of `WeightedBilinearTokenPlan.compact`:
+//   mass[k]    = ((1 + S_0) + S_1) + S_2) + S_3,    S_c = sum in source order of w
+//   compact[k] = ((x[keep_k] + T_0) + T_1 + T_2 + T_3) / mass[k],  T_c = sum of x*w
+// TokenPlan (FastVGGT) compaction is the one-segment case: the members of a
+// cluster in ascending token order, divided by their count
+// (token_merging.py:176-191).
+#include "vgo_common.h"
+
+namespace vgo {
+namespace {
+
+constexpr int kSortThreads = 256;
+constexpr int kSortRounds = 8;
+constexpr int kBlockItems = kSortThreads * kSortRounds;  // 2048 items per block
+constexpr int kSortWaves = kSortThreads / 64;
+
+__global__ __launch_bounds__(kSortThreads) void clamp_keys_kernel(const uint32_t* __restrict__ in,
+                                                                  uint32_t* __restrict__ keys,
+                                                                  uint32_t* __restrict__ vals,
+                                                                  int n, uint32_t limit) {
+  const int i = blockIdx.x * kSortThreads + threadIdx.x;
+  if (i >= n) return;
+  const uint32_t k = in[i];
+  keys[i] = k < limit ? k : limit;  // out-of-range keys sort past the last bucket
+  vals[i] = static_cast<uint32_t>(i);
+}
+
+__global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(const uint32_t* __restrict__ keys,
+                                                                  int n, int shift,
+                                                                  uint32_t* __restrict__ hist,
+                                                                  int nblocks) {
+  __shared__ uint32_t h[256];
+  const int tid = threadIdx.x;
+  h[tid] = 0;
+  __syncthreads();
+  const int base = blockIdx.x * kBlockItems;
+#pragma unroll
+  for (int r = 0; r < kSortRounds; ++r) {
+    const int i = base + r * kSortThreads + tid;
+    if (i < n) atomicAdd(&h[(keys[i] >> shift) & 0xFF], 1u);
+  }
+  __syncthreads();
+  hist[tid * nblocks + blockIdx.x] = h[tid];
+}
+
+// In-place exclusive scan of n values by one work-group (contiguous runs).
+__global__ __launch_bounds__(1024) void exclusive_scan_kernel(uint32_t* __restrict__ data, int n) {
+  __shared__ uint32_t waves[16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int per = (n + 1023) / 1024;
+  const int b = min(n, tid * per), e = min(n, b + per);
+  uint32_t sum = 0;
+  for (int i = b; i < e; ++i) sum += data[i];
+  uint32_t x = sum;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t y = __shfl_up(x, off);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) waves[wave] = x;
+  __syncthreads();
+  if (wave == 0) {
+    uint32_t w = lane < 16 ? waves[lane] : 0;
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) {
+      const uint32_t y = __shfl_up(w, off);
+      if (lane >= off) w += y;
+    }
+    if (lane < 16) waves[lane] = w;
+  }
+  __syncthreads();
+  uint32_t run = (wave > 0 ? waves[wave - 1] : 0) + x - sum;
+  for (int i = b; i < e; ++i) {
+    const uint32_t v = data[i];
+    data[i] = run;
+    run += v;
+  }
+}
+
+__global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
+    const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
+    uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out, int n, int shift,
+    const uint32_t* __restrict__ hist_scan, int nblocks) {
+  __shared__ uint32_t base[256];
+  __shared__ uint32_t running[256];
+  __shared__ uint32_t wcnt[kSortWaves][256];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  base[tid] = hist_scan[tid * nblocks + blockIdx.x];
+  running[tid] = 0;
+  const uint64_t lt_mask = (uint64_t(1) << lane) - 1;
+  for (int r = 0; r < kSortRounds; ++r) {
+#pragma unroll
+    for (int w = 0; w < kSortWaves; ++w) wcnt[w][tid] = 0;
+    __syncthreads();
+    const int i = blockIdx.x * kBlockItems + r * kSortThreads + tid;
+    const bool valid = i < n;
+    uint32_t key = 0, val = 0, d = 0;
+    if (valid) {
+      key = keys_in[i];
+      val = vals_in[i];
+      d = (key >> shift) & 0xFF;
+    }
+    uint64_t same = __ballot(valid);
+#pragma unroll
+    for (int bit = 0; bit < 8; ++bit) {
+      const uint64_t ones = __ballot(valid && ((d >> bit) & 1));
+      same &= ((d >> bit) & 1) ? ones : ~ones;
+    }
+    const uint32_t rank = __popcll(same & lt_mask);
+    if (valid && rank == 0) wcnt[wave][d] = __popcll(same);
+    __syncthreads();
+    if (valid) {
+      uint32_t pos = base[d] + running[d] + rank;
+      for (int w = 0; w < wave; ++w) pos += wcnt[w][d];
+      keys_out[pos] = key;
+      vals_out[pos] = val;
+    }
+    __syncthreads();
+    uint32_t add = 0;
+#pragma unroll
+    for (int w = 0; w < kSortWaves; ++w) add += wcnt[w][tid];
+    running[tid] += add;
+    __syncthreads();
+  }
+}
+
+// offsets[k] = first position of key k in the sorted keys; offsets[n_buckets] = n_valid.
+__global__ __launch_bounds__(256) void bucket_offsets_kernel(const uint32_t* __restrict__ skeys, int n,
+                                                             int n_buckets,
+                                                             int32_t* __restrict__ offsets) {
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (e >= n) return;
+  const int64_t k = min(static_cast<int64_t>(skeys[e]), static_cast<int64_t>(n_buckets));
+  const int64_t prev = e > 0 ? min(static_cast<int64_t>(skeys[e - 1]), static_cast<int64_t>(n_buckets)) : -1;
+  for (int64_t kk = prev + 1; kk <= k; ++kk) offsets[kk] = e;
+  if (e == n - 1)
+    for (int64_t kk = k + 1; kk <= n_buckets; ++kk) offsets[kk] = n;
+}
+
+__global__ __launch_bounds__(256) void fill_i32_kernel(int32_t* __restrict__ p, int n, int32_t v) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+int key_bits(int64_t limit) {
+  int bits = 1;
+  while ((int64_t(1) << bits) <= limit) ++bits;
+  return bits;
+}
+
+size_t align_up(size_t x) { return (x + 255) & ~size_t(255); }
+
+// ------------------------------------------------------------- mass ----
+__global__ __launch_bounds__(256) void segment_mass_kernel(
+    const int32_t* __restrict__ offsets, int segs_per_row, const uint32_t* __restrict__ items,
+    const float* __restrict__ weights, int n_weights, int rows, float start,
+    float* __restrict__ mass, float* __restrict__ log_mass) {
+  const int k = blockIdx.x * 256 + threadIdx.x;
+  if (k >= rows) return;
+  float m = start;
+  for (int c = 0; c < segs_per_row; ++c) {
+    const int b = offsets[k * segs_per_row + c], e = offsets[k * segs_per_row + c + 1];
+    float s = 0.0f;
+    for (int q = b; q < e; ++q) {
+      const uint32_t p = items[q];
+      s = s + (weights ? (static_cast<int>(p) < n_weights ? weights[p] : 0.0f) : 1.0f);
+    }
+    m = m + s;
+  }
+  mass[k] = m;
+  if (log_mass) log_mass[k] = logf(m);
+}
+
+// ------------------------------------------------------ compaction ----
+// out[k] = (base + sum_c sum_{p in seg(k,c)} x[row(p)] * w[p]) / norm[k], in fp32,
+// cast to the value type.  Channel c of token t lives at t*ts + (c/64)*hs + c%64
+// (hs = 64 for a row-contiguous tensor; a [B,H,N,64] tensor viewed per token
+// has ts = 64, hs = N*64), so head-major attention operands are read and written
+// without a transpose copy.
+template <typename T, int U>
+__global__ __launch_bounds__(256) void compact_kernel(
+    const T* __restrict__ x, int64_t xts, int64_t xhs, int64_t x_rows,
+    const int64_t* __restrict__ base_rows, const int32_t* __restrict__ offsets, int segs_per_row,
+    const uint32_t* __restrict__ items, int item_shift, const int64_t* __restrict__ item_rows,
+    const float* __restrict__ weights, int n_weights, const float* __restrict__ norm, int rows,
+    int dim, T* __restrict__ out, int64_t ots, int64_t ohs) {
+  const int lane = threadIdx.x & 63;
+  const int k = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (k >= rows) return;
+  for (int c0 = 0; c0 < dim; c0 += 64 * U) {
+    float acc[U];
+    const int64_t b = base_rows ? base_rows[k] : -1;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + u * 64 + lane;
+      acc[u] = (b >= 0 && b < x_rows && c < dim)
+                   ? to_f32(x[b * xts + (c >> 6) * xhs + (c & 63)])
+                   : 0.0f;
+    }
+    for (int sgi = 0; sgi < segs_per_row; ++sgi) {
+      const int sb = offsets[k * segs_per_row + sgi], se = offsets[k * segs_per_row + sgi + 1];
+      if (sb >= se) continue;
+      float seg[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) seg[u] = 0.0f;
+      for (int q = sb; q < se; ++q) {
+        const uint32_t p = items[q];
+        const int64_t i = static_cast<int64_t>(p >> item_shift);
+        const int64_t row = item_rows ? item_rows[i] : i;
+        const float w = weights ? (static_cast<int>(p) < n_weights ? weights[p] : 0.0f) : 1.0f;
+        if (row < 0 || row >= x_rows) continue;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int c = c0 + u * 64 + lane;
+          if (c < dim) seg[u] = seg[u] + to_f32(x[row * xts + (c >> 6) * xhs + (c & 63)]) * w;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc[u] = acc[u] + seg[u];
+    }
+    const float nk = norm ? norm[k] : 1.0f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + u * 64 + lane;
+      if (c < dim) out[static_cast<int64_t>(k) * ots + (c >> 6) * ohs + (c & 63)] = from_f32<T>(acc[u] / nk);
+    }
+  }
+}
+
+// ---------------------------------------------------- restore map ----
+// Dense [N,4] (index, weight) rows for the top-4 projection:
+//   kept token keep[k]              -> (k,k,k,k), (1,0,0,0)
+//   source token source[i]          -> parent[i,:], w[i,:]
+//   token with inverse[t] = k (TokenPlan)     -> (k,k,k,k), (1,0,0,0)
+__global__ __launch_bounds__(256) void restore_map_kernel(
+    const int64_t* __restrict__ keep, int n_keep, const int64_t* __restrict__ source,
+    const int64_t* __restrict__ parent, const float* __restrict__ w, int n_source,
+    const int64_t* __restrict__ inverse, int total, int32_t* __restrict__ index,
+    float* __restrict__ weight) {
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (inverse) {
+    if (e >= total) return;
+    const int64_t k = inverse[e];
+    const int32_t kk = static_cast<int32_t>(k);
+    index[4 * e + 0] = kk;
+    index[4 * e + 1] = kk;
+    index[4 * e + 2] = kk;
+    index[4 * e + 3] = kk;
+    weight[4 * e + 0] = k >= 0 ? 1.0f : 0.0f;
+    weight[4 * e + 1] = 0.0f;
+    weight[4 * e + 2] = 0.0f;
+    weight[4 * e + 3] = 0.0f;
+    return;
+  }
+  if (e < n_keep) {
+    const int64_t t = keep[e];
+    if (t < 0 || t >= total) return;
+    for (int c = 0; c < 4; ++c) {
+      index[4 * t + c] = e;
+      weight[4 * t + c] = c == 0 ? 1.0f : 0.0f;
+    }
+  } else if (e < n_keep + n_source) {
+    const int i = e - n_keep;
+    const int64_t t = source[i];
+    if (t < 0 || t >= total) return;
+    for (int c = 0; c < 4; ++c) {
+      index[4 * t + c] = static_cast<int32_t>(parent[4 * i + c]);
+      weight[4 * t + c] = w[4 * i + c];
+    }
+  }
+}
+
+}  // namespace
+}  // namespace vgo
+
+using namespace vgo;
+
+extern "C" int vgo_csr_workspace(int64_t n_items, int64_t n_buckets, size_t* bytes) {
+  VGO_REQUIRE(n_items >= 0 && n_buckets >= 1, "csr_build: bad size");
+  VGO_REQUIRE(n_items < (1LL << 31) && n_buckets < (1LL << 31) - 1, "csr_build: size too large");
+  const int64_t nblocks = (n_items + kBlockItems - 1) / kBlockItems;
+  size_t b = 0;
+  b += 3 * align_up(static_cast<size_t>(n_items) * 4);  // keys x2, vals ping
+  b += align_up(static_cast<size_t>(256) * (nblocks > 0 ? nblocks : 1) * 4);
+  *bytes = b;
+  return VGO_OK;
+}
+
+extern "C" int vgo_csr_build(const uint32_t* keys, int64_t n_items, int64_t n_buckets,
+                             void* workspace, size_t workspace_bytes, uint32_t* order,
+                             int32_t* offsets, void* stream) {
+  size_t need = 0;
+  int st = vgo_csr_workspace(n_items, n_buckets, &need);
+  if (st != VGO_OK) return st;
+  VGO_REQUIRE(offsets, "csr_build: null offsets");
+  hipStream_t s = as_stream(stream);
+  const int n = static_cast<int>(n_items);
+  const int nb = static_cast<int>(n_buckets);
+  if (n == 0) {
+    hipLaunchKernelGGL(fill_i32_kernel, dim3((nb + 1 + 255) / 256), dim3(256), 0, s, offsets, nb + 1, 0);
+    return check_launch("csr_build");
+  }
+  VGO_REQUIRE(keys && order && workspace, "csr_build: null pointer");
+  VGO_REQUIRE(workspace_bytes >= need && aligned(workspace, 256), "csr_build: workspace too small or misaligned");
+  char* ws = static_cast<char*>(workspace);
+  uint32_t* ka = reinterpret_cast<uint32_t*>(ws);
+  uint32_t* kb = reinterpret_cast<uint32_t*>(ws + align_up(size_t(n) * 4));
+  uint32_t* va = reinterpret_cast<uint32_t*>(ws + 2 * align_up(size_t(n) * 4));
+  uint32_t* hist = reinterpret_cast<uint32_t*>(ws + 3 * align_up(size_t(n) * 4));
+  const int nblocks = (n + kBlockItems - 1) / kBlockItems;
+  const int passes = (key_bits(n_buckets) + 7) / 8;
+  // Value buffers ping-pong between va and `order` so the last pass lands in `order`.
+  uint32_t* vbuf[2] = {va, order};
+  uint32_t* kbuf[2] = {ka, kb};
+  int cur = passes % 2 == 0 ? 1 : 0;  // buffer index holding the input of pass 0
+  // vals start in vbuf[cur]; after `passes` flips they end in vbuf[(cur + passes) % 2] == order.
+  hipLaunchKernelGGL(clamp_keys_kernel, dim3((n + kSortThreads - 1) / kSortThreads), dim3(kSortThreads), 0,
+                     s, keys, kbuf[cur], vbuf[cur], n, static_cast<uint32_t>(nb));
+  for (int p = 0; p < passes; ++p) {
+    const int shift = 8 * p;
+    hipLaunchKernelGGL(radix_hist_kernel, dim3(nblocks), dim3(kSortThreads), 0, s, kbuf[cur], n,
+                       shift, hist, nblocks);
+    hipLaunchKernelGGL(exclusive_scan_kernel, dim3(1), dim3(1024), 0, s, hist, 256 * nblocks);
+    hipLaunchKernelGGL(radix_scatter_kernel, dim3(nblocks), dim3(kSortThreads), 0, s, kbuf[cur],
+                       vbuf[cur], kbuf[1 - cur], vbuf[1 - cur], n, shift, hist, nblocks);
+    cur = 1 - cur;
+  }
+  hipLaunchKernelGGL(bucket_offsets_kernel, dim3((n + 255) / 256), dim3(256), 0, s, kbuf[cur], n,
+                     nb, offsets);
+  return check_launch("csr_build");
+}
+
+extern "C" int vgo_segment_mass(const int32_t* offsets, int64_t segs_per_row, const uint32_t* items,
+                                const float* weights, int64_t n_weights, int64_t rows, float start,
+                                float* mass, float* log_mass, void* stream) {
+  VGO_REQUIRE(rows >= 0 && segs_per_row >= 1, "segment_mass: bad size");
+  if (rows == 0) return VGO_OK;
+  VGO_REQUIRE(offsets && items && mass, "segment_mass: null pointer");
+  hipLaunchKernelGGL(segment_mass_kernel, dim3(static_cast<unsigned>((rows + 255) / 256)), dim3(256), 0,
+                     as_stream(stream), offsets, static_cast<int>(segs_per_row), items, weights,
+                     static_cast<int>(n_weights), static_cast<int>(rows), start, mass, log_mass);
+  return check_launch("segment_mass");
+}
+
+extern "C" int vgo_compact(const void* x, int64_t x_token_stride, int64_t x_head_stride, int64_t x_rows,
+                           const int64_t* base_rows, const int32_t* offsets, int64_t segs_per_row,
+                           const uint32_t* items, int item_shift, const int64_t* item_rows,
+                           const float* weights, int64_t n_weights, const float* normalizer,
+                           int64_t rows, int64_t dim, void* out, int64_t out_token_stride,
+                           int64_t out_head_stride, int dtype, void* stream) {
+  VGO_REQUIRE(rows >= 0 && dim >= 0 && segs_per_row >= 1, "compact: bad size");
+  if (rows == 0 || dim == 0) return VGO_OK;
+  VGO_REQUIRE(x && offsets && out, "compact: null pointer");
+  VGO_REQUIRE(item_shift >= 0 && item_shift < 8, "compact: bad item shift");
+  VGO_REQUIRE(rows < (1LL << 31) && dim < (1 << 20), "compact: size too large");
+  hipStream_t s = as_stream(stream);
+  const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
+  const int r = static_cast<int>(rows), d = static_cast<int>(dim), sp = static_cast<int>(segs_per_row);
+  const int nw = static_cast<int>(n_weights);
+  switch (dtype) {
+    case VGO_F32:
+      hipLaunchKernelGGL((compact_kernel<float, 16>), grid, dim3(256), 0, s, static_cast<const float*>(x),
+                         x_token_stride, x_head_stride, x_rows, base_rows, offsets, sp, items, item_shift,
+                         item_rows, weights, nw, normalizer, r, d, static_cast<float*>(out),
+                         out_token_stride, out_head_stride);
+      break;
+    case VGO_BF16:
+      hipLaunchKernelGGL((compact_kernel<bf16_t, 16>), grid, dim3(256), 0, s,
+                         static_cast<const bf16_t*>(x), x_token_stride, x_head_stride, x_rows, base_rows,
+                         offsets, sp, items, item_shift, item_rows, weights, nw, normalizer, r, d,
+                         static_cast<bf16_t*>(out), out_token_stride, out_head_stride);
+      break;
+    case VGO_F16:
+      hipLaunchKernelGGL((compact_kernel<f16_t, 16>), grid, dim3(256), 0, s, static_cast<const f16_t*>(x),
+                         x_token_stride, x_head_stride, x_rows, base_rows, offsets, sp, items, item_shift,
+                         item_rows, weights, nw, normalizer, r, d, static_cast<f16_t*>(out),
+                         out_token_stride, out_head_stride);
+      break;
+    default:
+      return fail(VGO_EINVAL, "compact: unknown dtype");
+  }
+  return check_launch("compact");
+}
+
+extern "C" int vgo_restore_map(const int64_t* keep, int64_t n_keep, const int64_t* source,
+                               const int64_t* parent, const float* weight, int64_t n_source,
+                               const int64_t* inverse, int64_t total, int32_t* index_out,
+                               float* weight_out, void* stream) {
+  VGO_REQUIRE(total >= 0 && n_keep >= 0 && n_source >= 0, "restore_map: bad size");
+  VGO_REQUIRE(total < (1LL << 31), "restore_map: size too large");
+  if (total == 0) return VGO_OK;
+  VGO_REQUIRE(index_out && weight_out, "restore_map: null pointer");
+  hipStream_t s = as_stream(stream);
+  const int64_t work = inverse ? total : n_keep + n_source;
+  if (!inverse) VGO_REQUIRE(keep && (n_source == 0 || (source && parent && weight)), "restore_map: null pointer");
+  if (work == 0) return VGO_OK;
+  hipLaunchKernelGGL(restore_map_kernel, dim3(static_cast<unsigned>((work + 255) / 256)), dim3(256), 0, s,
+                     keep, static_cast<int>(n_keep), source, parent, weight, static_cast<int>(n_source),
+                     inverse, static_cast<int>(total), index_out, weight_out);
+  return check_launch("restore_map");
+}

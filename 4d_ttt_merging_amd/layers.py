@@ -1,0 +1,289 @@
+"""Transformer layers of the merged global-attention path.
+
+`SelfAttention` and `SelfAttentionBlock` keep the parameter names, constructor
+arguments and forward signatures of vggt_omega/models/layers/attention.py:195-439
+and vggt_omega/models/layers/block.py:22-226, so reference state dicts load
+unchanged.  With a token plan, `SelfAttention` runs the merged path on the HIP
+library:
+
+  qkv = Linear(x)                         (torch GEMM, hipBLASLt)
+  q, k = LayerNorm64(q), LayerNorm64(k)   (torch)
+  Q/K/V compaction through the plan       vgo_compact, straight between
+                                          head-major [H, N, 64] views
+  mass-bias attention                     vgo_mass_bias_attn_fwd, written
+                                          directly in [B, N, H, 64] order
+  dense special queries                   vgo_mass_bias_attn_fwd without bias
+  out = Linear(x)                         (torch GEMM)
+  restore                                 vgo_top4_project
+
+Frame blocks (RoPE, no plan) use torch's SDPA exactly as the reference does.
+The reference's experimental hooks that import the absent module
+`sampled_update_operator` (attention.py:267-299) and the source-query
+correction branch (attention.py:304-312, 376-385) are not part of this path
+and raise NotImplementedError if a caller enables them.
+"""
+from __future__ import annotations
+
+import math
+from typing import Callable
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor, nn
+
+from .mass_bias_attention import _attention_into
+
+
+def rope_rotate_half(x: Tensor) -> Tensor:
+    x1, x2 = x.chunk(2, dim=-1)
+    return torch.cat([-x2, x1], dim=-1)
+
+
+def rope_apply(x: Tensor, sin: Tensor, cos: Tensor) -> Tensor:
+    return (x * cos) + (rope_rotate_half(x) * sin)
+
+
+class LinearKMaskedBias(nn.Linear):
+    """qkv projection whose K third of the bias is masked to zero (attention.py:195-207)."""
+
+    def __init__(self, *args, **kwargs):
+        super().__init__(*args, **kwargs)
+        o = self.out_features
+        assert o % 3 == 0
+        if self.bias is not None:
+            bias_mask = torch.ones_like(self.bias)
+            bias_mask[o // 3: 2 * o // 3].fill_(0)
+            self.register_buffer("bias_mask", bias_mask)
+
+    def forward(self, input: Tensor) -> Tensor:
+        masked_bias = self.bias * self.bias_mask.to(self.bias.dtype) if self.bias is not None else None
+        return F.linear(input, self.weight, masked_bias)
+
+
+class LayerScale(nn.Module):
+    def __init__(self, dim: int, init_values: float | Tensor = 1e-5, inplace: bool = False,
+                 device=None) -> None:
+        super().__init__()
+        self.inplace = inplace
+        self.gamma = nn.Parameter(torch.empty(dim, device=device))
+        self.init_values = init_values
+        self.reset_parameters()
+
+    def reset_parameters(self):
+        nn.init.constant_(self.gamma, self.init_values)
+
+    def forward(self, x: Tensor) -> Tensor:
+        return x.mul_(self.gamma) if self.inplace else x * self.gamma
+
+
+class Mlp(nn.Module):
+    def __init__(self, in_features: int, hidden_features: int | None = None,
+                 out_features: int | None = None, act_layer: Callable[..., nn.Module] = nn.GELU,
+                 drop: float = 0.0, bias: bool = True, device=None) -> None:
+        super().__init__()
+        out_features = out_features or in_features
+        hidden_features = hidden_features or in_features
+        self.fc1 = nn.Linear(in_features, hidden_features, bias=bias, device=device)
+        self.act = act_layer()
+        self.fc2 = nn.Linear(hidden_features, out_features, bias=bias, device=device)
+        self.drop = nn.Dropout(drop)
+
+    def forward(self, x: Tensor) -> Tensor:
+        return self.drop(self.fc2(self.drop(self.act(self.fc1(x)))))
+
+
+class SelfAttention(nn.Module):
+    def __init__(self, dim: int, num_heads: int = 8, qkv_bias: bool = False,
+                 proj_bias: bool = True, attn_drop: float = 0.0, proj_drop: float = 0.0,
+                 mask_k_bias: bool = False, use_qk_norm: bool = False, device=None) -> None:
+        super().__init__()
+        self.num_heads = num_heads
+        head_dim = dim // num_heads
+        self.scale = head_dim ** -0.5
+        self.use_qk_norm = use_qk_norm
+        if use_qk_norm:
+            self.q_norm = nn.LayerNorm(head_dim, eps=1e-5)
+            self.k_norm = nn.LayerNorm(head_dim, eps=1e-5)
+        else:
+            self.q_norm = None
+            self.k_norm = None
+        linear_class = LinearKMaskedBias if mask_k_bias else nn.Linear
+        self.qkv = linear_class(dim, dim * 3, bias=qkv_bias, device=device)
+        self.attn_drop = nn.Dropout(attn_drop)
+        self.proj = nn.Linear(dim, dim, bias=proj_bias, device=device)
+        self.proj_drop = nn.Dropout(proj_drop)
+
+    def apply_rope(self, q: Tensor, k: Tensor, rope) -> tuple[Tensor, Tensor]:
+        q_dtype, k_dtype = q.dtype, k.dtype
+        sin, cos = rope
+        q, k = q.to(sin.dtype), k.to(sin.dtype)
+        prefix = q.shape[-2] - sin.shape[-2]
+        assert prefix >= 0
+        q = torch.cat((q[:, :, :prefix], rope_apply(q[:, :, prefix:], sin, cos)), dim=-2)
+        k = torch.cat((k[:, :, :prefix], rope_apply(k[:, :, prefix:], sin, cos)), dim=-2)
+        return q.to(q_dtype), k.to(k_dtype)
+
+    def _check_hooks(self) -> None:
+        for name in ("fixed_update_operator_config", "sampled_update_operator_config",
+                     "dense_update_diagnostic_config", "baseline_trajectory_probe_config"):
+            if getattr(self, name, None) is not None:
+                raise NotImplementedError(f"{name} is outside the merged global-attention path")
+
+    def forward(self, x: Tensor, attn_bias=None, rope: Tensor = None, token_plan=None) -> Tensor:
+        if token_plan is not None and self.training:
+            raise RuntimeError("token compaction is inference-only")
+        self._check_hooks()
+        qkv = (token_plan.precomputed_qkv
+               if token_plan is not None and getattr(token_plan, "precomputed_qkv", None) is not None
+               else self.qkv(x))
+        attn_v = self.compute_attention(qkv=qkv, attn_bias=attn_bias, rope=rope, token_plan=token_plan)
+        x = self.proj_drop(self.proj(attn_v))
+        if token_plan is None:
+            return x
+        if (getattr(token_plan, "source_query_correction", False)
+                and not getattr(token_plan, "preserve_queries", False)):
+            raise NotImplementedError("source-query correction is outside the merged path")
+        return token_plan.restore(x)
+
+    def compute_attention(self, qkv: Tensor, attn_bias=None, rope=None, token_plan=None) -> Tensor:
+        assert attn_bias is None
+        B, N, _ = qkv.shape
+        C = self.qkv.in_features
+        H = self.num_heads
+        D = C // H
+        q, k, v = torch.unbind(qkv.reshape(B, N, 3, H, D), 2)
+        q, k, v = [t.transpose(1, 2) for t in (q, k, v)]
+        if self.use_qk_norm:
+            q = self.q_norm(q)
+            k = self.k_norm(k)
+        if rope is not None:
+            q, k = self.apply_rope(q, k, rope)
+        if token_plan is None:
+            x = F.scaled_dot_product_attention(q, k, v)
+            return x.transpose(1, 2).reshape(B, N, C)
+        return self._merged_attention(q, k, v, token_plan, B, N, C, H, D)
+
+    def _merged_attention(self, q, k, v, plan, B, N, C, H, D) -> Tensor:
+        if D != 64:
+            raise ValueError("the initial fused kernel supports head_dim=64 only")
+        preserve_queries = getattr(plan, "preserve_queries", False)
+        kept = plan.kept_tokens
+        n_query = N if preserve_queries else getattr(plan, "query_kept_tokens", kept)
+
+        def head_major(rows: int, dtype: torch.dtype) -> Tensor:
+            return torch.empty((B, H, rows, D), device=q.device, dtype=dtype)
+
+        # Compaction between head-major views: no transpose copies.
+        k_c = head_major(kept, k.dtype)
+        v_c = head_major(kept, v.dtype)
+        q_c = q if preserve_queries else head_major(n_query, q.dtype)
+        for b in range(B):
+            if preserve_queries:
+                if hasattr(plan, "compact_key_into"):
+                    plan.compact_key_into(k[b], k_c[b])
+                else:
+                    plan.compact_into(k[b], k_c[b], b=b, merge=plan.pool_sources)
+            else:
+                if hasattr(plan, "compact_query_into"):
+                    plan.compact_query_into(q[b], q_c[b])
+                    plan.compact_into(k[b], k_c[b])
+                else:
+                    plan.compact_into(q[b], q_c[b], b=b, merge=plan.pool_sources)
+                    plan.compact_into(k[b], k_c[b], b=b, merge=plan.pool_sources)
+            if hasattr(plan, "compact_query_into"):
+                plan.compact_into(v[b], v_c[b])
+            else:
+                plan.compact_into(v[b], v_c[b], b=b, merge=plan.pool_sources)
+
+        # Attention in the autocast dtype (reference mass_bias_attention.py:96-107).
+        dtype = q.dtype
+        if (torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16
+                and q.dtype == torch.float32):
+            dtype = torch.bfloat16
+        qa, ka, va = q_c.to(dtype), k_c.to(dtype), v_c.to(dtype)
+        bias = None
+        log_mass = getattr(plan, "key_log_mass", None)
+        if log_mass is not None:
+            bias = log_mass.reshape(-1).to(dtype)
+            if bias.numel() != kept:
+                raise ValueError("log_key_mass length does not match key tokens")
+        out = torch.empty((B, n_query, H, D), device=q.device, dtype=dtype)
+        x = out.permute(0, 2, 1, 3)  # [B, H, Nq, D] view written in [B, Nq, H, D] order
+        _attention_into(qa, ka, va, bias, x)
+
+        if getattr(plan, "dense_special_queries", False):
+            original = plan.special_query_original
+            output_indices = original if preserve_queries else plan.special_query_compact
+            if original is None or output_indices is None:
+                raise RuntimeError("dense-special attention plan has no special-token mapping")
+            special_q = q.index_select(2, original).to(dtype)
+            exact = torch.empty((B, H, original.numel(), D), device=q.device, dtype=dtype)
+            _attention_into(special_q, k.to(dtype), v.to(dtype), None, exact)
+            x.index_copy_(2, output_indices, exact)
+        return out.view(B, n_query, C)
+
+
+class SelfAttentionBlock(nn.Module):
+    def __init__(self, dim: int, num_heads: int, ffn_ratio: float = 4.0, qkv_bias: bool = False,
+                 proj_bias: bool = True, ffn_bias: bool = True, drop: float = 0.0,
+                 attn_drop: float = 0.0, init_values=None, drop_path: float = 0.0,
+                 act_layer: Callable[..., nn.Module] = nn.GELU,
+                 norm_layer: Callable[..., nn.Module] = nn.LayerNorm,
+                 attn_class: Callable[..., nn.Module] = SelfAttention,
+                 ffn_layer: Callable[..., nn.Module] = Mlp, mask_k_bias: bool = False,
+                 use_qk_norm: bool = False, device=None) -> None:
+        super().__init__()
+        self.norm1 = norm_layer(dim)
+        self.attn = attn_class(dim, num_heads=num_heads, qkv_bias=qkv_bias, proj_bias=proj_bias,
+                               attn_drop=attn_drop, proj_drop=drop, mask_k_bias=mask_k_bias,
+                               use_qk_norm=use_qk_norm, device=device)
+        self.ls1 = LayerScale(dim, init_values=init_values, device=device) if init_values else nn.Identity()
+        self.norm2 = norm_layer(dim)
+        self.mlp = ffn_layer(in_features=dim, hidden_features=int(dim * ffn_ratio),
+                             act_layer=act_layer, drop=drop, bias=ffn_bias, device=device)
+        self.ls2 = LayerScale(dim, init_values=init_values, device=device) if init_values else nn.Identity()
+        self.sample_drop_ratio = drop_path
+
+    def forward(self, x: Tensor, rope=None) -> Tensor:
+        """Inference forward of block.py:89-129 (no stochastic depth)."""
+        x_attn = x + self.ls1(self.attn(self.norm1(x), rope=rope))
+        return x_attn + self.ls2(self.mlp(self.norm2(x_attn)))
+
+    def forward_compacted(self, x: Tensor, token_plan, *, normalized: Tensor = None) -> Tensor:
+        """Inference-only compact-Q/K/V attention block (block.py:219-226)."""
+        if self.training:
+            raise RuntimeError("token compaction is inference-only")
+        if normalized is None:
+            normalized = self.norm1(x)
+        x_attn = x + self.ls1(self.attn(normalized, token_plan=token_plan))
+        return x_attn + self.ls2(self.mlp(self.norm2(x_attn)))
+
+
+def init_weights_vit(module: nn.Module, name: str = "") -> None:
+    """Random init of vggt_omega/models/layers/vision_transformer.py:47-63."""
+    if isinstance(module, nn.Linear):
+        torch.nn.init.trunc_normal_(module.weight, std=0.02)
+        if module.bias is not None:
+            nn.init.zeros_(module.bias)
+        if getattr(module, "bias_mask", None) is not None:
+            o = module.out_features
+            module.bias_mask.fill_(1)
+            module.bias_mask[o // 3: 2 * o // 3].fill_(0)
+    if isinstance(module, (nn.LayerNorm, LayerScale)):
+        module.reset_parameters()
+
+
+def rope_sincos(H: int, W: int, head_dim: int, base: float = 100.0,
+                device=None) -> tuple[Tensor, Tensor]:
+    """Axial RoPE tables of RopePositionEmbedding(normalize_coords="max") at inference
+    (vggt_omega/models/layers/rope_position_encoding.py:51-127), fp32 [H*W, head_dim]."""
+    dd = dict(device=device, dtype=torch.float32)
+    periods = base ** (2 * torch.arange(head_dim // 4, **dd) / (head_dim // 2))
+    m = max(H, W)
+    coords_h = torch.arange(0.5, H, **dd) / m
+    coords_w = torch.arange(0.5, W, **dd) / m
+    coords = torch.stack(torch.meshgrid(coords_h, coords_w, indexing="ij"), dim=-1).flatten(0, 1)
+    coords = 2.0 * coords - 1.0
+    angles = 2 * math.pi * coords[:, :, None] / periods[None, None, :]
+    angles = angles.flatten(1, 2).tile(2)
+    return torch.sin(angles), torch.cos(angles)

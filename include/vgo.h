@@ -79,6 +79,147 @@ int vgo_top4_project(const void* table, int64_t table_row_stride, const int32_t*
                      const float* weight, void* out, int64_t out_row_stride, int64_t n_rows,
                      int64_t table_rows, int64_t dim, int dtype, void* stream);
 
+
+/*
+ * Row gather + L2 normalisation: out[r] = x[rows[r]] / max(||x[rows[r]]||, eps),
+ * fp32 accumulation, one rounding to out_dtype.  rows == NULL means rows[r] = r;
+ * a row id outside [0, x_rows) yields a NaN row.  Replaces the
+ * `F.normalize(...).to(bfloat16)` front end of the matchers
+ * (vggt_omega/models/token_merging.py:1102-1103; sparse_convex.py:2384, 2403).
+ */
+int vgo_normalize_rows(const void* x, int64_t x_row_stride, int64_t x_rows, int x_dtype,
+                       const int64_t* rows, int64_t n_rows, int64_t dim, float eps, void* out,
+                       int64_t out_row_stride, int out_dtype, void* stream);
+
+/*
+ * Cosine matching with a per-source top-K (K = 1 or 4) over bf16 operands:
+ * score[i,j] = bf16(src[i] . dict[j]) (fp32 accumulation), ties to the lower j.
+ * Replaces the FastVGGT match loop `bmm(...).max(-1)`
+ * (vggt_omega/models/token_merging.py:1106-1111), the sparse-convex local and
+ * global `(...).topk(4)` (vggt_omega/models/sparse_convex.py:2402-2404, 2430) and
+ * the Triton `streaming_top4` (vggt_omega/models/sparse_convex_kernels.py:20-93,
+ * 309-329).
+ *   src: bf16 rows, source i reads row src_rows ? src_rows[i] : i (< src_capacity);
+ *        n_src_device (nullable) caps the source count on the device.
+ *   dict: bf16 rows; dictionary position j < dict_n0 reads row j, else row
+ *        dict_off1 + (j - dict_n0) (two contiguous ranges, e.g. frame-0 patches
+ *        plus a window of anchors).
+ *   values [n_src, K] fp32 (bf16-exact), index64/index32 [n_src, K] (either may
+ *        be NULL): the dictionary row of each match, mapped through
+ *        index_map[row] when index_map != NULL.  Ties break on the position j.
+ *   scores (nullable): also store the bf16 score matrix (test/debug use).
+ * Workspace size: vgo_similarity_topk_workspace.
+ */
+int vgo_similarity_topk_workspace(int64_t n_src, int64_t n_dict, int topk, int* parts,
+                                  size_t* bytes);
+int vgo_similarity_topk(const void* src, int64_t src_row_stride, int64_t src_capacity,
+                        const int64_t* src_rows, const int* n_src_device, int64_t n_src,
+                        const void* dict, int64_t dict_row_stride, int64_t dict_capacity,
+                        int64_t dict_n0, int64_t dict_off1, int64_t n_dict, int64_t dim, int topk,
+                        void* workspace, size_t workspace_bytes, float* values, int64_t* index64,
+                        int32_t* index32, const int64_t* index_map, void* scores,
+                        int64_t scores_row_stride, void* stream);
+
+/*
+ * FastVGGT plan assembly from match scores: removes the `removed` sources with
+ * the largest (best, -position) -- the set `argsort(best, descending=True,
+ * stable=True)[:removed]` selects -- and builds keep [batch, total-removed]
+ * (ascending ids) and inverse [batch, total] (compact id; removed sources get
+ * their target's).  Replaces vggt_omega/models/token_merging.py:1112-1121.
+ * removed_flag [batch, n_sources] receives 1 for removed sources.
+ */
+int vgo_fastvggt_assemble(const float* best, const int32_t* target, const int64_t* source_ids,
+                          const int64_t* dest_ids, int64_t batch, int64_t n_sources,
+                          int64_t n_dest, int64_t total_tokens, int64_t removed, int64_t* keep,
+                          int64_t* inverse, uint8_t* removed_flag, void* stream);
+
+/*
+ * Sparse-convex plan assembly (vggt_omega/models/sparse_convex.py:2435-2455):
+ * sources = candidates with fit >= threshold (ascending), keep = the rest,
+ * original_to_compact, parent = original_to_compact[support], weight = alpha.
+ * Outputs are sized for the worst case (n_candidates sources / total_tokens
+ * kept); stats[4] = {sources M, hard candidates, fallback candidates, sum of
+ * selected fits} lets the caller size the plan with one small device->host copy.
+ */
+int vgo_sparse_convex_assemble(const float* fit, const float* alpha, const int64_t* support,
+                               const int64_t* candidate, const float* top1, float easy_threshold,
+                               const int* failed_count, int64_t n_candidates,
+                               int64_t total_tokens, float threshold, int64_t* keep,
+                               int64_t* original_to_compact, int64_t* source, int64_t* parent,
+                               float* weight, float* stats, void* stream);
+
+/*
+ * Stable bucket order (CSR): order = item ids sorted by key, equal keys in item
+ * order; offsets[k] .. offsets[k+1] delimit bucket k; keys >= n_buckets are
+ * dropped.  Replaces the per-corner `argsort(stable=True)` + `bincount` of
+ * vggt_omega/models/token_merging.py:323-333 and :51-54.
+ */
+int vgo_csr_workspace(int64_t n_items, int64_t n_buckets, size_t* bytes);
+int vgo_csr_build(const uint32_t* keys, int64_t n_items, int64_t n_buckets, void* workspace,
+                  size_t workspace_bytes, uint32_t* order, int32_t* offsets, void* stream);
+
+/*
+ * Per-row mass: mass[k] = (((start + S_0) + S_1) + ...), S_c = sequential sum of
+ * weights[p] over the items p of segment (k, c) in CSR order (weights == NULL
+ * counts items); log_mass (nullable) = log(mass).  With start = 1 and one
+ * segment per corner this is `deterministic_weighted_normalizer`
+ * (vggt_omega/models/token_merging.py:40-59) and the sparse-convex mass
+ * (vggt_omega/models/sparse_convex.py:2448-2450, 2468).
+ */
+int vgo_segment_mass(const int32_t* offsets, int64_t segs_per_row, const uint32_t* items,
+                     const float* weights, int64_t n_weights, int64_t rows, float start,
+                     float* mass, float* log_mass, void* stream);
+
+/*
+ * Plan compaction (Q/K/V pooling): out[k] = (x[base_rows[k]] + sum_c sum_{p in
+ * segment (k,c)} x[item_rows[p >> item_shift]] * weights[p]) / normalizer[k] in
+ * fp32, cast to dtype.  Channel c of token t lives at t*token_stride +
+ * (c/64)*head_stride + c%64 for input and output.  Replaces
+ * WeightedBilinearTokenPlan.compact / compact_key / compact_query and
+ * TokenPlan.compact (vggt_omega/models/token_merging.py:343-385, 176-191), whose
+ * caller is vggt_omega/models/layers/attention.py:346-375.
+ */
+int vgo_compact(const void* x, int64_t x_token_stride, int64_t x_head_stride, int64_t x_rows,
+                const int64_t* base_rows, const int32_t* offsets, int64_t segs_per_row,
+                const uint32_t* items, int item_shift, const int64_t* item_rows,
+                const float* weights, int64_t n_weights, const float* normalizer, int64_t rows,
+                int64_t dim, void* out, int64_t out_token_stride, int64_t out_head_stride,
+                int dtype, void* stream);
+
+/*
+ * Dense [total, 4] restore map for vgo_top4_project: kept token keep[k] ->
+ * (k,k,k,k)/(1,0,0,0); source token source[i] -> parent[i,:]/weight[i,:]; with
+ * inverse != NULL (TokenPlan) token t -> inverse[t] one-hot.  Rows covered by
+ * neither stay as the caller initialised them (zero weights give zero rows, as
+ * the reference's `new_zeros` output does, token_merging.py:405-413).
+ */
+int vgo_restore_map(const int64_t* keep, int64_t n_keep, const int64_t* source,
+                    const int64_t* parent, const float* weight, int64_t n_source,
+                    const int64_t* inverse, int64_t total, int32_t* index_out, float* weight_out,
+                    void* stream);
+
+/*
+ * Exact four-support simplex fit (15 active sets, 5x5 KKT systems by Gaussian
+ * elimination with partial pivoting): `_convex_fit`
+ * (vggt_omega/models/sparse_convex.py:2260-2304) with the easy-accept rule of
+ * :2415-2418 (top1 >= easy_threshold keeps the one-hot fit).  Source rows[r] and
+ * supports[r,0..3] are token ids into `tokens` (normalised twice, eps).  With
+ * row_list != NULL only rows row_list[0 .. *n_list_device) are solved; with
+ * list_supports != NULL as well, list entry w takes its supports from
+ * list_supports[w,0..3] and writes them into supports[row_list[w],:] (the global
+ * fallback of :2424-2434).
+ */
+int vgo_convex_fit(const void* tokens, int64_t token_row_stride, int64_t n_tokens, int dtype,
+                   const int64_t* rows, int64_t* supports, const int64_t* list_supports,
+                   const float* top1,
+                   float easy_threshold, const int32_t* row_list, const int* n_list_device,
+                   int64_t n, int64_t dim, float eps, float ridge, float* fit, float* alpha,
+                   void* stream);
+
+/* Stable list of hard rows with fit < threshold and its length (sparse_convex.py:2424). */
+int vgo_failed_rows(const float* fit, const float* top1, float easy_threshold, int64_t n,
+                    float threshold, int32_t* list, int* count, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,70 @@
+"""Seeded synthetic inputs shared by the fixture script and the tests.
+
+`structured_tokens` builds a VGGT-Omega token layout [1, frames * (specials +
+H*W), dim] whose later frames are shifted, noisy copies of a latent scene, so
+merge planners find real matches, near-ties, hard cases and rejects:
+  frame f, patch (r, c) = scene[(r + f) % H, (c + 2f) % W] + sigma * noise,
+with sigma drawn per patch from {0.05, 0.3, 0.6, 1.5}; special tokens ~ N(0,1).
+Everything comes from torch's CPU generator, so every machine regenerates the
+same bits (the fixture manifest records a sha256 of each input).
+"""
+from __future__ import annotations
+
+import hashlib
+
+import torch
+
+NOISE_LEVELS = torch.tensor([0.05, 0.3, 0.6, 1.5])
+
+
+def structured_tokens(seed: int, frames: int, patch_hw: tuple[int, int], specials: int,
+                      dim: int) -> torch.Tensor:
+    g = torch.Generator().manual_seed(seed)
+    height, width = patch_hw
+    scene = torch.randn(height, width, dim, generator=g)
+    out = []
+    for f in range(frames):
+        rows = (torch.arange(height) + f) % height
+        cols = (torch.arange(width) + 2 * f) % width
+        patches = scene[rows][:, cols].reshape(height * width, dim)
+        sigma = NOISE_LEVELS[torch.randint(0, 4, (height * width,), generator=g)]
+        patches = patches + sigma[:, None] * torch.randn(height * width, dim, generator=g)
+        special = torch.randn(specials, dim, generator=g)
+        out.append(torch.cat((special, patches)))
+    return torch.cat(out)[None]
+
+
+def seeded_values(seed: int, shape: tuple[int, ...], dtype=torch.float32) -> torch.Tensor:
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g).to(dtype)
+
+
+def attention_weights(seed: int, dim: int) -> dict[str, torch.Tensor]:
+    """State dict of SelfAttention(dim, qkv_bias=True, mask_k_bias=True, use_qk_norm=True).
+
+    Non-trivial values everywhere (biases, LayerNorm affine) so that a dropped
+    term shows up in the output.
+    """
+    g = torch.Generator().manual_seed(seed)
+    head = 64
+
+    def r(*shape, s=0.02):
+        return torch.randn(*shape, generator=g) * s
+
+    bias_mask = torch.ones(3 * dim)
+    bias_mask[dim:2 * dim] = 0
+    return {
+        "qkv.weight": r(3 * dim, dim, s=dim ** -0.5),
+        "qkv.bias": r(3 * dim, s=0.1),
+        "qkv.bias_mask": bias_mask,
+        "proj.weight": r(dim, dim, s=dim ** -0.5),
+        "proj.bias": r(dim, s=0.1),
+        "q_norm.weight": 1.0 + r(head, s=0.1),
+        "q_norm.bias": r(head, s=0.1),
+        "k_norm.weight": 1.0 + r(head, s=0.1),
+        "k_norm.bias": r(head, s=0.1),
+    }
+
+
+def sha256(tensor: torch.Tensor) -> str:
+    return hashlib.sha256(tensor.detach().cpu().contiguous().numpy().tobytes()).hexdigest()

@@ -1,0 +1,371 @@
+"""GPU parity of the merge path (normalize, match, rank/select, CSR, mass,
+compaction, restore, convex fit, both planners) against the CPU oracle and the
+reference fixtures.
+
+Integer outputs (indices, keep/inverse, CSR order, integer masses) are
+compared bit-exactly.  Float reductions that the kernels perform in the
+oracle's operation order (segmented sums, masses, compaction, projection) are
+bit-exact too; scores and the convex fit are compared to tolerance, and any
+index difference must sit inside an exact bf16 tie.
+"""
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import layer as oracle_layer
+from oracle import merging as om
+from tests._tol import assert_close, rel_error
+from tests.conftest import import_package
+from tests.golden.inputs import attention_weights, seeded_values, structured_tokens
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).parent / "golden"
+KW = dict(frames=4, tokens_per_frame=261, patch_token_start=5, patch_hw=(16, 16))
+
+
+@pytest.fixture(scope="module")
+def kern():
+    return import_package("_kernels")
+
+
+@pytest.fixture(scope="module")
+def fx():
+    return np.load(GOLDEN / "fixtures_c1.npz")
+
+
+def ulp_bf16(x: torch.Tensor) -> torch.Tensor:
+    """bf16 spacing at |x| (float32 tensor of bf16 values)."""
+    e = torch.frexp(x.abs().clamp_min(1e-30))[1]
+    return torch.ldexp(torch.ones_like(x), e - 8)
+
+
+def score_tolerance(exact: torch.Tensor) -> torch.Tensor:
+    """One bf16 ulp, or the fp32 accumulation error of a unit-norm dot product
+    (about 2^-17 absolute) for scores so close to zero that it exceeds an ulp."""
+    return torch.maximum(ulp_bf16(exact) * 1.01, torch.full_like(exact, 2.0 ** -17))
+
+
+# ------------------------------------------------------------ normalize ----
+@pytest.mark.parametrize("dim,eps", [(1024, 1e-12), (1024, 1e-6), (64, 1e-6), (200, 1e-12)])
+def test_normalize_rows(kern, device, dim, eps):
+    print(f"[normalize] dim={dim}", flush=True)
+    g = torch.Generator().manual_seed(dim)
+    x = torch.randn(300, dim, generator=g) * 3
+    x[7] = 0.0  # eps path
+    rows = torch.randperm(300, generator=g)[:150]
+    out = kern.normalize_rows(x.to(device), rows.to(device), eps).cpu()
+    ref = F.normalize(x[rows], dim=-1, eps=eps).to(torch.bfloat16)
+    diff = out.float() != ref.float()
+    assert diff.float().mean() < 2e-3
+    if diff.any():
+        assert ((out.float() - ref.float()).abs()[diff] <= ulp_bf16(ref.float())[diff] * 1.01).all()
+    f32 = kern.normalize_rows(x.to(device), rows.to(device), eps, torch.float32).cpu()
+    assert rel_error(f32, F.normalize(x[rows], dim=-1, eps=eps)) < 1e-6
+
+
+# ------------------------------------------------------------- matching ----
+@pytest.mark.parametrize("topk", [1, 4])
+@pytest.mark.parametrize("ns,nd,dim", [(37, 11, 64), (300, 777, 1024), (1000, 130, 128)])
+def test_similarity_selection_is_exact_on_kernel_scores(kern, device, topk, ns, nd, dim):
+    print(f"[similarity] topk={topk} ns={ns} nd={nd} dim={dim}", flush=True)
+    g = torch.Generator().manual_seed(ns + nd + topk)
+    src = F.normalize(torch.randn(ns, dim, generator=g), dim=-1).bfloat16()
+    dst = F.normalize(torch.randn(nd, dim, generator=g), dim=-1).bfloat16()
+    dst[5] = dst[3]  # exact duplicate column: guaranteed ties
+    scores = torch.full((ns, nd), float("nan"), dtype=torch.bfloat16, device=device)
+    values, index = kern.similarity_topk(src.to(device), dst.to(device), topk, scores=scores)
+    scores = scores.float().cpu()
+    # (1) the kernel's bf16 scores are the exact-dot bf16 scores up to rare 1-ulp cases
+    exact = om.bf16_scores(src, dst)
+    mismatch = scores != exact
+    assert mismatch.float().mean() < 5e-3
+    if mismatch.any():
+        assert ((scores - exact).abs()[mismatch] <= score_tolerance(exact)[mismatch]).all()
+    # (2) given those scores, the selection is bit-exact (ties to the lower index)
+    ref_v, ref_i = om.topk_lowest_index(scores, topk)
+    assert torch.equal(index.cpu(), ref_i)
+    assert torch.equal(values.cpu(), ref_v)
+
+
+def test_similarity_ranges_rows_and_device_count(kern, device):
+    g = torch.Generator().manual_seed(3)
+    src = F.normalize(torch.randn(500, 256, generator=g), dim=-1).bfloat16()
+    dst = F.normalize(torch.randn(900, 256, generator=g), dim=-1).bfloat16()
+    rows = torch.randperm(500, generator=g)[:300]
+    count = torch.tensor([211], dtype=torch.int32)
+    index_map = torch.arange(900) * 7 + 3
+    n0, off1, n_dict = 128, 400, 128 + 300
+    scores = torch.full((300, n_dict), float("nan"), dtype=torch.bfloat16, device=device)
+    values, index = kern.similarity_topk(
+        src.to(device), dst.to(device), 4, src_rows=rows.to(device), n_src_device=count.to(device),
+        n_src=300, dict_ranges=(n0, off1, n_dict), index_map=index_map.to(device), scores=scores)
+    positions = torch.cat((torch.arange(n0), torch.arange(off1, off1 + n_dict - n0)))
+    kernel_scores = scores[:211].float().cpu()
+    exact = om.bf16_scores(src[rows[:211]], dst[positions])
+    assert ((kernel_scores - exact).abs() <= score_tolerance(exact)).all()
+    ref_v, ref_i = om.topk_lowest_index(kernel_scores, 4)
+    assert torch.equal(values[:211].cpu(), ref_v)
+    assert torch.equal(index[:211].cpu(), index_map[positions[ref_i]])
+    assert torch.isnan(scores[211:].float()).all()  # rows past the device count are untouched
+
+
+def test_streaming_top4_api(vgo, device):
+    g = torch.Generator().manual_seed(4)
+    q = torch.randn(64, 128, generator=g)
+    basis_t = torch.randn(128, 40, generator=g)
+    values, index = vgo.streaming_top4(q.to(device), basis_t.to(device))
+    assert values.shape == (64, 4) and index.dtype == torch.int64
+    exact = om.bf16_scores(q.bfloat16(), basis_t.T.bfloat16())
+    ref_v, _ = om.topk_lowest_index(exact, 4)
+    assert (values.cpu() - ref_v).abs().max() <= float(ulp_bf16(ref_v).max())
+    with pytest.raises(ValueError, match="at least four"):
+        vgo.streaming_top4(q.to(device), basis_t[:, :3].to(device))
+
+
+# ------------------------------------------------------ rank and select ----
+@pytest.mark.parametrize("batch,ns,nd,removed", [(1, 50, 20, 1), (2, 3000, 900, 1700),
+                                                 (1, 5000, 100, 5000), (1, 20000, 7000, 12345)])
+def test_fastvggt_assemble_exact(vgo, kern, device, batch, ns, nd, removed):
+    print(f"[assemble] batch={batch} ns={ns} removed={removed}", flush=True)
+    g = torch.Generator().manual_seed(ns + removed)
+    total = ns + nd + 37
+    perm = torch.randperm(total, generator=g)
+    sources = perm[:ns].sort().values
+    dests = perm[ns:ns + nd].sort().values
+    # bf16-valued scores with heavy ties
+    best = (torch.randint(0, 40, (batch, ns), generator=g).float() / 64).to(torch.bfloat16).float()
+    target = torch.randint(0, nd, (batch, ns), generator=g, dtype=torch.int32)
+    keep = torch.empty((batch, total - removed), dtype=torch.int64, device=device)
+    inverse = torch.empty((batch, total), dtype=torch.int64, device=device)
+    flags = torch.empty((batch, ns), dtype=torch.uint8, device=device)
+    best_d, target_d = best.to(device), target.to(device)
+    sources_d, dests_d = sources.to(device), dests.to(device)
+    lib = import_package("_lib")
+    status = lib.load().vgo_fastvggt_assemble(
+        best_d.data_ptr(), target_d.data_ptr(), sources_d.data_ptr(), dests_d.data_ptr(), batch,
+        ns, nd, total, removed, keep.data_ptr(), inverse.data_ptr(), flags.data_ptr(),
+        torch.cuda.current_stream().cuda_stream)
+    lib.check(status)
+    torch.cuda.synchronize()
+    for b in range(batch):
+        rk, ri = om.fastvggt_select(best[b], target[b].long(), sources, dests, total, removed)
+        assert torch.equal(keep[b].cpu(), rk)
+        assert torch.equal(inverse[b].cpu(), ri)
+
+
+# --------------------------------------------------------- FastVGGT plan ----
+@pytest.mark.parametrize("tag,ratio,protect", [("fv50", 0.5, 0.0), ("fvdef", 0.9, 0.10)])
+def test_fastvggt_plan_vs_reference(vgo, device, fx, tag, ratio, protect):
+    tokens = structured_tokens(1, 4, (16, 16), 5, 1024)
+    plan = vgo.build_fastvggt_plan(tokens.to(device), merge_ratio=ratio, protect_ratio=protect, **KW)
+    sources, dests, best, target, _ = plan._derived["match"]
+    # selection is exact given the kernel's scores
+    rk, ri = om.fastvggt_select(best[0].cpu(), target[0].cpu().long(), sources.cpu(), dests.cpu(),
+                                1044, plan.original_tokens - plan.kept_tokens)
+    assert torch.equal(plan.keep[0].cpu(), rk) and torch.equal(plan.inverse[0].cpu(), ri)
+    # and the kernel's match agrees with the oracle's exact-score match
+    o = om.fastvggt_plan(tokens, merge_ratio=ratio, protect_ratio=protect, **KW)
+    assert (best[0].cpu() - o["best"]).abs().max() <= float(ulp_bf16(o["best"]).max())
+    agree = best[0].cpu() == o["best"]
+    assert torch.equal(target[0].cpu().long()[agree], o["targets"][agree])
+    # end to end against the reference's own plan
+    if agree.all():
+        assert np.array_equal(plan.keep[0].cpu().numpy(), fx[f"{tag}_keep"])
+        assert np.array_equal(plan.inverse[0].cpu().numpy(), fx[f"{tag}_inverse"])
+
+
+def test_fastvggt_plan_batch_and_determinism(vgo, device):
+    tokens = torch.cat([structured_tokens(s, 4, (16, 16), 5, 256) for s in (5, 6)]).to(device)
+    a = vgo.build_fastvggt_plan(tokens, merge_ratio=0.5, protect_ratio=0.1, **KW)
+    b = vgo.build_fastvggt_plan(tokens, merge_ratio=0.5, protect_ratio=0.1, **KW)
+    assert torch.equal(a.keep, b.keep) and torch.equal(a.inverse, b.inverse)
+    for i in range(2):
+        single = vgo.build_fastvggt_plan(tokens[i:i + 1], merge_ratio=0.5, protect_ratio=0.1, **KW)
+        assert torch.equal(single.keep[0], a.keep[i])
+    with pytest.raises(ValueError, match="layout"):
+        vgo.build_fastvggt_plan(tokens[:, :1000], merge_ratio=0.5, **KW)
+    ident = vgo.build_fastvggt_plan(tokens, merge_ratio=0.0, **KW)
+    assert ident.kept_tokens == 1044
+
+
+# --------------------------------------------------- CSR, mass, compact ----
+@pytest.mark.parametrize("n,buckets", [(1, 1), (1000, 37), (70000, 9000), (300000, 4)])
+def test_csr_is_a_stable_bucket_sort(kern, device, n, buckets):
+    g = torch.Generator().manual_seed(n)
+    keys = torch.randint(0, buckets + 3, (n,), generator=g)  # some out of range: dropped
+    order, offsets = kern.csr_build(keys.to(device), buckets)
+    valid = keys < buckets
+    ref_order = torch.argsort(torch.where(valid, keys, buckets), stable=True)[: int(valid.sum())]
+    counts = torch.bincount(keys[valid], minlength=buckets)
+    ref_offsets = torch.cat((torch.zeros(1, dtype=torch.long), counts.cumsum(0)))
+    assert torch.equal(order.cpu()[: int(valid.sum())].long(), ref_order)
+    assert torch.equal(offsets.cpu().long(), ref_offsets)
+
+
+def _random_weighted_plan(seed, total, kept, sources, one_hot=False):
+    g = torch.Generator().manual_seed(seed)
+    perm = torch.randperm(total, generator=g)
+    keep = perm[:kept].sort().values
+    src = perm[kept:kept + sources].sort().values
+    parent = torch.stack([torch.randperm(kept, generator=g)[:4] for _ in range(sources)])
+    e = -torch.rand(sources, 4, generator=g, dtype=torch.float64).log()
+    w = (e / e.sum(1, keepdim=True)).float()
+    if one_hot:
+        w = torch.zeros(sources, 4)
+        w[:, 0] = 1
+    return keep, src, parent, w
+
+
+@pytest.mark.parametrize("one_hot", [False, True])
+def test_deterministic_mass_bit_exact(vgo, device, one_hot):
+    keep, src, parent, w = _random_weighted_plan(11, 3000, 900, 2000, one_hot)
+    mass = vgo.deterministic_weighted_normalizer(parent[None].to(device), w[None].to(device), 900)
+    ref = om.deterministic_weighted_normalizer(parent[None], w[None], 900)
+    assert torch.equal(mass.cpu(), ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_weighted_plan_compact_restore_bit_exact(vgo, device, dtype):
+    print(f"[weighted plan] dtype={dtype}", flush=True)
+    keep, src, parent, w = _random_weighted_plan(12, 2500, 700, 1800)
+    mass = om.deterministic_weighted_normalizer(parent[None], w[None], 700)
+    plan = vgo.WeightedBilinearTokenPlan(
+        keep=keep[None].to(device), source_original=src[None].to(device),
+        source_parent_compact=parent[None].to(device), source_pool_weights=w[None].to(device),
+        source_restore_weights=w[None].to(device), original_tokens=2500,
+        normalizer=mass.to(device))
+    value = seeded_values(5, (1, 2500, 1024), dtype)
+    out = plan.compact(value.to(device))
+    ref = om.weighted_compact(keep, src, parent, w, mass, value[0])
+    assert torch.equal(out[0].cpu(), ref)
+    small = seeded_values(6, (1, 700, 1024), dtype)
+    restored = plan.restore(small.to(device))
+    assert torch.equal(restored[0].cpu(), om.weighted_restore(keep, src, parent, w, 2500, small[0]))
+    # head-major [H, N, 64] views compact the same way without copies
+    hm = value[0].reshape(2500, 16, 64).transpose(0, 1).contiguous().to(device)
+    out_hm = torch.empty((16, 700, 64), dtype=dtype, device=device)
+    plan.compact_into(hm, out_hm)
+    assert torch.equal(out_hm.transpose(0, 1).reshape(700, 1024).cpu(), ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_token_plan_compact_restore_bit_exact(vgo, device, fx, dtype):
+    inv = torch.from_numpy(fx["fv50_inverse"])
+    keep = torch.from_numpy(fx["fv50_keep"])
+    plan = vgo.TokenPlan(keep[None].to(device), inv[None].to(device), 1044)
+    value = seeded_values(7, (1, 1044, 32), dtype)
+    out = plan.compact(value.to(device))
+    assert torch.equal(out[0].cpu(), om.token_plan_compact(inv, keep.numel(), value[0]))
+    assert rel_error(out[0].cpu(), torch.from_numpy(fx[f"fv_compact_{'f32' if dtype == torch.float32 else 'bf16'}"])) <= (1e-6 if dtype == torch.float32 else 1e-2)
+    gathered = plan.compact(value.to(device), merge=False)
+    assert torch.equal(gathered[0].cpu(), value[0][keep])
+    small = seeded_values(8, (1, keep.numel(), 32), dtype)
+    restored = plan.restore(small.to(device))
+    assert torch.equal(restored[0].cpu(), small[0][inv])
+
+
+# ------------------------------------------------------------ convex fit ----
+def test_convex_fit_matches_oracle(vgo, device):
+    tokens = structured_tokens(1, 4, (16, 16), 5, 1024)
+    o = om.sparse_convex_plan(tokens, threshold=0.9, **KW)
+    hard = o["hard"]
+    rows = o["candidate"][hard]
+    supports = o["support"][hard].contiguous()
+    fit, alpha = vgo.convex_fit(tokens[0].to(device), rows.to(device), supports.clone().to(device))
+    normalized = F.normalize(tokens[0], dim=-1, eps=1e-6)
+    ref_fit, ref_alpha = om.convex_fit(F.normalize(normalized[rows], dim=-1, eps=1e-6),
+                                       F.normalize(normalized[supports], dim=-1, eps=1e-6))
+    assert (fit.cpu() - ref_fit).abs().max() < 2e-5
+    assert (alpha.cpu() - ref_alpha).abs().max() < 2e-3
+    assert torch.allclose(alpha.sum(1).cpu(), torch.ones(len(hard)), atol=1e-5)
+
+
+# --------------------------------------------------------- sparse convex ----
+def test_sparse_convex_plan_vs_oracle_and_reference(vgo, device, fx):
+    tokens = structured_tokens(1, 4, (16, 16), 5, 1024)
+    plan = vgo.build_sparse_convex_plan(tokens.to(device), threshold=0.9, **KW)
+    o = om.sparse_convex_plan(tokens, threshold=0.9, **KW)
+    fit = plan._derived["fit"][0].cpu()
+    # Decisions agree except for fits within fp32 rounding of the threshold.
+    assert not ((o["fit"] - 0.9).abs() < 1e-5).any(), "fixture has a fit inside the rounding band"
+    assert torch.equal(plan.keep[0].cpu(), o["keep"])
+    assert torch.equal(plan.source_original[0].cpu(), o["source_original"])
+    assert (fit - o["fit"]).abs().max() < 2e-5
+    assert (plan.source_pool_weights[0].cpu() - o["weights"]).abs().max() < 2e-3
+    same_parent = (plan.source_parent_compact[0].cpu() == o["parent_compact"]).all(1)
+    assert same_parent.float().mean() > 0.99
+    assert torch.equal(plan.special_query_compact.cpu(), o["special_compact"])
+    # mass is the deterministic normalizer of the plan's own parents/weights, bit-exact
+    ref_mass = om.deterministic_weighted_normalizer(plan.source_parent_compact.cpu(),
+                                                    plan.source_pool_weights.cpu(), plan.kept_tokens)
+    assert torch.equal(plan.normalizer.cpu(), ref_mass)
+    assert rel_error(plan.key_log_mass.cpu().reshape(-1), ref_mass.reshape(-1).log()) < 1e-6
+    # against the reference fixture: same keep/sources, weights to tolerance
+    assert np.array_equal(plan.keep[0].cpu().numpy(), fx["sc_keep"])
+    assert np.array_equal(plan.source_original[0].cpu().numpy(), fx["sc_source"])
+    assert np.abs(plan.source_pool_weights[0].cpu().numpy() - fx["sc_weight"]).max() < 2e-3
+    md = plan.metadata
+    assert md["hard_candidates"] == 393 and md["fallback_candidates"] == 390
+    assert abs(md["merge_ratio"] - 186 / 1044) < 1e-9
+
+
+# ---------------------------------------------------------- attention layer ----
+@pytest.mark.parametrize("tag,preserve", [("attn_qkv", False), ("attn_kv", True)])
+def test_self_attention_layer_vs_reference(vgo, device, fx, tag, preserve):
+    print(f"[layer] {tag}", flush=True)
+    x = structured_tokens(3, 4, (16, 16), 5, 128)
+    layer = vgo.SelfAttention(128, num_heads=2, qkv_bias=True, mask_k_bias=True,
+                              use_qk_norm=True).eval().to(device)
+    layer.load_state_dict(attention_weights(4, 128))
+    keep = torch.from_numpy(fx[f"{tag}_keep"])
+    parent = torch.from_numpy(fx[f"{tag}_parent"])
+    w = torch.from_numpy(fx[f"{tag}_weight"])
+    mass = torch.from_numpy(fx[f"{tag}_mass"])
+    special = (torch.arange(4)[:, None] * 261 + torch.arange(5)[None]).flatten()
+    plan = vgo.WeightedBilinearTokenPlan(
+        keep=keep[None].to(device), source_original=torch.from_numpy(fx[f"{tag}_source"])[None].to(device),
+        source_parent_compact=parent[None].to(device), source_pool_weights=w[None].to(device),
+        source_restore_weights=w[None].to(device), original_tokens=1044,
+        normalizer=mass.view(1, -1, 1).to(device), preserve_queries=preserve,
+        preserve_destination_keys=preserve, dense_special_queries=True,
+        special_query_original=special.to(device),
+        special_query_compact=torch.from_numpy(fx[f"{tag}_special_compact"]).to(device),
+        key_log_mass=mass.log().view(1, -1).to(device))
+    with torch.no_grad():
+        out = layer(x.to(device), token_plan=plan)
+    assert_close(out[0].cpu(), torch.from_numpy(fx[f"{tag}_out"]), torch.float32, rtol=2e-5,
+                 what=f"{tag} fp32 layer")
+    # bf16 autocast path against the oracle's bf16-autocast semantics
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        out_bf16 = layer(x.to(device), token_plan=plan)
+    assert out_bf16.dtype == torch.bfloat16
+    oplan = dict(keep=keep, source_original=torch.from_numpy(fx[f"{tag}_source"]),
+                 parent_compact=parent, weights=w, mass=mass, special_original=special,
+                 special_compact=torch.from_numpy(fx[f"{tag}_special_compact"]))
+    ref_bf16 = oracle_layer.self_attention(x[0], attention_weights(4, 128), 2, oplan, preserve,
+                                           autocast_bf16=True)
+    assert_close(out_bf16[0].float().cpu(), ref_bf16.float(), torch.bfloat16,
+                 what=f"{tag} bf16 layer")
+
+
+def test_block_forward_compacted(vgo, device):
+    torch.manual_seed(0)
+    block = vgo.SelfAttentionBlock(256, 4, qkv_bias=True, init_values=0.5, mask_k_bias=True,
+                                   use_qk_norm=True).eval().to(device)
+    x = structured_tokens(9, 4, (16, 16), 5, 256).to(device)
+    plan = vgo.build_sparse_convex_plan(block.norm1(x), threshold=0.9, **KW)
+    with torch.no_grad():
+        out = block.forward_compacted(x, plan)
+        normalized = block.norm1(x)
+        again = block.forward_compacted(x, plan, normalized=normalized)
+    assert torch.equal(out, again)
+    assert out.shape == x.shape and torch.isfinite(out).all()
+    block.train()
+    with pytest.raises(RuntimeError, match="inference-only"):
+        block.forward_compacted(x, plan)

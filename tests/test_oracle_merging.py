@@ -1,0 +1,171 @@
+"""Pins the merge oracle against fixtures written from the real reference (CPU only).
+
+tests/golden/fixtures_c1.npz holds the outputs of the reference's own
+build_fastvggt_plan, build_sparse_convex_plan, plan.compact / plan.restore and
+SelfAttention.forward on seeded inputs (see tests/golden/make_fixtures.py).
+The one documented divergence is the order of exact bf16 ties in the top-4
+(torch.topk leaves it open; this project sends ties to the lower position, the
+contract of the reference's Triton streaming_top4): those rows are checked to
+differ only by tied candidates.
+"""
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import layer as oracle_layer
+from oracle import merging as om
+from tests._tol import rel_error
+from tests.golden.inputs import attention_weights, seeded_values, sha256, structured_tokens
+
+GOLDEN = Path(__file__).parent / "golden"
+KW = dict(frames=4, tokens_per_frame=261, patch_token_start=5, patch_hw=(16, 16))
+
+
+@pytest.fixture(scope="module")
+def fx():
+    return np.load(GOLDEN / "fixtures_c1.npz")
+
+
+@pytest.fixture(scope="module")
+def tokens():
+    t = structured_tokens(1, 4, (16, 16), 5, 1024)
+    import json
+    manifest = json.loads((GOLDEN / "fixtures_c1.json").read_text())
+    assert sha256(t) == manifest["tokens_sha256"], "seeded inputs no longer regenerate bit-exactly"
+    return t
+
+
+@pytest.fixture(scope="module")
+def sc_plan(tokens):
+    return om.sparse_convex_plan(tokens, threshold=0.9, **KW)
+
+
+@pytest.mark.parametrize("tag,ratio,protect", [("fv50", 0.5, 0.0), ("fvdef", 0.9, 0.10)])
+def test_fastvggt_plan_matches_reference(fx, tokens, tag, ratio, protect):
+    o = om.fastvggt_plan(tokens, merge_ratio=ratio, protect_ratio=protect, **KW)
+    assert np.array_equal(o["keep"].numpy(), fx[f"{tag}_keep"])
+    assert np.array_equal(o["inverse"].numpy(), fx[f"{tag}_inverse"])
+
+
+def test_fastvggt_invariants(tokens):
+    o = om.fastvggt_plan(tokens, merge_ratio=0.5, protect_ratio=0.0, **KW)
+    total = tokens.shape[1]
+    assert o["keep"].numel() == total - o["removed"] == total - min(int(total * 0.5), o["sources"].numel())
+    removed = torch.ones(total, dtype=torch.bool)
+    removed[o["keep"]] = False
+    # specials and frame-0 patches are never removed; keep and removed partition the tokens
+    specials = (torch.arange(4)[:, None] * 261 + torch.arange(5)[None]).flatten()
+    assert not removed[specials].any() and not removed[5:261].any()
+    assert torch.equal(o["inverse"][o["keep"]], torch.arange(o["keep"].numel()))
+    assert (o["inverse"] >= 0).all()
+
+
+def test_sparse_convex_plan_matches_reference(fx, sc_plan, tokens):
+    o = sc_plan
+    assert np.array_equal(o["keep"].numpy(), fx["sc_keep"])
+    assert np.array_equal(o["source_original"].numpy(), fx["sc_source"])
+    assert np.array_equal(o["special_compact"].numpy(), fx["sc_special_compact"])
+    assert np.array_equal(o["weights"].numpy(), fx["sc_weight"])
+    # Parents may differ only inside exact bf16 ties of the top-4.
+    ours, ref = o["parent_compact"].numpy(), fx["sc_parent"]
+    keep = o["keep"]
+    normalized = torch.nn.functional.normalize(tokens[0].float(), dim=-1, eps=1e-6).bfloat16()
+    diff_rows = np.nonzero((ours != ref).any(1))[0]
+    for r in diff_rows:
+        s = normalized[o["source_original"][r]].double()
+        score = lambda ids: (normalized[keep[ids]].double() @ s).to(torch.bfloat16)  # noqa: E731
+        assert torch.equal(score(torch.from_numpy(ours[r])), score(torch.from_numpy(ref[r])))
+    assert len(diff_rows) < 0.2 * len(ours)
+    # Mass: conservation (each row of weights sums to one) and the deterministic order.
+    mass = o["mass"]
+    assert abs(float(mass.double().sum()) - (keep.numel() + o["source_original"].numel())) < 1e-3
+    assert abs(float(mass.double().sum()) - float(fx["sc_mass"].astype(np.float64).sum())) < 1e-3
+
+
+def test_sparse_convex_metadata_counts(sc_plan):
+    assert sc_plan["hard"].numel() == 393
+    assert sc_plan["failed"].numel() == 390
+
+
+def test_convex_fit_satisfies_kkt(sc_plan, tokens):
+    # For interior solutions the residual of the simplex LS problem is orthogonal to
+    # the active face: g_i = (S^T (S a - x))_i equal across active i (Lagrange).
+    normalized = torch.nn.functional.normalize(tokens[0].float(), dim=-1, eps=1e-6)
+    hard = sc_plan["hard"][:64]
+    src = torch.nn.functional.normalize(normalized[sc_plan["candidate"][hard]], dim=-1, eps=1e-6)
+    sup = torch.nn.functional.normalize(normalized[sc_plan["support"][hard]], dim=-1, eps=1e-6)
+    fit, alpha = om.convex_fit(src, sup)
+    assert torch.allclose(alpha.sum(1), torch.ones(len(hard)), atol=1e-5)
+    assert (alpha >= 0).all()
+    for i in range(len(hard)):
+        a = alpha[i].double()
+        if a.max() >= 1.0:
+            continue  # one-hot override
+        s = sup[i].double()
+        grad = s @ (s.T @ a - src[i].double())
+        active = a > 1e-4
+        if active.sum() >= 2:
+            g = grad[active]
+            assert float(g.max() - g.min()) < 2e-3 + 1e-3 * float(g.abs().max())
+        # inactive coordinates have gradient >= the active level (KKT dual feasibility)
+        if (~active).any() and active.any():
+            assert float(grad[~active].min()) >= float(grad[active].max()) - 2e-3
+
+
+@pytest.mark.parametrize("dtype,dtag", [(torch.float32, "f32"), (torch.bfloat16, "bf16")])
+def test_plan_compact_and_restore_match_reference(fx, dtype, dtag):
+    keep = torch.from_numpy(fx["sc_keep"])
+    src = torch.from_numpy(fx["sc_source"])
+    parent = torch.from_numpy(fx["sc_parent"])
+    w = torch.from_numpy(fx["sc_weight"])
+    mass = torch.from_numpy(fx["sc_mass"])
+    value = seeded_values(7, (1, 1044, 32), dtype)[0]
+    tol = 1e-6 if dtype == torch.float32 else 1e-2
+    out = om.weighted_compact(keep, src, parent, w, mass, value)
+    assert rel_error(out, torch.from_numpy(fx[f"sc_compact_{dtag}"])) <= tol
+    small = seeded_values(8, (1, keep.numel(), 32), dtype)[0]
+    restored = om.weighted_restore(keep, src, parent, w, 1044, small)
+    assert torch.equal(restored.float(), torch.from_numpy(fx[f"sc_restore_{dtag}"]))
+    inv = torch.from_numpy(fx["fv50_inverse"])
+    kept = int(inv.max()) + 1
+    fv = om.token_plan_compact(inv, kept, value)
+    assert rel_error(fv, torch.from_numpy(fx[f"fv_compact_{dtag}"])) <= (1e-6 if dtype == torch.float32 else 1e-2)
+    small_fv = seeded_values(8, (1, kept, 32), dtype)[0]
+    assert torch.equal(om.token_plan_restore(inv, small_fv).float(),
+                       torch.from_numpy(fx[f"fv_restore_{dtag}"]))
+
+
+def test_deterministic_normalizer_integer_masses_are_counts():
+    parent = torch.tensor([[[0, 1, 2, 3], [0, 0, 0, 0], [3, 2, 1, 0]]])
+    w = torch.tensor([[[1., 0., 0., 0.], [1., 0., 0., 0.], [0., 0., 0., 1.]]])
+    mass = om.deterministic_weighted_normalizer(parent, w, 4)
+    assert torch.equal(mass.reshape(-1), torch.tensor([4., 1., 1., 1.]))
+
+
+@pytest.mark.parametrize("tag,preserve", [("attn_qkv", False), ("attn_kv", True)])
+def test_attention_layer_matches_reference(fx, tag, preserve):
+    x = structured_tokens(3, 4, (16, 16), 5, 128)[0]
+    plan = dict(keep=torch.from_numpy(fx[f"{tag}_keep"]),
+                source_original=torch.from_numpy(fx[f"{tag}_source"]),
+                parent_compact=torch.from_numpy(fx[f"{tag}_parent"]),
+                weights=torch.from_numpy(fx[f"{tag}_weight"]),
+                mass=torch.from_numpy(fx[f"{tag}_mass"]),
+                special_original=(torch.arange(4)[:, None] * 261 + torch.arange(5)[None]).flatten(),
+                special_compact=torch.from_numpy(fx[f"{tag}_special_compact"]))
+    out = oracle_layer.self_attention(x, attention_weights(4, 128), 2, plan, preserve)
+    assert rel_error(out, torch.from_numpy(fx[f"{tag}_out"])) < 1e-5
+
+
+def test_checks_have_teeth(fx):
+    # A transposed corner order in the restore breaks the fixture comparison.
+    keep = torch.from_numpy(fx["sc_keep"])
+    src = torch.from_numpy(fx["sc_source"])
+    parent = torch.from_numpy(fx["sc_parent"])
+    w = torch.from_numpy(fx["sc_weight"])
+    small = seeded_values(8, (1, keep.numel(), 32), torch.float32)[0]
+    bad = om.weighted_restore(keep, src, parent.flip(1), w, 1044, small)
+    assert not torch.equal(bad, torch.from_numpy(fx["sc_restore_f32"]))
