@@ -1,0 +1,235 @@
+"""Alternating frame / inter-frame attention encoder with merged global blocks.
+
+The caller of the merged global-attention path: the per-block loop and the
+global branch of vggt_omega/models/aggregator.py:49-1293, with the reference's
+parameter names (frame_blocks, inter_frame_blocks, camera_token,
+register_token) and merge setters (`set_fastvggt`, `set_sparse_convex`,
+`set_input_patch_tokens_cache`).  Scope:
+
+* global blocks run `build_fastvggt_plan` or `build_sparse_convex_plan`
+  ("fixed_topology") and `SelfAttentionBlock.forward_compacted` on the HIP
+  library; register blocks and frame blocks (RoPE) are stock PyTorch as in the
+  reference;
+* the DINOv3 patch encoder is not part of this path: forward() consumes the
+  patch tokens installed with `set_input_patch_tokens_cache` (the reference's
+  own bypass, aggregator.py:233-241, 735-743);
+* the other planners (k-means, hash, TTT, temporal, reference-anchor, affine)
+  are out of scope and rejected by the setters.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from . import profiling
+from .layers import Mlp, SelfAttentionBlock, init_weights_vit, rope_sincos
+from .sparse_convex import build_sparse_convex_plan
+from .token_merging import build_fastvggt_plan
+
+_DEFAULT_SPARSE_CONVEX_QKV_LAYERS = tuple(layer for layer in range(19) if layer not in {8, 10, 11, 12})
+
+
+class Aggregator(nn.Module):
+    def __init__(self, patch_size: int = 16, embed_dim: int = 1024, depth: int = 24,
+                 num_heads: int = 16, mlp_ratio: float = 4.0, num_register_tokens: int = 16,
+                 register_attention_block_indices: tuple[int, ...] = (2, 6, 9, 14, 20),
+                 cached_layer_indices: tuple[int, ...] = (4, 11, 17, 23),
+                 device=None) -> None:
+        super().__init__()
+
+        def block():
+            return SelfAttentionBlock(dim=embed_dim, num_heads=num_heads, ffn_ratio=mlp_ratio,
+                                      qkv_bias=True, proj_bias=True, ffn_bias=True, ffn_layer=Mlp,
+                                      init_values=1e-5, use_qk_norm=True, mask_k_bias=True,
+                                      device=device)
+
+        self.frame_blocks = nn.ModuleList([block() for _ in range(depth)])
+        self.inter_frame_blocks = nn.ModuleList([block() for _ in range(depth)])
+        self.depth = depth
+        self.patch_size = patch_size
+        self.num_heads = num_heads
+        self.cached_layer_indices = set(cached_layer_indices)
+        self.camera_token = nn.Parameter(torch.empty(1, 2, 1, embed_dim, device=device))
+        self.register_token = nn.Parameter(torch.empty(1, 2, num_register_tokens, embed_dim, device=device))
+        self.patch_token_start = 1 + num_register_tokens
+        self.inter_frame_attention_types = ["global"] * depth
+        for idx in register_attention_block_indices:
+            if idx < 0 or idx >= depth:
+                raise ValueError(f"register_attention_block_indices contains invalid block index {idx}")
+            self.inter_frame_attention_types[idx] = "register"
+        self.fastvggt_enabled = False
+        self.fastvggt_merge_ratio = 0.9
+        self.fastvggt_protect_ratio = 0.10
+        self.fastvggt_mass_bias = False
+        self.fastvggt_last_plan_stats: list[dict[str, float | int]] = []
+        self.sparse_convex_enabled = False
+        self.sparse_convex_threshold = .90
+        self.sparse_convex_planner = "fixed_topology"
+        self.sparse_convex_qkv_global_blocks = 15
+        self.sparse_convex_qkv_global_layers: frozenset[int] | None = frozenset(_DEFAULT_SPARSE_CONVEX_QKV_LAYERS)
+        self.sparse_convex_physical_key_layers: frozenset[int] = frozenset()
+        self.sparse_convex_dense_global_layers: frozenset[int] = frozenset()
+        self.sparse_convex_last_plan_stats: list[dict[str, float | int]] = []
+        self._input_patch_tokens_cache: torch.Tensor | None = None
+        self.init_weights()
+
+    # ---------------------------------------------------------- setters ----
+    def set_fastvggt(self, enabled: bool = True, merge_ratio: float = 0.9,
+                     protect_ratio: float = 0.10, mass_bias: bool = False) -> None:
+        """FastVGGT bipartite merging (aggregator.py:219-231); `mass_bias` adds log(cluster
+        size) as the per-key attention bias."""
+        if not 0.0 <= merge_ratio <= 1.0 or not 0.0 <= protect_ratio <= 1.0:
+            raise ValueError("FastVGGT ratios must lie in [0, 1]")
+        if enabled and self.sparse_convex_enabled:
+            raise ValueError("FastVGGT, temporal merging, reference-anchor, and reference-cluster merging are mutually exclusive")
+        self.fastvggt_enabled, self.fastvggt_merge_ratio = enabled, merge_ratio
+        self.fastvggt_protect_ratio, self.fastvggt_mass_bias = protect_ratio, mass_bias
+
+    def set_sparse_convex(self, enabled: bool = True, threshold: float = .90,
+                          qkv_global_blocks: int = 15,
+                          qkv_global_layers: tuple[int, ...] | None = _DEFAULT_SPARSE_CONVEX_QKV_LAYERS,
+                          physical_key_layers: tuple[int, ...] = (),
+                          planner: str = "fixed_topology",
+                          dense_global_layers: tuple[int, ...] = ()) -> None:
+        """Sparse-convex merging (aggregator.py:243-289), fixed-topology planner."""
+        if not -1.0 <= threshold <= 1.000001:
+            raise ValueError("sparse-convex threshold must lie in [-1,1]")
+        global_count = sum(kind == "global" for kind in self.inter_frame_attention_types)
+        if not 0 <= qkv_global_blocks <= global_count:
+            raise ValueError("invalid sparse-convex QKV global-block count")
+        if planner != "fixed_topology":
+            raise ValueError("only the fixed_topology sparse-convex planner is part of this path")
+        for name, layers in (("qkv_global_layers", qkv_global_layers),
+                             ("physical_key_layers", physical_key_layers),
+                             ("dense_global_layers", dense_global_layers)):
+            if layers is not None and any(not 0 <= int(layer) < global_count for layer in layers):
+                raise ValueError(f"invalid sparse-convex {name}: {layers}")
+        if enabled and self.fastvggt_enabled:
+            raise ValueError("sparse-convex merging is mutually exclusive with other merge modes")
+        self.sparse_convex_enabled = bool(enabled)
+        self.sparse_convex_threshold = float(threshold)
+        self.sparse_convex_planner = planner
+        self.sparse_convex_qkv_global_blocks = int(qkv_global_blocks)
+        self.sparse_convex_qkv_global_layers = (
+            None if qkv_global_layers is None else frozenset(int(x) for x in qkv_global_layers))
+        self.sparse_convex_physical_key_layers = frozenset(int(x) for x in physical_key_layers)
+        self.sparse_convex_dense_global_layers = frozenset(int(x) for x in dense_global_layers)
+
+    def set_input_patch_tokens_cache(self, tokens: torch.Tensor | None) -> None:
+        """Install or clear the patch tokens consumed by forward() (aggregator.py:233-241)."""
+        if tokens is not None:
+            if tokens.ndim != 3 or tokens.shape[-1] != self.camera_token.shape[-1]:
+                raise ValueError("cached patch tokens must be [batch*frames,patches,embed_dim]")
+            if not bool(torch.isfinite(tokens).all()):
+                raise ValueError("cached patch tokens must be finite")
+            tokens = tokens.detach().contiguous()
+        self._input_patch_tokens_cache = tokens
+
+    def init_weights(self) -> None:
+        nn.init.normal_(self.camera_token, std=1e-3)
+        nn.init.normal_(self.register_token, std=1e-3)
+        for blocks in (self.frame_blocks, self.inter_frame_blocks):
+            for module in blocks.modules():
+                init_weights_vit(module)
+
+    # ---------------------------------------------------------- forward ----
+    def forward(self, images: torch.Tensor) -> tuple[list[torch.Tensor | None], int]:
+        batch_size, num_frames, num_channels, height, width = images.shape
+        if num_channels != 3:
+            raise ValueError(f"Expected 3 input channels, got {num_channels}")
+        patch_tokens = self._input_patch_tokens_cache
+        if patch_tokens is None:
+            raise RuntimeError("the DINOv3 patch encoder is not part of this build: install patch "
+                               "tokens with set_input_patch_tokens_cache()")
+        grid = (height // self.patch_size, width // self.patch_size)
+        if (patch_tokens.shape[0] != batch_size * num_frames
+                or patch_tokens.shape[1] != grid[0] * grid[1]
+                or patch_tokens.device != images.device):
+            raise ValueError("cached patch tokens do not match the current model input")
+        camera = _slice_expand_and_flatten(self.camera_token, batch_size, num_frames)
+        register = _slice_expand_and_flatten(self.register_token, batch_size, num_frames)
+        tokens = torch.cat([camera.to(patch_tokens.dtype), register.to(patch_tokens.dtype),
+                            patch_tokens], dim=1)
+        _, num_tokens, embed_dim = tokens.shape
+        with torch.no_grad():
+            sin, cos = rope_sincos(grid[0], grid[1], embed_dim // self.num_heads,
+                                   device=patch_tokens.device)
+        rope = (sin, cos)
+        self.fastvggt_last_plan_stats = []
+        self.sparse_convex_last_plan_stats = []
+        outputs: list[torch.Tensor | None] = []
+        for block_idx in range(self.depth):
+            tokens = tokens.view(batch_size * num_frames, num_tokens, embed_dim)
+            tokens = self.frame_blocks[block_idx](tokens, rope)
+            frame_tokens = tokens.view(batch_size, num_frames, num_tokens, embed_dim)
+            tokens = self._run_inter_frame_attention_block(
+                tokens, batch_size, num_frames, num_tokens, embed_dim, block_idx, grid)
+            if block_idx in self.cached_layer_indices:
+                outputs.append(torch.cat([frame_tokens, tokens], dim=-1))
+            else:
+                outputs.append(None)
+        return outputs, self.patch_token_start
+
+    def _run_inter_frame_attention_block(self, tokens, batch_size, num_frames, num_tokens,
+                                         embed_dim, block_idx, patch_hw) -> torch.Tensor:
+        kind = self.inter_frame_attention_types[block_idx]
+        block = self.inter_frame_blocks[block_idx]
+        tokens = tokens.view(batch_size, num_frames, num_tokens, embed_dim)
+        if kind == "register":
+            pts = self.patch_token_start
+            special = tokens[:, :, :pts].reshape(batch_size, num_frames * pts, embed_dim)
+            special = block(special, None).view(batch_size, num_frames, pts, embed_dim)
+            return torch.cat([special, tokens[:, :, pts:]], dim=2)
+        if kind != "global":
+            raise ValueError(f"Unknown inter-frame attention type: {kind}")
+        tokens = tokens.reshape(batch_size, num_frames * num_tokens, embed_dim)
+        global_ordinal = sum(k == "global" for k in self.inter_frame_attention_types[:block_idx])
+        if not (self.fastvggt_enabled or self.sparse_convex_enabled):
+            tokens = block(tokens, None)
+            return tokens.view(batch_size, num_frames, num_tokens, embed_dim)
+        with profiling.span("global.block"):
+            if self.sparse_convex_enabled and global_ordinal in self.sparse_convex_dense_global_layers:
+                tokens = block(tokens, None)
+                return tokens.view(batch_size, num_frames, num_tokens, embed_dim)
+            layout = dict(frames=num_frames, tokens_per_frame=num_tokens,
+                          patch_token_start=self.patch_token_start, patch_hw=patch_hw)
+            normalized = block.norm1(tokens)
+            with profiling.span("global.plan_build"):
+                if self.sparse_convex_enabled:
+                    if self.sparse_convex_qkv_global_layers is not None:
+                        compact_queries = global_ordinal in self.sparse_convex_qkv_global_layers
+                    else:
+                        compact_queries = global_ordinal < self.sparse_convex_qkv_global_blocks
+                    preserve_queries = not compact_queries
+                    preserve_keys = preserve_queries or global_ordinal in self.sparse_convex_physical_key_layers
+                    plan = build_sparse_convex_plan(
+                        normalized, threshold=self.sparse_convex_threshold,
+                        preserve_queries=preserve_queries, preserve_destination_keys=preserve_keys,
+                        **layout)
+                    self.sparse_convex_last_plan_stats.append({
+                        "block_index": block_idx, "global_ordinal": global_ordinal,
+                        "original_tokens": plan.original_tokens, "kept_tokens": plan.kept_tokens,
+                        "merged_tokens": plan.original_tokens - plan.kept_tokens,
+                        "merge_ratio": 1.0 - plan.keep_ratio,
+                        "compact_queries": bool(compact_queries), "physical_keys": bool(preserve_keys),
+                        "attention_query_tokens": int(plan.kept_tokens if compact_queries
+                                                      else plan.original_tokens),
+                        **plan.metadata})
+                else:
+                    plan = build_fastvggt_plan(normalized, merge_ratio=self.fastvggt_merge_ratio,
+                                               protect_ratio=self.fastvggt_protect_ratio,
+                                               mass_bias=self.fastvggt_mass_bias, **layout)
+                    self.fastvggt_last_plan_stats.append({
+                        "block_index": block_idx, "original_tokens": plan.original_tokens,
+                        "kept_tokens": plan.kept_tokens,
+                        "merged_tokens": plan.original_tokens - plan.kept_tokens,
+                        "merge_ratio": 1.0 - plan.keep_ratio, **plan.metadata})
+            tokens = block.forward_compacted(tokens, plan, normalized=normalized)
+        return tokens.view(batch_size, num_frames, num_tokens, embed_dim)
+
+
+def _slice_expand_and_flatten(token_tensor: torch.Tensor, batch_size: int, num_frames: int) -> torch.Tensor:
+    first = token_tensor[:, 0:1].expand(batch_size, 1, *token_tensor.shape[2:])
+    others = token_tensor[:, 1:].expand(batch_size, num_frames - 1, *token_tensor.shape[2:])
+    tokens = torch.cat([first, others], dim=1)
+    return tokens.view(batch_size * num_frames, *tokens.shape[2:])

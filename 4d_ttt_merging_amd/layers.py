@@ -31,7 +31,16 @@ import torch
 import torch.nn.functional as F
 from torch import Tensor, nn
 
+from . import profiling
 from .mass_bias_attention import _attention_into
+
+
+class _null:
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        return False
 
 
 def rope_rotate_half(x: Tensor) -> Tensor:
@@ -133,17 +142,21 @@ class SelfAttention(nn.Module):
         if token_plan is not None and self.training:
             raise RuntimeError("token compaction is inference-only")
         self._check_hooks()
-        qkv = (token_plan.precomputed_qkv
-               if token_plan is not None and getattr(token_plan, "precomputed_qkv", None) is not None
-               else self.qkv(x))
-        attn_v = self.compute_attention(qkv=qkv, attn_bias=attn_bias, rope=rope, token_plan=token_plan)
-        x = self.proj_drop(self.proj(attn_v))
         if token_plan is None:
-            return x
+            qkv = self.qkv(x)
+            return self.proj_drop(self.proj(self.compute_attention(qkv=qkv, attn_bias=attn_bias,
+                                                                   rope=rope)))
+        with profiling.span("global.qkv_projection"):
+            qkv = (token_plan.precomputed_qkv
+                   if getattr(token_plan, "precomputed_qkv", None) is not None else self.qkv(x))
+        attn_v = self.compute_attention(qkv=qkv, attn_bias=attn_bias, rope=rope, token_plan=token_plan)
+        with profiling.span("global.output_projection"):
+            x = self.proj_drop(self.proj(attn_v))
         if (getattr(token_plan, "source_query_correction", False)
                 and not getattr(token_plan, "preserve_queries", False)):
             raise NotImplementedError("source-query correction is outside the merged path")
-        return token_plan.restore(x)
+        with profiling.span("global.update_restore"):
+            return token_plan.restore(x)
 
     def compute_attention(self, qkv: Tensor, attn_bias=None, rope=None, token_plan=None) -> Tensor:
         assert attn_bias is None
@@ -153,11 +166,12 @@ class SelfAttention(nn.Module):
         D = C // H
         q, k, v = torch.unbind(qkv.reshape(B, N, 3, H, D), 2)
         q, k, v = [t.transpose(1, 2) for t in (q, k, v)]
-        if self.use_qk_norm:
-            q = self.q_norm(q)
-            k = self.k_norm(k)
-        if rope is not None:
-            q, k = self.apply_rope(q, k, rope)
+        with profiling.span("global.qk_norm_rope") if token_plan is not None else _null():
+            if self.use_qk_norm:
+                q = self.q_norm(q)
+                k = self.k_norm(k)
+            if rope is not None:
+                q, k = self.apply_rope(q, k, rope)
         if token_plan is None:
             x = F.scaled_dot_product_attention(q, k, v)
             return x.transpose(1, 2).reshape(B, N, C)
@@ -174,6 +188,7 @@ class SelfAttention(nn.Module):
             return torch.empty((B, H, rows, D), device=q.device, dtype=dtype)
 
         # Compaction between head-major views: no transpose copies.
+        compaction = profiling.span("global.qkv_compaction").__enter__()
         k_c = head_major(kept, k.dtype)
         v_c = head_major(kept, v.dtype)
         q_c = q if preserve_queries else head_major(n_query, q.dtype)
@@ -194,6 +209,7 @@ class SelfAttention(nn.Module):
                 plan.compact_into(v[b], v_c[b])
             else:
                 plan.compact_into(v[b], v_c[b], b=b, merge=plan.pool_sources)
+        compaction.__exit__(None, None, None)
 
         # Attention in the autocast dtype (reference mass_bias_attention.py:96-107).
         dtype = q.dtype
@@ -209,17 +225,19 @@ class SelfAttention(nn.Module):
                 raise ValueError("log_key_mass length does not match key tokens")
         out = torch.empty((B, n_query, H, D), device=q.device, dtype=dtype)
         x = out.permute(0, 2, 1, 3)  # [B, H, Nq, D] view written in [B, Nq, H, D] order
-        _attention_into(qa, ka, va, bias, x)
+        with profiling.span("global.main_attention"):
+            _attention_into(qa, ka, va, bias, x)
 
         if getattr(plan, "dense_special_queries", False):
             original = plan.special_query_original
             output_indices = original if preserve_queries else plan.special_query_compact
             if original is None or output_indices is None:
                 raise RuntimeError("dense-special attention plan has no special-token mapping")
-            special_q = q.index_select(2, original).to(dtype)
-            exact = torch.empty((B, H, original.numel(), D), device=q.device, dtype=dtype)
-            _attention_into(special_q, k.to(dtype), v.to(dtype), None, exact)
-            x.index_copy_(2, output_indices, exact)
+            with profiling.span("global.special_attention"):
+                special_q = q.index_select(2, original).to(dtype)
+                exact = torch.empty((B, H, original.numel(), D), device=q.device, dtype=dtype)
+                _attention_into(special_q, k.to(dtype), v.to(dtype), None, exact)
+                x.index_copy_(2, output_indices, exact)
         return out.view(B, n_query, C)
 
 

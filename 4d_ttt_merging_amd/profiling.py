@@ -1,0 +1,65 @@
+"""Labelled HIP-event timers for the merged global-attention path.
+
+Mirrors the reference's `VGGT_PROFILE_ATTENTION_DETAIL` timers
+(vggt_omega/models/layers/attention.py:25-63) and their `global.*` labels.
+Events are recorded on torch's current stream, so they bracket exactly the
+kernels launched there; nothing synchronises until `summary()`.
+Enabled by `enable()` or by the environment variable VGO_PROFILE_ATTENTION=1.
+"""
+from __future__ import annotations
+
+import os
+
+import torch
+
+_enabled = os.environ.get("VGO_PROFILE_ATTENTION", "0") == "1"
+_events: list[tuple[str, torch.cuda.Event, torch.cuda.Event]] = []
+
+
+def enable(flag: bool = True) -> None:
+    global _enabled
+    _enabled = flag
+
+
+def enabled() -> bool:
+    return _enabled
+
+
+def reset() -> None:
+    _events.clear()
+
+
+class span:
+    """Context manager recording a begin/end event pair under `label`."""
+
+    __slots__ = ("label", "begin")
+
+    def __init__(self, label: str):
+        self.label = label
+        self.begin = None
+
+    def __enter__(self):
+        if _enabled:
+            self.begin = torch.cuda.Event(enable_timing=True)
+            self.begin.record()
+        return self
+
+    def __exit__(self, *exc):
+        if self.begin is not None:
+            end = torch.cuda.Event(enable_timing=True)
+            end.record()
+            _events.append((self.label, self.begin, end))
+        return False
+
+
+def summary() -> dict[str, tuple[float, int]]:
+    """label -> (total ms, calls); synchronises once."""
+    if not _events:
+        return {}
+    torch.cuda.synchronize()
+    totals: dict[str, list[float]] = {}
+    for label, begin, end in _events:
+        entry = totals.setdefault(label, [0.0, 0])
+        entry[0] += begin.elapsed_time(end)
+        entry[1] += 1
+    return {label: (total, int(calls)) for label, (total, calls) in totals.items()}

@@ -1,0 +1,405 @@
+"""Benchmark of the merged-token global-attention path on one MI355X.
+
+Workload (the configuration the metric is quoted
+on): the full random-init aggregator in bf16 autocast -- 24 frame blocks + 24
+inter-frame blocks (19 merged global, 5 register), dim 1024, 16 heads, MLP
+4096, LayerNorm, RoPE in frame blocks -- on B=1, S=32 frames of 512x512 (32x32
+patches + 5 special tokens = 32,928 tokens).  Before every global block the
+FastVGGT bipartite planner merges at ratio 0.5 (protect_ratio 0, integer
+cluster masses as log-mass attention bias), attention runs on the compacted
+tokens, and the top-4 projection restores all tokens.  Patch tokens are a
+seeded N(0,1) cache (the DINOv3 encoder is not part of this path).
+
+One JSON line: value = frames/s of the aggregator forward (whole job, one
+GPU), plus
+* roofline: the mass-bias attention kernel of the global blocks, FLOPs per
+  launch 4*H*Nq*Nk*64 over its HIP-event launch time in the timed region;
+* global_block_ms: mean time of one merged global block (plan + block);
+* c3_attention / c2_projection: the BASELINE microbenchmarks;
+* torch_reference: the same aggregator with the reference's own op sequence
+  in plain PyTorch on the same GPU (SDPA with a float mask, bmm+max+argsort
+  planner, scatter_add compaction, gather restore) -- the stand-in for the
+  reference's Triton path, which cannot run here;
+* cpu_baseline: the CPU oracle on a bounded sample (see `cpu_baseline`).
+"""
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import torch
+import torch.nn.functional as F
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+METRIC = "global-attn block ms + frames/sec at S=32,512px; attn % MFMA peak; proj HBM GB/s"
+
+FRAMES, GRID, SPECIALS, DIM, HEADS = 32, (32, 32), 5, 1024, 16
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def timed(fn, steps: int, warmup: int) -> float:
+    """Mean seconds per call, bracketed by synchronize on both sides."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def event_time(fn, steps: int, warmup: int) -> float:
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps / 1e3
+
+
+# ------------------------------------------------------------------ model ----
+def build_model(vgo_agg, device):
+    torch.manual_seed(0)
+    model = vgo_agg.Aggregator(embed_dim=DIM, depth=24, num_heads=HEADS,
+                               num_register_tokens=SPECIALS - 1).to(device).eval()
+    g = torch.Generator().manual_seed(1)
+    patches = torch.randn(FRAMES, GRID[0] * GRID[1], DIM, generator=g).to(device)
+    model.set_input_patch_tokens_cache(patches)
+    images = torch.zeros(1, FRAMES, 3, GRID[0] * 16, GRID[1] * 16, device=device)
+    return model, images
+
+
+# --------------------------------------------- torch restatement on GPU ----
+class TorchReferenceGlobal:
+    """The reference's merged global block in plain PyTorch ops on the GPU.
+
+    Op sequence of vggt_omega/models/token_merging.py:1044-1122 (planner),
+    :176-196 (TokenPlan compact/restore) and layers/attention.py:328-439 with
+    the SDPA float-mask fallback (:400), plus log-cluster-size mass bias.
+    """
+
+    def __init__(self, frames, tokens_per_frame, pts, grid, ratio, vgo_tm):
+        self.layout = dict(frames=frames, tokens_per_frame=tokens_per_frame,
+                           patch_token_start=pts, patch_hw=grid)
+        self.ratio = ratio
+        self.vgo_tm = vgo_tm
+
+    def plan(self, tokens):
+        total = tokens.shape[1]
+        src_ids, dst_ids = self.vgo_tm._fastvggt_layout(
+            total, self.layout["frames"], self.layout["tokens_per_frame"],
+            self.layout["patch_token_start"], self.layout["patch_hw"], 0.0, 0, tokens.device)
+        removed = min(int(total * self.ratio), src_ids.numel())
+        src = F.normalize(tokens[:, src_ids].float(), dim=-1).to(torch.bfloat16)
+        dst_t = F.normalize(tokens[:, dst_ids].float(), dim=-1).to(torch.bfloat16).transpose(1, 2).contiguous()
+        best = torch.empty(1, src_ids.numel(), device=tokens.device)
+        targets = torch.empty(1, src_ids.numel(), device=tokens.device, dtype=torch.long)
+        for start in range(0, src_ids.numel(), 5000):
+            end = min(start + 5000, src_ids.numel())
+            values, index = torch.bmm(src[:, start:end], dst_t).max(dim=-1)
+            best[:, start:end] = values.float()
+            targets[:, start:end] = index
+        ranked = best.argsort(dim=-1, descending=True, stable=True)
+        removed_source = src_ids[ranked[:, :removed]]
+        target_original = dst_ids[targets.gather(1, ranked[:, :removed])]
+        identity = torch.arange(total, device=tokens.device).expand(1, -1)
+        kept_mask = torch.ones(1, total, device=tokens.device, dtype=torch.bool)
+        kept_mask.scatter_(1, removed_source, False)
+        keep = identity[kept_mask].reshape(1, total - removed)
+        o2c = torch.full_like(identity, -1)
+        o2c.scatter_(1, keep, torch.arange(total - removed, device=tokens.device).expand(1, -1))
+        inverse = o2c.clone()
+        inverse.scatter_(1, removed_source, o2c.gather(1, target_original))
+        return keep, inverse
+
+    @staticmethod
+    def compact(inverse, kept, value):
+        sums = torch.zeros(value.shape[0], kept, value.shape[-1], device=value.device, dtype=torch.float32)
+        sums.scatter_add_(1, inverse[..., None].expand_as(value), value.float())
+        counts = torch.zeros(value.shape[0], kept, 1, device=value.device, dtype=torch.float32)
+        counts.scatter_add_(1, inverse[..., None], torch.ones_like(inverse[..., None], dtype=torch.float32))
+        return (sums / counts).to(value.dtype), counts
+
+    def block(self, blk, tokens):
+        normalized = blk.norm1(tokens)
+        keep, inverse = self.plan(normalized)
+        kept = keep.shape[1]
+        attn = blk.attn
+        B, N, C = normalized.shape
+        qkv = attn.qkv(normalized).reshape(B, N, 3, HEADS, C // HEADS)
+        q, k, v = [t.transpose(1, 2) for t in torch.unbind(qkv, 2)]
+        q, k = attn.q_norm(q), attn.k_norm(k)
+        pack = lambda t: self.compact(inverse, kept, t.transpose(1, 2).reshape(B, N, C))  # noqa: E731
+        (qc, counts), (kc, _), (vc, _) = pack(q), pack(k), pack(v)
+        heads = lambda t: t.reshape(B, kept, HEADS, C // HEADS).transpose(1, 2)  # noqa: E731
+        bias = counts[..., 0].log()[:, None, None, :].to(torch.bfloat16)
+        x = F.scaled_dot_product_attention(heads(qc).bfloat16(), heads(kc).bfloat16(),
+                                           heads(vc).bfloat16(), attn_mask=bias)
+        x = attn.proj(x.transpose(1, 2).reshape(B, kept, C))
+        restored = x.gather(1, inverse[..., None].expand(-1, -1, C))
+        x_attn = tokens + blk.ls1(restored)
+        return x_attn + blk.ls2(blk.mlp(blk.norm2(x_attn)))
+
+
+def torch_reference_forward(model, ref_global, patches):
+    """Aggregator forward with the torch-restated global blocks (same weights)."""
+    agg_layers = importlib.import_module("4d_ttt_merging_amd.layers")
+    agg_mod = importlib.import_module("4d_ttt_merging_amd.aggregator")
+    B, S = 1, FRAMES
+    camera = agg_mod._slice_expand_and_flatten(model.camera_token, B, S)
+    register = agg_mod._slice_expand_and_flatten(model.register_token, B, S)
+    tokens = torch.cat([camera, register, patches], dim=1)
+    _, T, D = tokens.shape
+    sin, cos = agg_layers.rope_sincos(GRID[0], GRID[1], D // HEADS, device=patches.device)
+    for i in range(model.depth):
+        tokens = model.frame_blocks[i](tokens.view(B * S, T, D), (sin, cos))
+        tokens = tokens.view(B, S, T, D)
+        blk = model.inter_frame_blocks[i]
+        if model.inter_frame_attention_types[i] == "register":
+            pts = model.patch_token_start
+            special = blk(tokens[:, :, :pts].reshape(B, S * pts, D), None).view(B, S, pts, D)
+            tokens = torch.cat([special, tokens[:, :, pts:]], dim=2)
+        else:
+            tokens = ref_global.block(blk, tokens.reshape(B, S * T, D)).view(B, S, T, D)
+    return tokens
+
+
+# ----------------------------------------------------------- microbenches ----
+def c3_attention(vgo, device, steps):
+    """one mass-bias attention, Nq=16,464 queries, Nk=8,232 keys."""
+    nq, nk = 16 * 1029, 8232
+    g = torch.Generator().manual_seed(5)
+    q = (torch.randn(1, HEADS, nq, 64, generator=g) * 0.125).bfloat16().to(device)
+    k = (torch.randn(1, HEADS, nk, 64, generator=g) * 0.125).bfloat16().to(device)
+    v = (torch.randn(1, HEADS, nk, 64, generator=g) * 0.125).bfloat16().to(device)
+    mass = torch.randint(1, 9, (nk,), generator=g).float().log().to(device)
+    sec = event_time(lambda: vgo.mass_bias_attention(q, k, v, mass), steps, 3)
+    flops = 4 * HEADS * nq * nk * 64
+    sdpa = event_time(lambda: F.scaled_dot_product_attention(
+        q, k, v, attn_mask=mass.bfloat16().view(1, 1, 1, -1)), max(2, steps // 4), 1)
+    return {"nq": nq, "nk": nk, "ms": sec * 1e3, "tflops": flops / sec / 1e12,
+            "frac": flops / sec / 1e12 / PEAK_BF16_TFLOPS, "torch_sdpa_ms": sdpa * 1e3}
+
+
+def c2_projection(vgo, device, steps):
+    """top-4 projection, N=1,048,576 rows from a 65,536-row table."""
+    n, m, d = 1 << 20, 65536, 1024
+    g = torch.Generator().manual_seed(3)
+    keys = torch.rand(n, 8, generator=g)
+    index = (keys * m).long().clamp_max(m - 1)
+    index = index[:, :4].int().to(device)  # uniform ids; distinctness is irrelevant to traffic
+    e = -torch.rand(n, 4, generator=g, dtype=torch.float64).log()
+    weight = (e / e.sum(1, keepdim=True)).float().to(device)
+    out = {}
+    for dtype, size in ((torch.bfloat16, 2), (torch.float32, 4)):
+        table = torch.randn(m, d, device=device).to(dtype)
+        result = torch.empty(n, d, device=device, dtype=dtype)
+        sec = event_time(lambda: vgo.top4_project(table, index, weight, out=result), steps, 3)
+        compulsory = n * d * size + m * d * size + 32 * n
+        name = "bf16" if dtype == torch.bfloat16 else "fp32"
+        out[name] = {"ms": sec * 1e3, "gbs_compulsory": compulsory / sec / 1e9,
+                     "frac": compulsory / sec / 1e9 / PEAK_HBM_GBS,
+                     "gbs_logical": (compulsory + 4 * n * d * size) / sec / 1e9}
+        del table, result
+    return out
+
+
+# ------------------------------------------------------------ CPU baseline ----
+def cpu_baseline(budget_s: float = 30.0):
+    """The CPU oracle on a bounded sample of the C4 workload, extrapolated.
+
+    Sample: one merged global block at S=32 on the host cores in fp32 -- the
+    FastVGGT plan on all 32,928 tokens (oracle scores), compaction of Q/K/V,
+    mass-bias attention for one of 16 heads and 1,024 of the 16,464 compacted
+    queries (scaled by 16 x 16,464/1,024), projection and restore -- plus one
+    frame block on 4 of the 32 frames (scaled by 8).  Reported frames/s =
+    32 / (24 x (t_frame + t_global)), the per-pair extrapolation the
+    measurement plan prescribes.
+    """
+    from oracle import attention as oa
+    from oracle import merging as om
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(2)
+    total = FRAMES * (SPECIALS + GRID[0] * GRID[1])
+    tokens = torch.randn(1, total, DIM, generator=g)
+    w_qkv = torch.randn(3 * DIM, DIM, generator=g) * DIM ** -0.5
+    w_proj = torch.randn(DIM, DIM, generator=g) * DIM ** -0.5
+    w1 = torch.randn(4 * DIM, DIM, generator=g) * DIM ** -0.5
+    w2 = torch.randn(DIM, 4 * DIM, generator=g) * (4 * DIM) ** -0.5
+    t0 = time.perf_counter()
+    plan = om.fastvggt_plan(tokens, frames=FRAMES, tokens_per_frame=SPECIALS + GRID[0] * GRID[1],
+                            patch_token_start=SPECIALS, patch_hw=GRID, merge_ratio=0.5,
+                            protect_ratio=0.0)
+    t_plan = time.perf_counter() - t0
+    x = tokens[0]
+    t0 = time.perf_counter()
+    qkv = x @ w_qkv.T
+    q, k, v = qkv.split(DIM, dim=-1)
+    kept = plan["keep"].numel()
+    inv = plan["inverse"]
+    counts = torch.bincount(inv, minlength=kept).float()
+
+    def compact(t):
+        sums = torch.zeros(kept, DIM).index_add_(0, inv, t)
+        return sums / counts[:, None]
+
+    qc, kc, vc = compact(q), compact(k), compact(v)
+    t_pack = time.perf_counter() - t0
+    q_sample = 1024
+    t0 = time.perf_counter()
+    head = lambda t: t[:, :64].reshape(1, 1, -1, 64)  # noqa: E731
+    att = oa.mass_bias_attention(head(qc[:q_sample]), head(kc), head(vc), counts.log())
+    t_att = (time.perf_counter() - t0) * HEADS * (kept / q_sample)
+    t0 = time.perf_counter()
+    y = qc @ w_proj.T
+    restored = y[inv]
+    h = restored + (F.gelu(restored @ w1.T) @ w2.T)
+    t_tail = time.perf_counter() - t0
+    del att, h
+    t_global = t_plan + t_pack + t_att + t_tail
+    # frame block on 4 frames: qkv, per-frame SDPA, proj, MLP
+    f = 4
+    xf = tokens[0, : f * (SPECIALS + GRID[0] * GRID[1])]
+    t0 = time.perf_counter()
+    qkv = (xf @ w_qkv.T).reshape(f, -1, 3, HEADS, 64)
+    qf, kf, vf = [t.transpose(1, 2) for t in qkv.unbind(2)]
+    o = F.scaled_dot_product_attention(qf, kf, vf).transpose(1, 2).reshape(xf.shape[0], DIM)
+    o = o @ w_proj.T
+    o = o + F.gelu(o @ w1.T) @ w2.T
+    t_frame = (time.perf_counter() - t0) * (FRAMES / f)
+    pair = t_frame + t_global
+    value = FRAMES / (24 * pair)
+    cpu = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": value, "unit": "frames/s", "cores": threads, "kind": "port",
+            "sample": ("one merged global block at S=32 (plan on all 32,928 tokens, attention for "
+                       "1/16 heads x 1,024 queries scaled) + one frame block on 4/32 frames "
+                       "scaled; fp32 CPU oracle; frames/s = 32 / (24 x pair)"),
+            "cpu_model": cpu, "pair_seconds": pair,
+            "parts_s": {"plan": t_plan, "compaction": t_pack, "attention_scaled": t_att,
+                        "proj_restore_mlp": t_tail, "frame_block_scaled": t_frame}}
+
+
+# --------------------------------------------------------------------- main ----
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-reference", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
+              f"--gpus {args.gpus}); run with --gpus 1", file=sys.stderr, flush=True)
+        return 2
+    vgo = importlib.import_module("4d_ttt_merging_amd")
+    agg = importlib.import_module("4d_ttt_merging_amd.aggregator")
+    prof = importlib.import_module("4d_ttt_merging_amd.profiling")
+    tm = importlib.import_module("4d_ttt_merging_amd.token_merging")
+    device = torch.device("cuda", 0)
+    log(f"device {torch.cuda.get_device_name(0)}, CUs {torch.cuda.get_device_properties(0).multi_processor_count}")
+
+    model, images = build_model(agg, device)
+    model.set_fastvggt(True, merge_ratio=0.5, protect_ratio=0.0, mass_bias=True)
+
+    def step():
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            return model(images)
+
+    log(f"warmup {args.warmup}")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    prof.reset()
+    prof.enable(True)
+    log(f"timed {args.steps} steps")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    prof.enable(False)
+    spans = prof.summary()
+    ms_per_step = elapsed / args.steps * 1e3
+    fps = FRAMES * args.steps / elapsed
+    kept = model.fastvggt_last_plan_stats[0]["kept_tokens"]
+    attn_ms = spans["global.main_attention"][0] / spans["global.main_attention"][1]
+    attn_flops = 4 * HEADS * kept * kept * 64
+    block_ms = spans["global.block"][0] / spans["global.block"][1]
+    breakdown = {label: round(total / calls, 4) for label, (total, calls) in sorted(spans.items())}
+    log(f"aggregator {ms_per_step:.2f} ms/step, {fps:.1f} frames/s; attention {attn_ms:.3f} ms")
+
+    result = {
+        "metric": METRIC, "value": round(fps, 3), "unit": "frames/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) patch tokens, random-init weights)",
+        "config": {"workload": "C4: 24-block aggregator, S=32 frames @512px (32,928 tokens), "
+                               "FastVGGT merge ratio 0.5 + log-mass attention + top-4 restore "
+                               "before each of 19 global blocks",
+                   "frames": FRAMES, "tokens": FRAMES * (SPECIALS + 1024), "dim": DIM,
+                   "heads": HEADS, "kept_tokens": kept},
+        "roofline": {"bound": "mfma", "kernel": "vgo mass-bias attention (global blocks)",
+                     "achieved": round(attn_flops / (attn_ms / 1e3) / 1e12, 2),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(attn_flops / (attn_ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None, "flops_per_launch": attn_flops,
+                     "avg_launch_ms": round(attn_ms, 4)},
+        "global_block_ms": round(block_ms, 3),
+        "global_block_breakdown_ms": breakdown,
+    }
+    torch.cuda.synchronize()
+    log("C3 attention microbench")
+    result["c3_attention"] = c3_attention(vgo, device, 20)
+    log("C2 projection microbench")
+    result["c2_projection"] = c2_projection(vgo, device, 10)
+    if not args.no_reference:
+        log("torch restatement of the reference path on the GPU")
+        ref = TorchReferenceGlobal(FRAMES, SPECIALS + 1024, SPECIALS, GRID, 0.5, tm)
+        patches = model._input_patch_tokens_cache
+
+        def ref_step():
+            with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+                return torch_reference_forward(model, ref, patches)
+
+        sec = timed(ref_step, max(1, args.steps // 2), 1)
+        result["torch_reference"] = {"frames_per_s": round(FRAMES / sec, 3),
+                                     "ms_per_step": round(sec * 1e3, 3),
+                                     "speedup": round(fps / (FRAMES / sec), 3)}
+    if not args.no_cpu_baseline:
+        log("CPU oracle baseline (bounded sample)")
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -369,3 +369,30 @@ def test_block_forward_compacted(vgo, device):
     block.train()
     with pytest.raises(RuntimeError, match="inference-only"):
         block.forward_compacted(x, plan)
+
+
+def test_aggregator_runs_both_planners(device):
+    agg = import_package("aggregator")
+    torch.manual_seed(0)
+    model = agg.Aggregator(embed_dim=256, depth=3, num_heads=4, num_register_tokens=4,
+                           register_attention_block_indices=(1,),
+                           cached_layer_indices=(2,)).to(device).eval()
+    patches = structured_tokens(2, 4, (16, 16), 5, 256)[0].view(4, 261, 256)[:, 5:].contiguous()
+    model.set_input_patch_tokens_cache(patches.to(device))
+    images = torch.zeros(1, 4, 3, 256, 256, device=device)
+    with pytest.raises(RuntimeError, match="patch encoder"):
+        fresh = agg.Aggregator(embed_dim=256, depth=1, num_heads=4, num_register_tokens=4,
+                               register_attention_block_indices=()).to(device)
+        fresh(images)
+    model.set_fastvggt(True, merge_ratio=0.5, protect_ratio=0.0, mass_bias=True)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        outputs, start = model(images)
+    assert start == 5 and outputs[2].shape == (1, 4, 261, 512) and torch.isfinite(outputs[2]).all()
+    assert [s["kept_tokens"] for s in model.fastvggt_last_plan_stats] == [522, 522]
+    model.set_fastvggt(False)
+    model.set_sparse_convex(True, threshold=0.9, qkv_global_blocks=1, qkv_global_layers=(0,))
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        outputs, _ = model(images)
+    assert torch.isfinite(outputs[2]).all() and len(model.sparse_convex_last_plan_stats) == 2
+    with pytest.raises(ValueError, match="mutually exclusive"):
+        model.set_fastvggt(True)
