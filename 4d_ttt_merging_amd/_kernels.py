@@ -136,22 +136,31 @@ def token_layout(t: torch.Tensor) -> tuple[int, int]:
 def compact_into(x: torch.Tensor, out: torch.Tensor, *, base_rows: torch.Tensor | None,
                  offsets: torch.Tensor, segs_per_row: int, items: torch.Tensor | None,
                  item_shift: int, item_rows: torch.Tensor | None, weights: torch.Tensor | None,
-                 normalizer: torch.Tensor | None) -> torch.Tensor:
-    """Segmented weighted pooling; x/out are [N, C] or head-major [H, N, 64] views."""
+                 normalizer: torch.Tensor | None,
+                 layer_norm: tuple[torch.Tensor, torch.Tensor, float] | None = None) -> torch.Tensor:
+    """Segmented weighted pooling; x/out are [N, C] or head-major [H, N, 64] views.
+
+    `layer_norm` = (weight [64], bias [64], eps) normalises every gathered row per
+    64-channel head first; `out` may be narrower than `x` (one final rounding).
+    """
     lib = _lib.load()
     _lib.require_gpu(x, out)
-    if x.dtype != out.dtype:
-        raise ValueError("compaction input and output dtypes differ")
     xts, xhs = token_layout(x)
     ots, ohs = token_layout(out)
     n_rows_x = x.shape[0] if x.ndim == 2 else x.shape[1]
     rows = out.shape[0] if out.ndim == 2 else out.shape[1]
     dim = out.shape[1] if out.ndim == 2 else out.shape[0] * 64
+    ln_w = ln_b = None
+    ln_eps = 0.0
+    if layer_norm is not None:
+        ln_w, ln_b, ln_eps = layer_norm
+        ln_w = ln_w.detach().to(torch.float32).contiguous()
+        ln_b = ln_b.detach().to(torch.float32).contiguous()
     status = lib.vgo_compact(
         x.data_ptr(), xts, xhs, n_rows_x, _c(base_rows), offsets.data_ptr(), segs_per_row,
         _c(items), item_shift, _c(item_rows), _c(weights), 0 if weights is None else weights.numel(),
-        _c(normalizer), rows, dim, out.data_ptr(), ots, ohs, _lib.dtype_code(x.dtype),
-        _lib.stream_of(x))
+        _c(normalizer), rows, dim, _c(ln_w), _c(ln_b), float(ln_eps), out.data_ptr(), ots, ohs,
+        _lib.dtype_code(x.dtype), _lib.dtype_code(out.dtype), _lib.stream_of(x))
     _lib.check(status)
     return out
 
@@ -171,3 +180,42 @@ def restore_map(total: int, *, device: torch.device, keep: torch.Tensor | None =
         index_out.data_ptr(), weight_out.data_ptr(), torch.cuda.current_stream(device).cuda_stream)
     _lib.check(status)
     return index_out, weight_out
+
+
+def qkv_epilogue(qkv: torch.Tensor, heads: int, *, tokens_in: int, tokens_out: int | None = None,
+                 rows: torch.Tensor | None = None, q_norm=None, k_norm=None, eps: float = 1e-5,
+                 rope: tuple[torch.Tensor, torch.Tensor] | None = None, rope_prefix: int = 0,
+                 want=(True, True, True), out_dtype: torch.dtype | None = None):
+    """Split packed qkv rows [T, 3C] into head-major [S, H, tokens_out, 64] q/k/v.
+
+    q_norm / k_norm are (weight, bias) of the per-head LayerNorm(64); rope is
+    (sin, cos) [positions, 64] applied to tokens at position >= rope_prefix of
+    each tokens_in-long sequence.  Returns (q, k, v) with None for unwanted ones.
+    """
+    lib = _lib.load()
+    _lib.require_gpu(qkv, rows)
+    if qkv.ndim != 2 or qkv.stride(1) != 1:
+        raise ValueError("qkv_epilogue expects [rows, 3C] projection rows")
+    out_dtype = out_dtype or qkv.dtype
+    n_out = qkv.shape[0] if rows is None else rows.numel()
+    tokens_out = tokens_out or tokens_in
+    seqs = n_out // tokens_out
+    if rows is not None:
+        rows = rows.to(torch.int64).contiguous()
+    outs = [torch.empty((seqs, heads, tokens_out, 64), device=qkv.device, dtype=out_dtype) if w else None
+            for w in want]
+    f32 = lambda t: None if t is None else t.detach().to(torch.float32).contiguous()  # noqa: E731
+    qw, qb = (f32(q_norm[0]), f32(q_norm[1])) if q_norm is not None else (None, None)
+    kw, kb = (f32(k_norm[0]), f32(k_norm[1])) if k_norm is not None else (None, None)
+    rs = rc = None
+    rope_rows = 0
+    if rope is not None:
+        rs, rc = f32(rope[0]), f32(rope[1])
+        rope_rows = rs.shape[0]
+    status = lib.vgo_qkv_epilogue(
+        qkv.data_ptr(), qkv.stride(0), qkv.shape[0], _lib.dtype_code(qkv.dtype), _c(rows), n_out,
+        tokens_in, tokens_out, heads, _c(qw), _c(qb), _c(kw), _c(kb), float(eps), _c(rs), _c(rc),
+        rope_prefix, rope_rows, _c(outs[0]), _c(outs[1]), _c(outs[2]), _lib.dtype_code(out_dtype),
+        _lib.stream_of(qkv))
+    _lib.check(status)
+    return tuple(outs)

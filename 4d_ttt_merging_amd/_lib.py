@@ -66,7 +66,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ]),
     "vgo_compact": (_c_int, [
         _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_int, _c_p, _c_p, _c_i64, _c_p,
-        _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_int, _c_p,
+        _c_i64, _c_i64, _c_p, _c_p, _c_f32, _c_p, _c_i64, _c_i64, _c_int, _c_int, _c_p,
+    ]),
+    "vgo_qkv_epilogue": (_c_int, [
+        _c_p, _c_i64, _c_i64, _c_int, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p,
+        _c_p, _c_f32, _c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_int, _c_p,
     ]),
     "vgo_restore_map": (_c_int, [
         _c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p,

@@ -237,6 +237,129 @@ __global__ __launch_bounds__(256) void compact_kernel(
   }
 }
 
+// Vectorised compaction: lane l owns 16 contiguous channels [16 l, 16 l + 16)
+// of every 1024-channel slab (a head is four lanes), loaded and stored as
+// 16-byte vectors.  With ln_w != NULL every gathered row is first normalised
+// per 64-channel head (LayerNorm, eps, shared affine) in fp32 -- the q_norm /
+// k_norm of vggt_omega/models/layers/attention.py:337-339 fused into the pooling
+// -- and the output may be a narrower dtype than the input, so q/k go from the
+// bf16 projection to bf16 attention operands with one rounding.
+template <typename T>
+struct V16;
+template <>
+struct V16<bf16_t> {
+  typedef bf16x8 half;
+  static constexpr int kLoads = 2;
+};
+template <>
+struct V16<f16_t> {
+  typedef f16x8 half;
+  static constexpr int kLoads = 2;
+};
+template <>
+struct V16<float> {
+  typedef f32x4 half;
+  static constexpr int kLoads = 4;
+};
+
+template <typename T>
+__device__ __forceinline__ void v16_load(const T* p, float* v) {
+  typedef typename V16<T>::half V;
+  constexpr int kPer = 16 / V16<T>::kLoads;
+#pragma unroll
+  for (int i = 0; i < V16<T>::kLoads; ++i) {
+    const V x = *reinterpret_cast<const V*>(p + i * kPer);
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) v[i * kPer + j] = to_f32(x[j]);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void v16_store(T* p, const float* v) {
+  typedef typename V16<T>::half V;
+  constexpr int kPer = 16 / V16<T>::kLoads;
+#pragma unroll
+  for (int i = 0; i < V16<T>::kLoads; ++i) {
+    V x;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) x[j] = from_f32<T>(v[i * kPer + j]);
+    *reinterpret_cast<V*>(p + i * kPer) = x;
+  }
+}
+
+__device__ __forceinline__ void ln64_4lanes(float* v, const float* w, const float* b, int d0,
+                                            float eps) {
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) s += v[j];
+  s += __shfl_xor(s, 1);
+  s += __shfl_xor(s, 2);
+  const float mean = s / 64.0f;
+  float q = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const float d = v[j] - mean;
+    q = fmaf(d, d, q);
+  }
+  q += __shfl_xor(q, 1);
+  q += __shfl_xor(q, 2);
+  const float rstd = 1.0f / sqrtf(q / 64.0f + eps);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) v[j] = (v[j] - mean) * rstd * w[d0 + j] + b[d0 + j];
+}
+
+template <typename TI, typename TO>
+__global__ __launch_bounds__(256) void compact16_kernel(
+    const TI* __restrict__ x, int64_t xts, int64_t xhs, int64_t x_rows,
+    const int64_t* __restrict__ base_rows, const int32_t* __restrict__ offsets, int segs_per_row,
+    const uint32_t* __restrict__ items, int item_shift, const int64_t* __restrict__ item_rows,
+    const float* __restrict__ weights, int n_weights, const float* __restrict__ norm, int rows,
+    int dim, const float* __restrict__ ln_w, const float* __restrict__ ln_b, float ln_eps,
+    TO* __restrict__ out, int64_t ots, int64_t ohs) {
+  const int lane = threadIdx.x & 63;
+  const int k = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (k >= rows) return;
+  const int64_t b = base_rows ? base_rows[k] : -1;
+  const float nk = norm ? norm[k] : 1.0f;
+  for (int c0 = 0; c0 < dim; c0 += 1024) {
+    const int c = c0 + lane * 16;
+    const bool active = c < dim;  // whole 4-lane head groups are active together (dim % 64 == 0)
+    const int64_t xoff = static_cast<int64_t>(c >> 6) * xhs + (c & 63);
+    float acc[16], v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+    if (active && b >= 0 && b < x_rows) {
+      v16_load(x + b * xts + xoff, acc);
+      if (ln_w) ln64_4lanes(acc, ln_w, ln_b, c & 63, ln_eps);
+    }
+    for (int sgi = 0; sgi < segs_per_row; ++sgi) {
+      const int sb = offsets[k * segs_per_row + sgi], se = offsets[k * segs_per_row + sgi + 1];
+      if (sb >= se) continue;
+      float seg[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) seg[j] = 0.0f;
+      for (int q = sb; q < se; ++q) {
+        const uint32_t p = items[q];
+        const int64_t i = static_cast<int64_t>(p >> item_shift);
+        const int64_t row = item_rows ? item_rows[i] : i;
+        const float w = weights ? (static_cast<int>(p) < n_weights ? weights[p] : 0.0f) : 1.0f;
+        if (row < 0 || row >= x_rows || !active) continue;
+        v16_load(x + row * xts + xoff, v);
+        if (ln_w) ln64_4lanes(v, ln_w, ln_b, c & 63, ln_eps);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) seg[j] = seg[j] + v[j] * w;
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[j] = acc[j] + seg[j];
+    }
+    if (active) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[j] = acc[j] / nk;
+      v16_store(out + static_cast<int64_t>(k) * ots + static_cast<int64_t>(c >> 6) * ohs + (c & 63), acc);
+    }
+  }
+}
+
 // ---------------------------------------------------- restore map ----
 // Dense [N,4] (index, weight) rows for the top-4 projection:
 //   kept token keep[k]              -> (k,k,k,k), (1,0,0,0)
@@ -356,18 +479,42 @@ extern "C" int vgo_compact(const void* x, int64_t x_token_stride, int64_t x_head
                            const int64_t* base_rows, const int32_t* offsets, int64_t segs_per_row,
                            const uint32_t* items, int item_shift, const int64_t* item_rows,
                            const float* weights, int64_t n_weights, const float* normalizer,
-                           int64_t rows, int64_t dim, void* out, int64_t out_token_stride,
-                           int64_t out_head_stride, int dtype, void* stream) {
+                           int64_t rows, int64_t dim, const float* ln_weight, const float* ln_bias,
+                           float ln_eps, void* out, int64_t out_token_stride, int64_t out_head_stride,
+                           int in_dtype, int out_dtype, void* stream) {
   VGO_REQUIRE(rows >= 0 && dim >= 0 && segs_per_row >= 1, "compact: bad size");
   if (rows == 0 || dim == 0) return VGO_OK;
   VGO_REQUIRE(x && offsets && out, "compact: null pointer");
   VGO_REQUIRE(item_shift >= 0 && item_shift < 8, "compact: bad item shift");
   VGO_REQUIRE(rows < (1LL << 31) && dim < (1 << 20), "compact: size too large");
+  VGO_REQUIRE((ln_weight == nullptr) == (ln_bias == nullptr), "compact: LayerNorm weight and bias go together");
   hipStream_t s = as_stream(stream);
   const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
   const int r = static_cast<int>(rows), d = static_cast<int>(dim), sp = static_cast<int>(segs_per_row);
   const int nw = static_cast<int>(n_weights);
-  switch (dtype) {
+  const int64_t in_vec = in_dtype == VGO_F32 ? 4 : 8;
+  const int64_t out_vec = out_dtype == VGO_F32 ? 4 : 8;
+  const bool vec = dim % 64 == 0 && x_token_stride % in_vec == 0 && x_head_stride % in_vec == 0 &&
+                   out_token_stride % out_vec == 0 && out_head_stride % out_vec == 0 &&
+                   aligned(x, 16) && aligned(out, 16);
+  if (vec) {
+#define VGO_C16(TI, TO)                                                                            \
+  hipLaunchKernelGGL((compact16_kernel<TI, TO>), grid, dim3(256), 0, s, static_cast<const TI*>(x), \
+                     x_token_stride, x_head_stride, x_rows, base_rows, offsets, sp, items,         \
+                     item_shift, item_rows, weights, nw, normalizer, r, d, ln_weight, ln_bias,     \
+                     ln_eps, static_cast<TO*>(out), out_token_stride, out_head_stride);            \
+  return check_launch("compact")
+    if (in_dtype == VGO_F32 && out_dtype == VGO_F32) { VGO_C16(float, float); }
+    if (in_dtype == VGO_BF16 && out_dtype == VGO_BF16) { VGO_C16(bf16_t, bf16_t); }
+    if (in_dtype == VGO_F16 && out_dtype == VGO_F16) { VGO_C16(f16_t, f16_t); }
+    if (in_dtype == VGO_BF16 && out_dtype == VGO_F32) { VGO_C16(bf16_t, float); }
+    if (in_dtype == VGO_F32 && out_dtype == VGO_BF16) { VGO_C16(float, bf16_t); }
+#undef VGO_C16
+    return fail(VGO_EINVAL, "compact: unsupported dtype pair");
+  }
+  VGO_REQUIRE(in_dtype == out_dtype && ln_weight == nullptr,
+              "compact: LayerNorm and dtype conversion need 64-aligned channels and 16-byte rows");
+  switch (in_dtype) {
     case VGO_F32:
       hipLaunchKernelGGL((compact_kernel<float, 16>), grid, dim3(256), 0, s, static_cast<const float*>(x),
                          x_token_stride, x_head_stride, x_rows, base_rows, offsets, sp, items, item_shift,

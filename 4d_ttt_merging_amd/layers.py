@@ -31,7 +31,7 @@ import torch
 import torch.nn.functional as F
 from torch import Tensor, nn
 
-from . import profiling
+from . import _kernels, profiling
 from .mass_bias_attention import _attention_into
 
 
@@ -158,12 +158,38 @@ class SelfAttention(nn.Module):
         with profiling.span("global.update_restore"):
             return token_plan.restore(x)
 
+    # ---------------------------------------------------------------------
+    def _attention_dtype(self, qkv: Tensor) -> torch.dtype:
+        """dtype the attention runs in: the autocast dtype, as the reference's SDPA /
+        mass_bias_attention see it (mass_bias_attention.py:96-107), else qkv's."""
+        if torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") in (
+                torch.bfloat16, torch.float16):
+            return torch.get_autocast_dtype("cuda")
+        return qkv.dtype
+
+    def _norm_params(self):
+        if not self.use_qk_norm:
+            return None, None
+        return ((self.q_norm.weight, self.q_norm.bias, self.q_norm.eps),
+                (self.k_norm.weight, self.k_norm.bias, self.k_norm.eps))
+
+    def _fusable(self, qkv: Tensor, C: int, H: int) -> bool:
+        return (qkv.is_cuda and C == H * 64 and qkv.stride(-1) == 1
+                and qkv.dtype in (torch.bfloat16, torch.float16, torch.float32)
+                and (not self.use_qk_norm or (self.q_norm.eps == self.k_norm.eps)))
+
     def compute_attention(self, qkv: Tensor, attn_bias=None, rope=None, token_plan=None) -> Tensor:
         assert attn_bias is None
         B, N, _ = qkv.shape
         C = self.qkv.in_features
         H = self.num_heads
         D = C // H
+        if self._fusable(qkv, C, H):
+            if token_plan is not None and rope is None:
+                return self._merged_fused(qkv, token_plan, B, N, C, H)
+            if token_plan is None and self._attention_dtype(qkv) in (torch.bfloat16, torch.float16):
+                return self._dense_fused(qkv, rope, B, N, C, H)
+        # General path: the reference's op sequence (torch LayerNorm / RoPE / SDPA).
         q, k, v = torch.unbind(qkv.reshape(B, N, 3, H, D), 2)
         q, k, v = [t.transpose(1, 2) for t in (q, k, v)]
         with profiling.span("global.qk_norm_rope") if token_plan is not None else _null():
@@ -177,7 +203,94 @@ class SelfAttention(nn.Module):
             return x.transpose(1, 2).reshape(B, N, C)
         return self._merged_attention(q, k, v, token_plan, B, N, C, H, D)
 
+    def _dense_fused(self, qkv: Tensor, rope, B: int, N: int, C: int, H: int) -> Tensor:
+        """Frame/register attention: fused LayerNorm+RoPE epilogue, then the HIP kernel."""
+        dtype = self._attention_dtype(qkv)
+        qn, kn = self._norm_params()
+        rope_prefix = 0
+        if rope is not None:
+            rope_prefix = N - rope[0].shape[-2]
+            assert rope_prefix >= 0
+        rows = qkv.reshape(B * N, 3 * C)
+        q, k, v = _kernels.qkv_epilogue(
+            rows, H, tokens_in=N, q_norm=None if qn is None else qn[:2],
+            k_norm=None if kn is None else kn[:2], eps=qn[2] if qn is not None else 1e-5,
+            rope=rope, rope_prefix=rope_prefix, out_dtype=dtype)
+        out = torch.empty((B, N, H, 64), device=qkv.device, dtype=dtype)
+        _attention_into(q, k, v, None, out.permute(0, 2, 1, 3))
+        return out.view(B, N, C)
+
+    def _merged_fused(self, qkv: Tensor, plan, B: int, N: int, C: int, H: int) -> Tensor:
+        """Merged global attention straight from the packed projection.
+
+        q/k LayerNorm happens inside the compaction (every pooled row is normalised
+        first, as the reference normalises before packing, attention.py:337-375), and
+        the pooled operands are written once, in the attention dtype, head-major."""
+        dtype = self._attention_dtype(qkv)
+        qn, kn = self._norm_params()
+        preserve_queries = getattr(plan, "preserve_queries", False)
+        weighted = hasattr(plan, "compact_query_into")
+        kept = plan.kept_tokens
+        n_query = N if preserve_queries else getattr(plan, "query_kept_tokens", kept)
+        device = qkv.device
+        with profiling.span("global.qkv_compaction"):
+            k_c = torch.empty((B, H, kept, 64), device=device, dtype=dtype)
+            v_c = torch.empty((B, H, kept, 64), device=device, dtype=dtype)
+            q_c = None if preserve_queries else torch.empty((B, H, n_query, 64), device=device, dtype=dtype)
+            for b in range(B):
+                rows = qkv[b]
+                qs, ks, vs = rows[:, :C], rows[:, C:2 * C], rows[:, 2 * C:]
+                if weighted:
+                    if preserve_queries:
+                        plan.compact_key_into(ks, k_c[b], layer_norm=kn)
+                    else:
+                        plan.compact_query_into(qs, q_c[b], layer_norm=qn)
+                        plan.compact_into(ks, k_c[b], layer_norm=kn)
+                    plan.compact_into(vs, v_c[b])
+                else:
+                    merge = plan.pool_sources
+                    if not preserve_queries:
+                        plan.compact_into(qs, q_c[b], b=b, merge=merge, layer_norm=qn)
+                    plan.compact_into(ks, k_c[b], b=b, merge=merge, layer_norm=kn)
+                    plan.compact_into(vs, v_c[b], b=b, merge=merge)
+            if preserve_queries:
+                q_c = _kernels.qkv_epilogue(
+                    qkv.reshape(B * N, 3 * C), H, tokens_in=N,
+                    q_norm=None if qn is None else qn[:2], eps=qn[2] if qn is not None else 1e-5,
+                    want=(True, False, False), out_dtype=dtype)[0]
+        bias = None
+        log_mass = getattr(plan, "key_log_mass", None)
+        if log_mass is not None:
+            bias = log_mass.reshape(-1).to(dtype)
+            if bias.numel() != kept:
+                raise ValueError("log_key_mass length does not match key tokens")
+        out = torch.empty((B, n_query, H, 64), device=device, dtype=dtype)
+        x = out.permute(0, 2, 1, 3)  # [B, H, Nq, 64] view written in [B, Nq, H, 64] order
+        with profiling.span("global.main_attention"):
+            _attention_into(q_c, k_c, v_c, bias, x)
+        if getattr(plan, "dense_special_queries", False):
+            original = plan.special_query_original
+            output_indices = original if preserve_queries else plan.special_query_compact
+            if original is None or output_indices is None:
+                raise RuntimeError("dense-special attention plan has no special-token mapping")
+            if B != 1:
+                raise RuntimeError("dense special queries need the batch-1 plans they are built for")
+            with profiling.span("global.special_attention"):
+                rows = qkv.reshape(N, 3 * C)
+                _, dense_k, dense_v = _kernels.qkv_epilogue(
+                    rows, H, tokens_in=N, k_norm=None if kn is None else kn[:2],
+                    eps=kn[2] if kn is not None else 1e-5, want=(False, True, True), out_dtype=dtype)
+                special_q = _kernels.qkv_epilogue(
+                    rows, H, tokens_in=N, tokens_out=original.numel(), rows=original,
+                    q_norm=None if qn is None else qn[:2], eps=qn[2] if qn is not None else 1e-5,
+                    want=(True, False, False), out_dtype=dtype)[0]
+                exact = torch.empty_like(special_q)
+                _attention_into(special_q, dense_k, dense_v, None, exact)
+                x.index_copy_(2, output_indices, exact)
+        return out.view(B, n_query, C)
+
     def _merged_attention(self, q, k, v, plan, B, N, C, H, D) -> Tensor:
+        """Merged attention from already normalised [B, H, N, 64] q/k/v views (RoPE case)."""
         if D != 64:
             raise ValueError("the initial fused kernel supports head_dim=64 only")
         preserve_queries = getattr(plan, "preserve_queries", False)
@@ -187,31 +300,28 @@ class SelfAttention(nn.Module):
         def head_major(rows: int, dtype: torch.dtype) -> Tensor:
             return torch.empty((B, H, rows, D), device=q.device, dtype=dtype)
 
-        # Compaction between head-major views: no transpose copies.
-        compaction = profiling.span("global.qkv_compaction").__enter__()
-        k_c = head_major(kept, k.dtype)
-        v_c = head_major(kept, v.dtype)
-        q_c = q if preserve_queries else head_major(n_query, q.dtype)
-        for b in range(B):
-            if preserve_queries:
-                if hasattr(plan, "compact_key_into"):
-                    plan.compact_key_into(k[b], k_c[b])
+        with profiling.span("global.qkv_compaction"):
+            k_c = head_major(kept, k.dtype)
+            v_c = head_major(kept, v.dtype)
+            q_c = q if preserve_queries else head_major(n_query, q.dtype)
+            for b in range(B):
+                if preserve_queries:
+                    if hasattr(plan, "compact_key_into"):
+                        plan.compact_key_into(k[b], k_c[b])
+                    else:
+                        plan.compact_into(k[b], k_c[b], b=b, merge=plan.pool_sources)
                 else:
-                    plan.compact_into(k[b], k_c[b], b=b, merge=plan.pool_sources)
-            else:
+                    if hasattr(plan, "compact_query_into"):
+                        plan.compact_query_into(q[b], q_c[b])
+                        plan.compact_into(k[b], k_c[b])
+                    else:
+                        plan.compact_into(q[b], q_c[b], b=b, merge=plan.pool_sources)
+                        plan.compact_into(k[b], k_c[b], b=b, merge=plan.pool_sources)
                 if hasattr(plan, "compact_query_into"):
-                    plan.compact_query_into(q[b], q_c[b])
-                    plan.compact_into(k[b], k_c[b])
+                    plan.compact_into(v[b], v_c[b])
                 else:
-                    plan.compact_into(q[b], q_c[b], b=b, merge=plan.pool_sources)
-                    plan.compact_into(k[b], k_c[b], b=b, merge=plan.pool_sources)
-            if hasattr(plan, "compact_query_into"):
-                plan.compact_into(v[b], v_c[b])
-            else:
-                plan.compact_into(v[b], v_c[b], b=b, merge=plan.pool_sources)
-        compaction.__exit__(None, None, None)
+                    plan.compact_into(v[b], v_c[b], b=b, merge=plan.pool_sources)
 
-        # Attention in the autocast dtype (reference mass_bias_attention.py:96-107).
         dtype = q.dtype
         if (torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16
                 and q.dtype == torch.float32):
@@ -224,10 +334,9 @@ class SelfAttention(nn.Module):
             if bias.numel() != kept:
                 raise ValueError("log_key_mass length does not match key tokens")
         out = torch.empty((B, n_query, H, D), device=q.device, dtype=dtype)
-        x = out.permute(0, 2, 1, 3)  # [B, H, Nq, D] view written in [B, Nq, H, D] order
+        x = out.permute(0, 2, 1, 3)
         with profiling.span("global.main_attention"):
             _attention_into(qa, ka, va, bias, x)
-
         if getattr(plan, "dense_special_queries", False):
             original = plan.special_query_original
             output_indices = original if preserve_queries else plan.special_query_compact

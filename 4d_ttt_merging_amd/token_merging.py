@@ -46,6 +46,14 @@ def _as_rows(value: torch.Tensor) -> torch.Tensor:
     return value if value.stride(-1) == 1 else value.contiguous()
 
 
+def _zero_offsets(cache: dict, rows: int, device) -> torch.Tensor:
+    """All-empty CSR offsets [rows + 1]: makes vgo_compact a plain row gather."""
+    key = ("zero_offsets", rows)
+    if key not in cache:
+        cache[key] = torch.zeros(rows + 1, device=device, dtype=torch.int32)
+    return cache[key]
+
+
 @dataclass
 class _Csr:
     order: torch.Tensor      # int32 item ids grouped by segment (stable)
@@ -155,19 +163,21 @@ class TokenPlan:
         return out
 
     def compact_into(self, x: torch.Tensor, out: torch.Tensor, *, b: int = 0,
-                     merge: bool = True) -> torch.Tensor:
-        """compact() of one batch element between [N,C] / [H,N,64] views."""
+                     merge: bool = True, layer_norm=None) -> torch.Tensor:
+        """compact() of one batch element between [N,C] / [H,N,64] views.
+
+        `layer_norm` = (weight, bias, eps) applies the per-head LayerNorm(64)
+        to every member row before pooling (the q/k norm of the attention)."""
         if not merge and self.pool_mask is None:
-            zeros = self._derived.setdefault(
-                "gather_offsets",
-                torch.zeros(self.kept_tokens + 1, device=x.device, dtype=torch.int32))
             return _kernels.compact_into(x, out, base_rows=self.keep[b].contiguous(),
-                                         offsets=zeros, segs_per_row=1, items=None, item_shift=0,
-                                         item_rows=None, weights=None, normalizer=None)
+                                         offsets=_zero_offsets(self._derived, self.kept_tokens, x.device),
+                                         segs_per_row=1, items=None, item_shift=0, item_rows=None,
+                                         weights=None, normalizer=None, layer_norm=layer_norm)
         csr, counts = self._cluster_csr(b)
         return _kernels.compact_into(x, out, base_rows=None, offsets=csr.offsets, segs_per_row=1,
                                      items=csr.order, item_shift=0, item_rows=None,
-                                     weights=self._contribution(b), normalizer=counts)
+                                     weights=self._contribution(b), normalizer=counts,
+                                     layer_norm=layer_norm)
 
     def restore(self, value: torch.Tensor) -> torch.Tensor:
         if self.kept_tokens == self.original_tokens:
@@ -249,26 +259,28 @@ class WeightedBilinearTokenPlan:
             self._derived[name] = tensor.reshape(-1).to(dtype).contiguous()
         return self._derived[name]
 
-    def _gather_into(self, rows: torch.Tensor, x: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
-        zeros = self._derived.setdefault(
-            ("gather_offsets", rows.numel()),
-            torch.zeros(rows.numel() + 1, device=x.device, dtype=torch.int32))
-        return _kernels.compact_into(x, out, base_rows=rows, offsets=zeros, segs_per_row=1,
-                                     items=None, item_shift=0, item_rows=None, weights=None,
-                                     normalizer=None)
+    def _gather_into(self, rows: torch.Tensor, x: torch.Tensor, out: torch.Tensor,
+                     layer_norm=None) -> torch.Tensor:
+        return _kernels.compact_into(x, out, base_rows=rows,
+                                     offsets=_zero_offsets(self._derived, rows.numel(), x.device),
+                                     segs_per_row=1, items=None, item_shift=0, item_rows=None,
+                                     weights=None, normalizer=None, layer_norm=layer_norm)
 
-    def compact_into(self, x: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
-        """compact() between [N,C] / [H,N,64] views of the single batch element."""
+    def compact_into(self, x: torch.Tensor, out: torch.Tensor, *, layer_norm=None) -> torch.Tensor:
+        """compact() between [N,C] / [H,N,64] views of the single batch element.
+
+        `layer_norm` = (weight, bias, eps) normalises every gathered row per
+        64-channel head before pooling (the q/k norm of the attention)."""
         keep = self._flat("keep", self.keep, torch.int64)
         if self.source_original.shape[1] == 0 or not self.pool_source_content:
-            return self._gather_into(keep, x, out)
+            return self._gather_into(keep, x, out, layer_norm)
         return _kernels.compact_into(
             x, out, base_rows=keep, offsets=self._csr.offsets,
             segs_per_row=self.source_parent_compact.shape[-1], items=self._csr.order,
             item_shift=2 if self.source_parent_compact.shape[-1] == 4 else 0,
             item_rows=self._flat("source", self.source_original, torch.int64),
             weights=self._flat("pool_w", self.source_pool_weights, torch.float32),
-            normalizer=self._flat("norm", self.normalizer, torch.float32))
+            normalizer=self._flat("norm", self.normalizer, torch.float32), layer_norm=layer_norm)
 
     def compact(self, value: torch.Tensor, *, merge: bool = True) -> torch.Tensor:
         """Pool source Q/K/V mass into its four retained bilinear parents."""
@@ -282,10 +294,10 @@ class WeightedBilinearTokenPlan:
             self.compact_into(value[b], out[b])
         return out
 
-    def compact_key_into(self, x: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    def compact_key_into(self, x: torch.Tensor, out: torch.Tensor, *, layer_norm=None) -> torch.Tensor:
         if not self.preserve_destination_keys:
-            return self.compact_into(x, out)
-        return self._gather_into(self._flat("keep", self.keep, torch.int64), x, out)
+            return self.compact_into(x, out, layer_norm=layer_norm)
+        return self._gather_into(self._flat("keep", self.keep, torch.int64), x, out, layer_norm)
 
     def compact_key(self, value: torch.Tensor) -> torch.Tensor:
         """Keep physical keys unchanged for the Q-preserving KV-only path."""
@@ -298,10 +310,11 @@ class WeightedBilinearTokenPlan:
             self.compact_key_into(value[b], out[b])
         return out
 
-    def compact_query_into(self, x: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    def compact_query_into(self, x: torch.Tensor, out: torch.Tensor, *, layer_norm=None) -> torch.Tensor:
         if self.query_keep is None:
-            return self.compact_into(x, out)
-        return self._gather_into(self._flat("qkeep", self.query_keep, torch.int64), x, out)
+            return self.compact_into(x, out, layer_norm=layer_norm)
+        return self._gather_into(self._flat("qkeep", self.query_keep, torch.int64), x, out,
+                                 layer_norm)
 
     def compact_query(self, value: torch.Tensor) -> torch.Tensor:
         if self.query_keep is None:

@@ -171,11 +171,15 @@ int vgo_segment_mass(const int32_t* offsets, int64_t segs_per_row, const uint32_
                      float* mass, float* log_mass, void* stream);
 
 /*
- * Plan compaction (Q/K/V pooling): out[k] = (x[base_rows[k]] + sum_c sum_{p in
- * segment (k,c)} x[item_rows[p >> item_shift]] * weights[p]) / normalizer[k] in
- * fp32, cast to dtype.  Channel c of token t lives at t*token_stride +
- * (c/64)*head_stride + c%64 for input and output.  Replaces
- * WeightedBilinearTokenPlan.compact / compact_key / compact_query and
+ * Plan compaction (Q/K/V pooling): out[k] = (f(x[base_rows[k]]) + sum_c sum_{p in
+ * segment (k,c)} f(x[item_rows[p >> item_shift]]) * weights[p]) / normalizer[k] in
+ * fp32, rounded once to out_dtype.  f is the identity, or with ln_weight != NULL a
+ * per-head LayerNorm over 64 channels (eps ln_eps, shared affine) -- the q_norm /
+ * k_norm of vggt_omega/models/layers/attention.py:337-339 fused into the pooling.
+ * Channel c of token t lives at t*token_stride + (c/64)*head_stride + c%64 for
+ * input and output, so the packed qkv projection ([N, 3C] rows) is read and
+ * head-major [H, K, 64] attention operands are written without copies.
+ * Replaces WeightedBilinearTokenPlan.compact / compact_key / compact_query and
  * TokenPlan.compact (vggt_omega/models/token_merging.py:343-385, 176-191), whose
  * caller is vggt_omega/models/layers/attention.py:346-375.
  */
@@ -183,8 +187,27 @@ int vgo_compact(const void* x, int64_t x_token_stride, int64_t x_head_stride, in
                 const int64_t* base_rows, const int32_t* offsets, int64_t segs_per_row,
                 const uint32_t* items, int item_shift, const int64_t* item_rows,
                 const float* weights, int64_t n_weights, const float* normalizer, int64_t rows,
-                int64_t dim, void* out, int64_t out_token_stride, int64_t out_head_stride,
-                int dtype, void* stream);
+                int64_t dim, const float* ln_weight, const float* ln_bias, float ln_eps, void* out,
+                int64_t out_token_stride, int64_t out_head_stride, int in_dtype, int out_dtype,
+                void* stream);
+
+/*
+ * Fused QKV epilogue: from packed projection rows qkv[src] = [q | k | v] (each
+ * heads*64 channels), write head-major q/k/v [seq, heads, tokens_out, 64] for
+ * output rows r (src = rows ? rows[r] : r; seq = r / tokens_out), applying the
+ * per-head LayerNorm(64) to q and k (when weights are given) and axial RoPE
+ * (when rope_sin/cos are given) to tokens whose position within their
+ * tokens_in-long sequence is >= rope_prefix, in fp32, one rounding to
+ * out_dtype.  Any of q_out/k_out/v_out may be NULL.  Replaces the reshape,
+ * q_norm/k_norm, apply_rope and transposes of
+ * vggt_omega/models/layers/attention.py:243-262, 334-341.
+ */
+int vgo_qkv_epilogue(const void* qkv, int64_t row_stride, int64_t n_in_rows, int in_dtype,
+                     const int64_t* rows, int64_t n_out, int64_t tokens_in, int64_t tokens_out,
+                     int64_t heads, const float* q_weight, const float* q_bias,
+                     const float* k_weight, const float* k_bias, float eps, const float* rope_sin,
+                     const float* rope_cos, int64_t rope_prefix, int64_t rope_rows, void* q_out,
+                     void* k_out, void* v_out, int out_dtype, void* stream);
 
 /*
  * Dense [total, 4] restore map for vgo_top4_project: kept token keep[k] ->

@@ -396,3 +396,89 @@ def test_aggregator_runs_both_planners(device):
     assert torch.isfinite(outputs[2]).all() and len(model.sparse_convex_last_plan_stats) == 2
     with pytest.raises(ValueError, match="mutually exclusive"):
         model.set_fastvggt(True)
+
+
+# ------------------------------------------------------- fused epilogue ----
+def _ref_epilogue(qkv, heads, tokens, qn, kn, sin, cos, prefix):
+    """Reference op sequence (attention.py:334-341, 243-262) in fp32 on the CPU."""
+    n, c3 = qkv.shape
+    c = c3 // 3
+    x = qkv.float().view(n // tokens, tokens, 3, heads, 64)
+    q, k, v = x[:, :, 0], x[:, :, 1], x[:, :, 2]  # [S, T, H, 64]
+    q = F.layer_norm(q, (64,), qn[0], qn[1], 1e-5)
+    k = F.layer_norm(k, (64,), kn[0], kn[1], 1e-5)
+
+    def rope(t):
+        body = t[:, prefix:]
+        half = torch.cat([-body[..., 32:], body[..., :32]], dim=-1)
+        return torch.cat([t[:, :prefix], body * cos[:, None] + half * sin[:, None]], dim=1)
+
+    if sin is not None:
+        q, k = rope(q), rope(k)
+    hm = lambda t: t.permute(0, 2, 1, 3)  # noqa: E731
+    return hm(q), hm(k), hm(v)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_qkv_epilogue_layer_norm_and_rope(kern, device, dtype):
+    layers = import_package("layers")
+    g = torch.Generator().manual_seed(21)
+    heads, tokens, seqs = 4, 261, 3
+    qkv = torch.randn(seqs * tokens, 3 * heads * 64, generator=g).to(dtype)
+    qn = (1 + 0.1 * torch.randn(64, generator=g), 0.1 * torch.randn(64, generator=g))
+    kn = (1 + 0.1 * torch.randn(64, generator=g), 0.1 * torch.randn(64, generator=g))
+    sin, cos = layers.rope_sincos(16, 16, 64)
+    q, k, v = kern.qkv_epilogue(qkv.to(device), heads, tokens_in=tokens,
+                                q_norm=(qn[0].to(device), qn[1].to(device)),
+                                k_norm=(kn[0].to(device), kn[1].to(device)),
+                                rope=(sin.to(device), cos.to(device)), rope_prefix=5, out_dtype=dtype)
+    rq, rk, rv = _ref_epilogue(qkv, heads, tokens, qn, kn, sin, cos, 5)
+    tol = 1e-5 if dtype == torch.float32 else 8e-3
+    assert_close(q.cpu(), rq.to(dtype), rtol=tol, what="epilogue q")
+    assert_close(k.cpu(), rk.to(dtype), rtol=tol, what="epilogue k")
+    assert torch.equal(v.cpu(), rv.to(dtype))
+    # row-list variant (special queries) and no-RoPE variant
+    rows = torch.tensor([0, 5, 261, 700])
+    (qs,) = kern.qkv_epilogue(qkv.to(device), heads, tokens_in=tokens, tokens_out=4, rows=rows.to(device),
+                              q_norm=(qn[0].to(device), qn[1].to(device)), want=(True, False, False),
+                              out_dtype=dtype)[:1]
+    flat_ref = F.layer_norm(qkv.float().view(-1, 3, heads, 64)[:, 0], (64,), qn[0], qn[1], 1e-5)
+    assert_close(qs[0].cpu(), flat_ref[rows].permute(1, 0, 2).to(dtype), rtol=tol, what="row list")
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_compaction_with_fused_layer_norm(vgo, device, out_dtype):
+    keep, src, parent, w = _random_weighted_plan(31, 2000, 600, 1400)
+    mass = om.deterministic_weighted_normalizer(parent[None], w[None], 600)
+    plan = vgo.WeightedBilinearTokenPlan(
+        keep=keep[None].to(device), source_original=src[None].to(device),
+        source_parent_compact=parent[None].to(device), source_pool_weights=w[None].to(device),
+        source_restore_weights=w[None].to(device), original_tokens=2000, normalizer=mass.to(device))
+    g = torch.Generator().manual_seed(32)
+    qkv = torch.randn(2000, 3 * 1024, generator=g).bfloat16()
+    lw, lb = 1 + 0.1 * torch.randn(64, generator=g), 0.1 * torch.randn(64, generator=g)
+    qkv_d = qkv.to(device)
+    out = torch.empty((16, 600, 64), device=device, dtype=out_dtype)
+    plan.compact_into(qkv_d[:, :1024], out, layer_norm=(lw.to(device), lb.to(device), 1e-5))
+    normed = F.layer_norm(qkv[:, :1024].float().view(2000, 16, 64), (64,), lw, lb, 1e-5).view(2000, 1024)
+    ref = om.weighted_compact(keep, src, parent, w, mass, normed)
+    got = out.transpose(0, 1).reshape(600, 1024).cpu()
+    assert_close(got, ref.to(out_dtype), rtol=1e-5 if out_dtype == torch.float32 else 8e-3,
+                 what="LN-fused compaction")
+
+
+def test_dense_fused_attention_matches_reference_ops(vgo, device):
+    layers = import_package("layers")
+    torch.manual_seed(3)
+    layer = vgo.SelfAttention(256, num_heads=4, qkv_bias=True, mask_k_bias=True,
+                              use_qk_norm=True).eval().to(device)
+    with torch.no_grad():
+        layer.q_norm.weight.normal_(1.0, 0.1)
+        layer.k_norm.bias.normal_(0.0, 0.1)
+    x = structured_tokens(4, 3, (16, 16), 5, 256)[0].view(3, 261, 256).to(device)
+    sin, cos = layers.rope_sincos(16, 16, 64, device=device)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        fused = layer(x, rope=(sin, cos))
+        layer._fusable = lambda *a: False  # reference op sequence: torch LN, RoPE, SDPA
+        general = layer(x, rope=(sin, cos))
+    assert_close(fused.float().cpu(), general.float().cpu(), torch.bfloat16, what="frame attention")
