@@ -34,6 +34,10 @@ COMMON_FLAGS = [
 ]
 
 
+# Per-source additions (file name -> extra hipcc flags).
+SOURCE_FLAGS: dict[str, list[str]] = {}
+
+
 def hipcc() -> str:
     rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
     candidate = Path(rocm) / "bin" / "hipcc"
@@ -47,7 +51,8 @@ def hipcc() -> str:
 
 def _compile(source: Path) -> Path:
     obj = BUILD_DIR / (source.stem + ".o")
-    cmd = [hipcc(), *COMMON_FLAGS, "-c", str(source), "-o", str(obj)]
+    cmd = [hipcc(), *COMMON_FLAGS, *SOURCE_FLAGS.get(source.name, []), "-c", str(source), "-o",
+           str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {source.name}:\n{proc.stderr}")

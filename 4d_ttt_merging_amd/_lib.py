@@ -39,6 +39,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
         _i64x3, _i64x3, _i64x3, _i64x3, _c_int, _c_p,
     ]),
+    "vgo_mass_bias_attn_workspace": (_c_int, [
+        _c_i64, _c_i64, _c_i64, _c_i64, _c_int, ctypes.POINTER(_c_size),
+    ]),
+    "vgo_mass_bias_attn_fwd_ws": (_c_int, [
+        _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+        _i64x3, _i64x3, _i64x3, _i64x3, _c_int, _c_p, _c_size, _c_p,
+    ]),
     "vgo_top4_project": (_c_int, [
         _c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_p,
     ]),

@@ -5,14 +5,18 @@
 // vggt_omega/models/layers/attention.py:406-422.
 //
 // bf16 / f16 path (the autocast path of the reference):
-//  * A work-group of 4 waves owns 4*QB*32 queries of one (batch, head); each
-//    wave keeps its Q rows in registers as MFMA B operands.
-//  * Keys stream through LDS in tiles of 64: K row-major, V transposed (V^T, d
-//    rows) so both feed v_mfma_f32_32x32x16 as A operands with one 16-byte LDS
-//    read per lane.
+//  * A task is 256 queries of one (batch, head): 4 waves x 64 queries, each
+//    wave holding its Q rows in registers as MFMA B operands (2 x 32 columns).
+//  * Keys stream through LDS in tiles of 64, double-buffered: the next tile's
+//    K/V rows are loaded into registers while the current tile is computed,
+//    then stored to the other buffer -- one barrier per tile.  K is stored
+//    row-major, V transposed (V^T, one row per dim) so both feed
+//    v_mfma_f32_32x32x16 as A operands with one 16-byte LDS read per lane;
+//    rows are 128 B with XOR-permuted 16-byte chunks (no padding, no bank
+//    conflicts for the reads or for the transposing V stores).
 //  * Scores are computed transposed, S^T = K' Q'^T, so a lane owns one query
 //    and 16 keys of every 32-key sub-tile: the row max/sum of the online
-//    softmax stay in registers except for one exchange with lane l^32, and the
+//    softmax stay in registers except for one v_permlane32_swap, and the
 //    exponentiated scores are already laid out as the B operand of O^T = V^T P^T.
 //  * The per-key bias rides in the MFMA: a fifth k-step multiplies a Q-side
 //    column of ones with a K-side column holding 8*log(m) (exact in bf16/f16),
@@ -20,19 +24,31 @@
 //    rounds log(m) to the input dtype first (mass_bias_attention.py:109); so do
 //    we.  P is rounded to the input dtype before P.V (reference :74) and the row
 //    sum is accumulated from those rounded values with v_dot2 (fp32 accumulate).
+//  * The O / row-sum rescale runs only when some lane's running max moved
+//    (otherwise its factor is exactly 1, so skipping it changes no bit).
+//  * Scheduling: the (task, key tile) units of a call are split evenly over
+//    the work-groups the chip holds at once (stream-K); tasks cut between two
+//    work-groups are finished by attn_merge_kernel from fp32 partial states.
 // fp32 path: exact fp32 arithmetic, one query row per lane, K/V tiles in LDS.
+#include <algorithm>
+#include <type_traits>
+
 #include "vgo_common.h"
 
 namespace vgo {
 namespace {
 
 constexpr int kD = 64;
-constexpr int kBN = 64;                 // keys per LDS tile
-constexpr int kWavesA = 4;              // waves per work-group
-constexpr int kPad = 8;                 // elements of padding per LDS row
-constexpr int kKRow = kD + kPad;        // K tile: [kBN keys][kKRow]
-constexpr int kVRow = kBN + kPad;       // V^T tile: [kD dims][kVRow]
+constexpr int kBN = 64;                      // keys per LDS tile
+constexpr int kWaves = 4;                    // waves per work-group
+constexpr int kQB = 2;                       // 32-query MFMA column blocks per wave
+constexpr int kQPerWave = 32 * kQB;          // 64
+constexpr int kQBlock = kWaves * kQPerWave;  // 256 queries per work-group task
+constexpr int kTileElems = kBN * kD;         // one K (or V^T) tile, elements
 constexpr float kLog2e = 1.4426950408889634f;
+// Partial state of one stream-K segment: O (fp32, unnormalised) then the
+// running max and sum of every query of the task.
+constexpr int kPartialFloats = kQBlock * kD + 2 * kQBlock;
 
 template <typename T>
 struct Mma;
@@ -40,6 +56,7 @@ template <>
 struct Mma<bf16_t> {
   typedef bf16x8 op8;
   typedef bf16x2 op2;
+  typedef bf16x4 op4;
   static __device__ __forceinline__ f32x16 mma(op8 a, op8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
@@ -51,6 +68,7 @@ template <>
 struct Mma<f16_t> {
   typedef f16x8 op8;
   typedef f16x2 op2;
+  typedef f16x4 op4;
   static __device__ __forceinline__ f32x16 mma(op8 a, op8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
@@ -59,7 +77,23 @@ struct Mma<f16_t> {
   }
 };
 
-__device__ __forceinline__ float other_half(float x) { return __shfl_xor(x, 32); }
+// (x[l], x[l ^ 32]) for every lane l in one VALU op: v_permlane32_swap
+// exchanges the upper half of one register with the lower half of another.
+__device__ __forceinline__ void both_halves(float x, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float half_max(float x) {
+  float a, b;
+  both_halves(x, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float half_sum(float x) {
+  float a, b;
+  both_halves(x, a, b);
+  return a + b;  // identical in both halves: IEEE addition commutes
+}
 
 // Position of key `kk` (0..63) inside a V^T row.  Within every 16-key group the
 // two middle quads are swapped, which is the order in which S^T's accumulator
@@ -68,55 +102,123 @@ __device__ __forceinline__ int vt_pos(int kk) {
   return (kk & ~12) | ((kk & 4) << 1) | ((kk & 8) >> 1);
 }
 
-template <typename T, int QB>
-__global__ __launch_bounds__(kWavesA * 64, 2) void attn_mfma_kernel(
-    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
-    const T* __restrict__ bias, T* __restrict__ out, int heads, int nq, int nk, int n_qblocks,
-    int64_t qsb, int64_t qsh, int64_t qsn, int64_t ksb, int64_t ksh, int64_t ksn, int64_t vsb,
-    int64_t vsh, int64_t vsn, int64_t osb, int64_t osh, int64_t osn, float c) {
+// LDS tiles are 64 rows x 64 elements (128 B) with no padding; the eight
+// 16-byte chunks of a row are XOR-permuted by swz(row), so that eight
+// consecutive rows read at one logical chunk, and eight chunks of eight rows
+// written by one store, all fall in distinct banks.
+__device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 7); }
+
+template <typename T>
+struct AttnArgs {
+  const T* q;
+  const T* k;
+  const T* v;
+  const T* bias;
+  T* out;
+  float* partial;  // stream-K partial states, 2 per work-group (may be null)
+  int heads, nq, nk, n_qblocks, ntiles;
+  int64_t units, groups;  // stream-K: `units` (task, tile) pairs over `groups` work-groups
+  int64_t qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn, osb, osh, osn;
+  float c;  // log2(e) / 8: S'' -> exp2 domain
+};
+
+// First unit of work-group w under the static stream-K partition.
+__host__ __device__ __forceinline__ int64_t sk_begin(int64_t w, int64_t units, int64_t groups) {
+  return w * units / groups;
+}
+// Work-group whose range holds unit u.
+__host__ __device__ __forceinline__ int64_t sk_owner(int64_t u, int64_t units, int64_t groups) {
+  return ((u + 1) * groups - 1) / units;
+}
+
+template <typename T>
+__device__ __forceinline__ void attn_segment(const AttnArgs<T>& a, T* k_lds, T* vt_lds, T* b_lds,
+                                             int bh, int qblk, int tile0, int tile1, float* partial) {
   typedef typename Mma<T>::op8 op8;
   typedef typename Mma<T>::op2 op2;
-  constexpr int kQPerWave = QB * 32;
-  constexpr int kQPerBlock = kWavesA * kQPerWave;
-  __shared__ __attribute__((aligned(16))) T k_lds[kBN * kKRow];
-  __shared__ __attribute__((aligned(16))) T vt_lds[kD * kVRow];
-  __shared__ __attribute__((aligned(16))) T b_lds[kBN];
-
-  const int task = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = task / n_qblocks;
-  const int qblk = task - bh * n_qblocks;
-  const int b = bh / heads;
-  const int h = bh - b * heads;
-
+  typedef typename Mma<T>::op4 op4;
+  const int b = bh / a.heads;
+  const int h = bh - b * a.heads;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int l32 = lane & 31;
   const int hh = lane >> 5;
-  const int qw0 = qblk * kQPerBlock + wave * kQPerWave;
+  const int qw0 = qblk * kQBlock + wave * kQPerWave;
 
-  const T* qb_ptr = q + b * qsb + h * qsh;
-  const T* kb_ptr = k + b * ksb + h * ksh;
-  const T* vb_ptr = v + b * vsb + h * vsh;
+  const T* qb_ptr = a.q + b * a.qsb + h * a.qsh;
+  const T* kb_ptr = a.k + b * a.ksb + h * a.ksh;
+  const T* vb_ptr = a.v + b * a.vsb + h * a.vsh;
 
-  const op8 zero8 = {};
-  op8 qreg[QB][4];
+  // Q rows as MFMA B operands (rows past n_query read a valid row; never stored).
+  op8 qreg[kQB][4];
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const int row = qw0 + qb * 32 + l32;
+  for (int qb = 0; qb < kQB; ++qb) {
+    const int row = min(qw0 + qb * 32 + l32, a.nq - 1);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      qreg[qb][t] = row < nq ? *reinterpret_cast<const op8*>(qb_ptr + row * qsn + 16 * t + 8 * hh)
-                             : zero8;
-    }
+    for (int t = 0; t < 4; ++t)
+      qreg[qb][t] = *reinterpret_cast<const op8*>(qb_ptr + row * a.qsn + 16 * t + 8 * hh);
   }
+  const op8 zero8 = {};
   op8 qone = zero8;
-  if (hh == 0) qone[0] = static_cast<T>(1.0f);
+  qone[0] = hh == 0 ? static_cast<T>(1.0f) : static_cast<T>(0.0f);
+  const op2 ones2 = {static_cast<T>(1.0f), static_cast<T>(1.0f)};
 
-  float m[QB], lsum[QB];
-  f32x16 o[QB][2];
+  // Per-lane LDS read offsets (elements) of logical chunk pair t of row l32;
+  // row l32 + 32 uses off[t ^ 2] (swz flips bit 2 of the chunk there).
+  int off[4];
+  {
+    const int s0 = swz(l32);
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
+    for (int t = 0; t < 4; ++t) off[t] = l32 * kD + (((2 * t + hh) ^ s0) << 3);
+  }
+
+  // Staging roles.  K: rows st and st+32, chunk sc.  V: keys 2st, 2st+1, dims 8sc..8sc+7.
+  const int st = tid >> 3;
+  const int sc = tid & 7;
+  const int kw0 = st * kD + ((sc ^ swz(st)) << 3);
+  const int kw1 = (st + 32) * kD + ((sc ^ swz(st + 32)) << 3);
+  const int vpos = vt_pos(2 * st);
+  const int vphys = (vpos >> 3) ^ sc;  // chunk of dim 8sc+i is vphys ^ i
+  const int vbase = 8 * sc * kD + (vpos & 7);
+  const int last_key = a.nk - 1;
+  // Row offsets fit in 32 bits (checked on the host): one multiply per row.
+  const int ksn = static_cast<int>(a.ksn), vsn = static_cast<int>(a.vsn);
+  const T* kcol = kb_ptr + 8 * sc;
+  const T* vcol = vb_ptr + 8 * sc;
+
+  // The next tile's rows are loaded into registers while the current tile is
+  // computed (rows past n_key read a valid row; their bias is -inf).
+  op8 pk0, pk1, pv0, pv1;
+  T pb = static_cast<T>(0.0f);
+  auto stage_load = [&](int tile) {
+    const int kt = tile * kBN;
+    pk0 = *reinterpret_cast<const op8*>(kcol + min(kt + st, last_key) * ksn);
+    pk1 = *reinterpret_cast<const op8*>(kcol + min(kt + st + 32, last_key) * ksn);
+    pv0 = *reinterpret_cast<const op8*>(vcol + min(kt + 2 * st, last_key) * vsn);
+    pv1 = *reinterpret_cast<const op8*>(vcol + min(kt + 2 * st + 1, last_key) * vsn);
+    if (a.bias) pb = a.bias[min(kt + lane, last_key)];
+  };
+  // Every wave writes the same 64 bias values (branch-free; identical data).
+  auto stage_store = [&](int tile, int buf) {
+    T* kl = k_lds + buf * kTileElems;
+    T* vl = vt_lds + buf * kTileElems;
+    *reinterpret_cast<op8*>(kl + kw0) = pk0;
+    *reinterpret_cast<op8*>(kl + kw1) = pk1;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const op2 pr = {pv0[i], pv1[i]};
+      *reinterpret_cast<op2*>(vl + vbase + i * kD + ((vphys ^ i) << 3)) = pr;
+    }
+    const bool valid = tile * kBN + lane < a.nk;
+    const float bv = a.bias ? 8.0f * to_f32(pb) : 0.0f;
+    b_lds[buf * kBN + lane] = static_cast<T>(valid ? bv : -__builtin_inff());
+  };
+
+  float m[kQB], lsum[kQB];
+  f32x16 o[kQB][2];
+#pragma unroll
+  for (int qb = 0; qb < kQB; ++qb) {
     m[qb] = -__builtin_inff();
     lsum[qb] = 0.0f;
 #pragma unroll
@@ -124,96 +226,75 @@ __global__ __launch_bounds__(kWavesA * 64, 2) void attn_mfma_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) o[qb][dt][r] = 0.0f;
   }
-  const op2 ones2 = {static_cast<T>(1.0f), static_cast<T>(1.0f)};
 
-  // Staging roles: K rows (tid>>3) and (tid>>3)+32, V key pair 2*(tid>>3), 8 dims at dc.
-  const int st_row = tid >> 3;
-  const int dc = (tid & 7) * 8;
+  stage_load(tile0);
+  stage_store(tile0, 0);
+  __syncthreads();
 
-  for (int kt = 0; kt < nk; kt += kBN) {
-    __syncthreads();
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const int key = st_row + 32 * p;
-      const op8 val =
-          kt + key < nk ? *reinterpret_cast<const op8*>(kb_ptr + (kt + key) * ksn + dc) : zero8;
-      *reinterpret_cast<op8*>(&k_lds[key * kKRow + dc]) = val;
-    }
-    {
-      const int key0 = 2 * st_row;
-      const op8 v0 =
-          kt + key0 < nk ? *reinterpret_cast<const op8*>(vb_ptr + (kt + key0) * vsn + dc) : zero8;
-      const op8 v1 = kt + key0 + 1 < nk
-                         ? *reinterpret_cast<const op8*>(vb_ptr + (kt + key0 + 1) * vsn + dc)
-                         : zero8;
-      const int pos = vt_pos(key0);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const op2 pr = {v0[i], v1[i]};
-        *reinterpret_cast<op2*>(&vt_lds[(dc + i) * kVRow + pos]) = pr;
-      }
-    }
-    if (tid < kBN) {
-      const int key = kt + tid;
-      float bv = -__builtin_inff();
-      if (key < nk) bv = bias ? 8.0f * to_f32(bias[key]) : 0.0f;
-      b_lds[tid] = static_cast<T>(bv);
-    }
-    __syncthreads();
+  for (int tile = tile0; tile < tile1; ++tile) {
+    const int buf = (tile - tile0) & 1;
+    const bool more = tile + 1 < tile1;
+    if (more) stage_load(tile + 1);
+    const T* kl = k_lds + buf * kTileElems;
+    const T* vl = vt_lds + buf * kTileElems;
 
-    // S^T = K' Q'^T for two 32-key sub-tiles.
-    f32x16 s[QB][2];
+    // S^T = K' Q'^T for two 32-key sub-tiles, bias in a fifth k-step.
+    f32x16 s[kQB][2];
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb)
+      for (int qb = 0; qb < kQB; ++qb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) s[qb][sub][r] = 0.0f;
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const op8 a = *reinterpret_cast<const op8*>(&k_lds[(sub * 32 + l32) * kKRow + 16 * t + 8 * hh]);
+        const op8 ka = *reinterpret_cast<const op8*>(kl + sub * 32 * kD + off[t ^ (2 * sub)]);
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) s[qb][sub] = Mma<T>::mma(a, qreg[qb][t], s[qb][sub]);
+        for (int qb = 0; qb < kQB; ++qb) s[qb][sub] = Mma<T>::mma(ka, qreg[qb][t], s[qb][sub]);
       }
-      op8 a = zero8;
-      if (hh == 0) a[0] = b_lds[sub * 32 + l32];
+      const T bv = b_lds[buf * kBN + sub * 32 + l32];
+      op8 ba = zero8;
+      ba[0] = hh == 0 ? bv : static_cast<T>(0.0f);
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) s[qb][sub] = Mma<T>::mma(a, qone, s[qb][sub]);
+      for (int qb = 0; qb < kQB; ++qb) s[qb][sub] = Mma<T>::mma(ba, qone, s[qb][sub]);
     }
 
-    // Online softmax in the exp2 domain; P rounded to T as the B operand.
-    op8 pk[QB][4];
+    // Online softmax in the exp2 domain.  The O/l rescale is skipped when no
+    // lane's running max moved (the factor would be exactly 1).
+    op8 p[kQB][4];
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
+    for (int qb = 0; qb < kQB; ++qb) {
       float mx = s[qb][0][0];
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[qb][sub][r]);
-      mx = fmaxf(mx, other_half(mx));
-      const float mnew = fmaxf(m[qb], mx);
-      const float corr = __builtin_amdgcn_exp2f((m[qb] - mnew) * c);
-      const float mc = mnew * c;
+      const float mnew = fmaxf(m[qb], half_max(mx));
+      if (__ballot(mnew > m[qb])) {
+        const float corr = __builtin_amdgcn_exp2f((m[qb] - mnew) * a.c);
+        lsum[qb] *= corr;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[qb][dt][r] *= corr;
+        m[qb] = mnew;
+      }
+      const float mc = m[qb] * a.c;
       float part = 0.0f;
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float pv = __builtin_amdgcn_exp2f(fmaf(s[qb][t >> 1][(t & 1) * 8 + j], c, -mc));
-          pk[qb][t][j] = static_cast<T>(pv);
-        }
+        i32x4 packed;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const op2 pr = {pk[qb][t][2 * j], pk[qb][t][2 * j + 1]};
+          const int r = (t & 1) * 8 + 2 * j;
+          const op2 pr = {static_cast<T>(__builtin_amdgcn_exp2f(fmaf(s[qb][t >> 1][r], a.c, -mc))),
+                          static_cast<T>(__builtin_amdgcn_exp2f(fmaf(s[qb][t >> 1][r + 1], a.c, -mc)))};
           part = Mma<T>::dot2(pr, ones2, part);
+          packed[j] = __builtin_bit_cast(int, pr);
         }
+        p[qb][t] = __builtin_bit_cast(op8, packed);
       }
-      lsum[qb] = lsum[qb] * corr + part;
-      m[qb] = mnew;
-#pragma unroll
-      for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[qb][dt][r] *= corr;
+      lsum[qb] += part;
     }
 
     // O^T += V^T P^T.
@@ -221,33 +302,135 @@ __global__ __launch_bounds__(kWavesA * 64, 2) void attn_mfma_kernel(
     for (int t = 0; t < 4; ++t) {
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt) {
-        const op8 a =
-            *reinterpret_cast<const op8*>(&vt_lds[(dt * 32 + l32) * kVRow + 16 * t + 8 * hh]);
+        const op8 va = *reinterpret_cast<const op8*>(vl + dt * 32 * kD + off[t ^ (2 * dt)]);
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) o[qb][dt] = Mma<T>::mma(a, pk[qb][t], o[qb][dt]);
+        for (int qb = 0; qb < kQB; ++qb) o[qb][dt] = Mma<T>::mma(va, p[qb][t], o[qb][dt]);
       }
     }
+
+    if (more) stage_store(tile + 1, buf ^ 1);
+    __syncthreads();
   }
 
-  T* ob_ptr = out + b * osb + h * osh;
+  if (partial == nullptr) {
+    T* ob_ptr = a.out + b * a.osb + h * a.osh;
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const float ltot = lsum[qb] + other_half(lsum[qb]);
-    const int row = qw0 + qb * 32 + l32;
-    if (row < nq) {
+    for (int qb = 0; qb < kQB; ++qb) {
+      const float ltot = half_sum(lsum[qb]);
+      const int row = qw0 + qb * 32 + l32;
+      if (row < a.nq) {
 #pragma unroll
-      for (int dt = 0; dt < 2; ++dt) {
+        for (int dt = 0; dt < 2; ++dt) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int d = dt * 32 + 8 * g + 4 * hh;
-          typedef __attribute__((__vector_size__(4 * sizeof(T)))) T t4;
-          t4 val;
+          for (int g = 0; g < 4; ++g) {
+            op4 val;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) val[e] = static_cast<T>(o[qb][dt][4 * g + e] / ltot);
-          *reinterpret_cast<t4*>(ob_ptr + row * osn + d) = val;
+            for (int e = 0; e < 4; ++e) val[e] = static_cast<T>(o[qb][dt][4 * g + e] / ltot);
+            *reinterpret_cast<op4*>(ob_ptr + row * a.osn + dt * 32 + 8 * g + 4 * hh) = val;
+          }
         }
       }
     }
+  } else {
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb) {
+      const int ql = wave * kQPerWave + qb * 32 + l32;
+      float* po = partial + ql * kD;
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 val = {o[qb][dt][4 * g], o[qb][dt][4 * g + 1], o[qb][dt][4 * g + 2],
+                             o[qb][dt][4 * g + 3]};
+          *reinterpret_cast<f32x4*>(po + dt * 32 + 8 * g + 4 * hh) = val;
+        }
+      const float ltot = half_sum(lsum[qb]);
+      if (hh == 0) {
+        partial[kQBlock * kD + ql] = m[qb];
+        partial[kQBlock * kD + kQBlock + ql] = ltot;
+      }
+    }
+  }
+}
+
+// One work-group walks the units [sk_begin(w), sk_begin(w+1)) of the flattened
+// (task, key tile) space; a task is a (batch*head, 256-query block) pair.  A
+// segment that covers a whole task writes the output; a segment that covers a
+// part writes its partial state (slot 0: the work-group's first segment, slot
+// 1: its last), which attn_merge_kernel combines.  With groups == tasks every
+// work-group owns exactly one whole task (no partial states).
+template <typename T>
+__global__ __launch_bounds__(kWaves * 64, 2) void attn_mfma_kernel(AttnArgs<T> a) {
+  __shared__ __attribute__((aligned(16))) T k_lds[2 * kTileElems];
+  __shared__ __attribute__((aligned(16))) T vt_lds[2 * kTileElems];
+  __shared__ __attribute__((aligned(16))) T b_lds[2 * kBN];
+  const int64_t w = xcd_remap(blockIdx.x, gridDim.x);
+  int64_t u = sk_begin(w, a.units, a.groups);
+  const int64_t u_end = sk_begin(w + 1, a.units, a.groups);
+  bool first = true;
+  while (u < u_end) {
+    const int64_t task = u / a.ntiles;
+    const int tile0 = static_cast<int>(u - task * a.ntiles);
+    const int64_t seg_end = min(u_end, (task + 1) * a.ntiles);
+    const int tile1 = static_cast<int>(seg_end - task * a.ntiles);
+    const int bh = static_cast<int>(task / a.n_qblocks);
+    const int qblk = static_cast<int>(task - static_cast<int64_t>(bh) * a.n_qblocks);
+    float* partial = nullptr;
+    if (tile0 != 0 || tile1 != a.ntiles)
+      partial = a.partial + (2 * w + (first ? 0 : 1)) * static_cast<int64_t>(kPartialFloats);
+    attn_segment<T>(a, k_lds, vt_lds, b_lds, bh, qblk, tile0, tile1, partial);
+    u = seg_end;
+    first = false;
+  }
+}
+
+// Combines the partial states of every task split across work-groups.  Block
+// j handles the task that starts inside the range of work-group j (if that
+// task is split); 16 threads per query, 4 dims each.
+template <typename T>
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs<T> a) {
+  const int64_t w0 = blockIdx.x;
+  const int64_t ub = sk_begin(w0, a.units, a.groups);
+  const int64_t ue = sk_begin(w0 + 1, a.units, a.groups);
+  if (ub >= ue) return;
+  // Only the last task that starts inside [ub, ue) can continue past ue.
+  const int64_t task = (ue - 1) / a.ntiles;
+  const int64_t t0 = task * a.ntiles;
+  if (t0 < ub) return;  // no task starts here
+  const int64_t w1 = sk_owner(t0 + a.ntiles - 1, a.units, a.groups);
+  if (w1 == w0) return;  // whole inside w0: already written
+  const int first_slot = ub < t0 ? 1 : 0;  // w0's segment is its last (or only) one
+  const int bh = static_cast<int>(task / a.n_qblocks);
+  const int qblk = static_cast<int>(task - static_cast<int64_t>(bh) * a.n_qblocks);
+  const int b = bh / a.heads;
+  const int h = bh - b * a.heads;
+  T* ob_ptr = a.out + b * a.osb + h * a.osh;
+  const int d0 = (threadIdx.x & 15) * 4;
+  for (int ql = threadIdx.x >> 4; ql < kQBlock; ql += 16) {
+    const int row = qblk * kQBlock + ql;
+    if (row >= a.nq) break;
+    float mmax = -__builtin_inff();
+    for (int64_t w = w0; w <= w1; ++w) {
+      const int slot = w == w0 ? first_slot : 0;
+      const float* p = a.partial + (2 * w + slot) * static_cast<int64_t>(kPartialFloats);
+      mmax = fmaxf(mmax, p[kQBlock * kD + ql]);
+    }
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    float l = 0.0f;
+    for (int64_t w = w0; w <= w1; ++w) {
+      const int slot = w == w0 ? first_slot : 0;
+      const float* p = a.partial + (2 * w + slot) * static_cast<int64_t>(kPartialFloats);
+      const float f = __builtin_amdgcn_exp2f((p[kQBlock * kD + ql] - mmax) * a.c);
+      const f32x4 x = *reinterpret_cast<const f32x4*>(p + ql * kD + d0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] = fmaf(x[e], f, acc[e]);
+      l = fmaf(p[kQBlock * kD + kQBlock + ql], f, l);
+    }
+    typedef typename Mma<T>::op4 op4;
+    op4 val;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) val[e] = static_cast<T>(acc[e] / l);
+    *reinterpret_cast<op4*>(ob_ptr + row * a.osn + d0) = val;
   }
 }
 
@@ -324,23 +507,84 @@ __global__ __launch_bounds__(64) void attn_f32_kernel(
   }
 }
 
+// Resident work-groups of attn_mfma_kernel<T> on the current device (CUs x
+// blocks per CU), cached per device.
+template <typename T>
+int64_t resident_groups() {
+  static int cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] == 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attn_mfma_kernel<T>, kWaves * 64, 0) !=
+        hipSuccess)
+      return 0;
+    cache[dev] = cus * (per_cu > 0 ? per_cu : 1);
+  }
+  return cache[dev];
+}
+
+constexpr int64_t kMinUnitsPerGroup = 8;  // key tiles per work-group, at least
+
+// Work-group count of the stream-K schedule (0: plain schedule, one task per group).
+template <typename T>
+int64_t stream_groups(int64_t tasks, int64_t units) {
+  const int64_t slots = resident_groups<T>();
+  if (slots <= 0) return 0;
+  int64_t groups = std::min<int64_t>(slots, (units + kMinUnitsPerGroup - 1) / kMinUnitsPerGroup);
+  if (groups <= 0 || groups == tasks) return 0;
+  return groups;
+}
+
 template <typename T>
 int launch_mfma(const void* q, const void* k, const void* v, const void* bias, void* out,
                 int64_t batch, int64_t heads, int64_t nq, int64_t nk, const int64_t* qs,
-                const int64_t* ks, const int64_t* vs, const int64_t* os, hipStream_t stream) {
-  constexpr int QB = 1;
-  constexpr int kQPerBlock = kWavesA * QB * 32;
-  const int64_t n_qblocks = (nq + kQPerBlock - 1) / kQPerBlock;
-  const int64_t total = n_qblocks * batch * heads;
-  VGO_REQUIRE(total <= 0x7fffffff, "mass_bias_attention: grid too large");
-  const float c = kLog2e / 8.0f;
-  hipLaunchKernelGGL((attn_mfma_kernel<T, QB>), dim3(static_cast<unsigned>(total)),
-                     dim3(kWavesA * 64), 0, stream, static_cast<const T*>(q),
-                     static_cast<const T*>(k), static_cast<const T*>(v),
-                     static_cast<const T*>(bias), static_cast<T*>(out), static_cast<int>(heads),
-                     static_cast<int>(nq), static_cast<int>(nk), static_cast<int>(n_qblocks), qs[0],
-                     qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0], os[1], os[2], c);
-  return check_launch("mass_bias_attention");
+                const int64_t* ks, const int64_t* vs, const int64_t* os, void* workspace,
+                size_t workspace_bytes, bool split, hipStream_t stream) {
+  const int64_t n_qblocks = (nq + kQBlock - 1) / kQBlock;
+  const int64_t ntiles = (nk + kBN - 1) / kBN;
+  const int64_t tasks = n_qblocks * batch * heads;
+  VGO_REQUIRE(tasks <= 0x7fffffff && batch * heads <= 0x7fffffff,
+              "mass_bias_attention: grid too large");
+  AttnArgs<T> a;
+  a.q = static_cast<const T*>(q);
+  a.k = static_cast<const T*>(k);
+  a.v = static_cast<const T*>(v);
+  a.bias = static_cast<const T*>(bias);
+  a.out = static_cast<T*>(out);
+  a.partial = nullptr;
+  a.heads = static_cast<int>(heads);
+  a.nq = static_cast<int>(nq);
+  a.nk = static_cast<int>(nk);
+  a.n_qblocks = static_cast<int>(n_qblocks);
+  a.ntiles = static_cast<int>(ntiles);
+  a.units = tasks * ntiles;
+  a.groups = tasks;
+  a.qsb = qs[0], a.qsh = qs[1], a.qsn = qs[2];
+  a.ksb = ks[0], a.ksh = ks[1], a.ksn = ks[2];
+  a.vsb = vs[0], a.vsh = vs[1], a.vsn = vs[2];
+  a.osb = os[0], a.osh = os[1], a.osn = os[2];
+  a.c = kLog2e / 8.0f;
+  if (split) {
+    const int64_t groups = stream_groups<T>(tasks, a.units);
+    if (groups > 0) {
+      const size_t need = static_cast<size_t>(groups) * 2 * kPartialFloats * sizeof(float);
+      if (workspace == nullptr || workspace_bytes < need)
+        return fail(VGO_EWORKSPACE, "mass_bias_attention: workspace too small");
+      VGO_REQUIRE(aligned(workspace, 16), "mass_bias_attention: workspace must be 16-byte aligned");
+      a.groups = groups;
+      a.partial = static_cast<float*>(workspace);
+    }
+  }
+  hipLaunchKernelGGL((attn_mfma_kernel<T>), dim3(static_cast<unsigned>(a.groups)), dim3(kWaves * 64),
+                     0, stream, a);
+  int status = check_launch("mass_bias_attention");
+  if (status != VGO_OK || a.partial == nullptr) return status;
+  hipLaunchKernelGGL((attn_merge_kernel<T>), dim3(static_cast<unsigned>(a.groups)), dim3(256), 0,
+                     stream, a);
+  return check_launch("mass_bias_attention(merge)");
 }
 
 int launch_f32(const void* q, const void* k, const void* v, const void* bias, void* out,
@@ -362,14 +606,15 @@ int launch_f32(const void* q, const void* k, const void* v, const void* bias, vo
 }  // namespace
 }  // namespace vgo
 
-extern "C" int vgo_mass_bias_attn_fwd(const void* q, const void* k, const void* v,
-                                      const void* log_mass, void* out, int64_t batch,
-                                      int64_t heads, int64_t n_query, int64_t n_key,
-                                      int64_t head_dim, const int64_t q_stride[3],
-                                      const int64_t k_stride[3], const int64_t v_stride[3],
-                                      const int64_t o_stride[3], int dtype, void* stream) {
+namespace {
+
+int attn_entry(const void* q, const void* k, const void* v, const void* log_mass, void* out,
+               int64_t batch, int64_t heads, int64_t n_query, int64_t n_key, int64_t head_dim,
+               const int64_t* q_stride, const int64_t* k_stride, const int64_t* v_stride,
+               const int64_t* o_stride, int dtype, void* workspace, size_t workspace_bytes,
+               bool split, void* stream) {
   using namespace vgo;
-  VGO_REQUIRE(head_dim == 64, "the initial fused kernel supports head_dim=64 only");
+  VGO_REQUIRE(head_dim == 64, "mass_bias_attention: only head_dim=64 is supported");
   VGO_REQUIRE(batch >= 0 && heads >= 0 && n_query >= 0 && n_key >= 0,
               "mass_bias_attention: negative size");
   if (batch == 0 || heads == 0 || n_query == 0) return VGO_OK;
@@ -386,14 +631,59 @@ extern "C" int vgo_mass_bias_attn_fwd(const void* q, const void* k, const void* 
     }
     VGO_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(out, 8),
                 "mass_bias_attention: q/k/v must be 16-byte aligned");
+    // Token offsets inside one (batch, head) plane are 32-bit in the kernel.
+    const int64_t lim = int64_t(1) << 31;
+    if (n_key * std::max<int64_t>(k_stride[2], v_stride[2]) >= lim ||
+        n_query * std::max<int64_t>(q_stride[2], o_stride[2]) >= lim)
+      return fail(VGO_EUNSUPPORTED, "mass_bias_attention: token stride x tokens exceeds 2^31 elements");
     if (dtype == VGO_BF16)
       return launch_mfma<bf16_t>(q, k, v, log_mass, out, batch, heads, n_query, n_key, q_stride,
-                                 k_stride, v_stride, o_stride, s);
+                                 k_stride, v_stride, o_stride, workspace, workspace_bytes, split, s);
     return launch_mfma<f16_t>(q, k, v, log_mass, out, batch, heads, n_query, n_key, q_stride,
-                              k_stride, v_stride, o_stride, s);
+                              k_stride, v_stride, o_stride, workspace, workspace_bytes, split, s);
   }
   if (dtype == VGO_F32)
     return launch_f32(q, k, v, log_mass, out, batch, heads, n_query, n_key, q_stride, k_stride,
                       v_stride, o_stride, s);
   return fail(VGO_EINVAL, "mass_bias_attention: unsupported dtype");
+}
+
+}  // namespace
+
+extern "C" int vgo_mass_bias_attn_fwd(const void* q, const void* k, const void* v,
+                                      const void* log_mass, void* out, int64_t batch,
+                                      int64_t heads, int64_t n_query, int64_t n_key,
+                                      int64_t head_dim, const int64_t q_stride[3],
+                                      const int64_t k_stride[3], const int64_t v_stride[3],
+                                      const int64_t o_stride[3], int dtype, void* stream) {
+  return attn_entry(q, k, v, log_mass, out, batch, heads, n_query, n_key, head_dim, q_stride,
+                    k_stride, v_stride, o_stride, dtype, nullptr, 0, false, stream);
+}
+
+extern "C" int vgo_mass_bias_attn_workspace(int64_t batch, int64_t heads, int64_t n_query,
+                                            int64_t n_key, int dtype, size_t* bytes) {
+  using namespace vgo;
+  VGO_REQUIRE(bytes, "mass_bias_attention: null size pointer");
+  VGO_REQUIRE(batch >= 0 && heads >= 0 && n_query >= 0 && n_key >= 0,
+              "mass_bias_attention: negative size");
+  *bytes = 0;
+  if (batch == 0 || heads == 0 || n_query == 0 || n_key == 0 || dtype == VGO_F32) return VGO_OK;
+  VGO_REQUIRE(dtype == VGO_BF16 || dtype == VGO_F16, "mass_bias_attention: unsupported dtype");
+  const int64_t tasks = (n_query + kQBlock - 1) / kQBlock * batch * heads;
+  const int64_t units = tasks * ((n_key + kBN - 1) / kBN);
+  const int64_t groups =
+      dtype == VGO_BF16 ? stream_groups<bf16_t>(tasks, units) : stream_groups<f16_t>(tasks, units);
+  *bytes = static_cast<size_t>(groups) * 2 * kPartialFloats * sizeof(float);
+  return VGO_OK;
+}
+
+extern "C" int vgo_mass_bias_attn_fwd_ws(const void* q, const void* k, const void* v,
+                                         const void* log_mass, void* out, int64_t batch,
+                                         int64_t heads, int64_t n_query, int64_t n_key,
+                                         int64_t head_dim, const int64_t q_stride[3],
+                                         const int64_t k_stride[3], const int64_t v_stride[3],
+                                         const int64_t o_stride[3], int dtype, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
+  return attn_entry(q, k, v, log_mass, out, batch, heads, n_query, n_key, head_dim, q_stride,
+                    k_stride, v_stride, o_stride, dtype, workspace, workspace_bytes, true, stream);
 }

@@ -8,14 +8,22 @@ allocation.  The arithmetic runs in the hand-written HIP kernel
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
 
 
 def _attention_into(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                    bias: torch.Tensor | None, out: torch.Tensor) -> torch.Tensor:
-    """Run the kernel on [B,H,N,64] views (any batch/head/token strides) into `out`."""
+                    bias: torch.Tensor | None, out: torch.Tensor, *,
+                    split: bool = True) -> torch.Tensor:
+    """Run the kernel on [B,H,N,64] views (any batch/head/token strides) into `out`.
+
+    split=True lets the library balance (query block, key tile) work over the
+    resident work-groups (stream-K, partial states in a workspace merged by a
+    second kernel); split=False runs one work-group per 256-query block.
+    """
     lib = _lib.load()
     _lib.require_gpu(q, k, v, bias, out)
     if not (q.dtype == k.dtype == v.dtype == out.dtype):
@@ -33,12 +41,21 @@ def _attention_into(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if out.stride(-1) != 1:
         raise ValueError("output channel stride must be 1")
     batch, heads, n_query, head_dim = q.shape
-    status = lib.vgo_mass_bias_attn_fwd(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.ptr(bias), out.data_ptr(),
-        batch, heads, n_query, k.shape[-2], head_dim,
-        _lib.strides3(q), _lib.strides3(k), _lib.strides3(v), _lib.strides3(out),
-        _lib.dtype_code(q.dtype), _lib.stream_of(q),
-    )
+    n_key = k.shape[-2]
+    dtype = _lib.dtype_code(q.dtype)
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.ptr(bias), out.data_ptr(),
+            batch, heads, n_query, n_key, head_dim,
+            _lib.strides3(q), _lib.strides3(k), _lib.strides3(v), _lib.strides3(out), dtype)
+    need = ctypes.c_size_t(0)
+    if split:
+        _lib.check(lib.vgo_mass_bias_attn_workspace(batch, heads, n_query, n_key, dtype,
+                                                    ctypes.byref(need)))
+    if need.value == 0:
+        status = lib.vgo_mass_bias_attn_fwd(*args, _lib.stream_of(q))
+    else:
+        workspace = torch.empty(need.value // 4, device=q.device, dtype=torch.float32)
+        status = lib.vgo_mass_bias_attn_fwd_ws(*args, workspace.data_ptr(), need.value,
+                                               _lib.stream_of(q))
     _lib.check(status)
     return out
 

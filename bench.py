@@ -170,6 +170,10 @@ def torch_reference_forward(model, ref_global, patches):
     tokens = torch.cat([camera, register, patches], dim=1)
     _, T, D = tokens.shape
     sin, cos = agg_layers.rope_sincos(GRID[0], GRID[1], D // HEADS, device=patches.device)
+    # Frame and register blocks on the reference's op sequence too (torch LayerNorm,
+    # RoPE, SDPA) -- not on this build's fused kernels.
+    for blk in list(model.frame_blocks) + list(model.inter_frame_blocks):
+        blk.attn._fusable = lambda *a: False
     for i in range(model.depth):
         tokens = model.frame_blocks[i](tokens.view(B * S, T, D), (sin, cos))
         tokens = tokens.view(B, S, T, D)
@@ -180,6 +184,8 @@ def torch_reference_forward(model, ref_global, patches):
             tokens = torch.cat([special, tokens[:, :, pts:]], dim=2)
         else:
             tokens = ref_global.block(blk, tokens.reshape(B, S * T, D)).view(B, S, T, D)
+    for blk in list(model.frame_blocks) + list(model.inter_frame_blocks):
+        del blk.attn._fusable
     return tokens
 
 

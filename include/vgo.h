@@ -63,6 +63,25 @@ int vgo_mass_bias_attn_fwd(const void* q, const void* k, const void* v, const vo
                            const int64_t o_stride[3], int dtype, void* stream);
 
 /*
+ * Workspace variant of vgo_mass_bias_attn_fwd, same arguments and result.
+ * The library balances the (256-query block, 64-key tile) work of the whole
+ * call over the work-groups the device holds resident at once (stream-K):
+ * a block whose key range is shared by two work-groups is finished by a
+ * second, small kernel from partial states kept in `workspace`.  Query the
+ * size with vgo_mass_bias_attn_workspace on the device that will run the
+ * call; 0 bytes means no split is needed (workspace may be NULL).  Same
+ * replaced reference function as vgo_mass_bias_attn_fwd.
+ */
+int vgo_mass_bias_attn_workspace(int64_t batch, int64_t heads, int64_t n_query, int64_t n_key,
+                                 int dtype, size_t* bytes);
+int vgo_mass_bias_attn_fwd_ws(const void* q, const void* k, const void* v, const void* log_mass,
+                              void* out, int64_t batch, int64_t heads, int64_t n_query,
+                              int64_t n_key, int64_t head_dim, const int64_t q_stride[3],
+                              const int64_t k_stride[3], const int64_t v_stride[3],
+                              const int64_t o_stride[3], int dtype, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
+/*
  * Top-4 convex projection (unmerge): out[i,:] = sum_c w[i,c] * table[index[i,c],:].
  *
  * Replaces the restore of WeightedBilinearTokenPlan / TokenPlan

@@ -45,7 +45,6 @@ def test_argument_errors_raise_value_error_without_a_gpu():
     # Validation happens on the host before any launch, so this runs on CPU.
     lib_mod = import_package("_lib")
     lib = lib_mod.load()
-    strides = lib_mod.strides3
     status = lib.vgo_mass_bias_attn_fwd(None, None, None, None, None, 1, 1, 1, 1, 32,
                                         (ctypes.c_int64 * 3)(), (ctypes.c_int64 * 3)(),
                                         (ctypes.c_int64 * 3)(), (ctypes.c_int64 * 3)(), 1, None)
@@ -53,7 +52,6 @@ def test_argument_errors_raise_value_error_without_a_gpu():
     assert "head_dim=64" in lib_mod.last_error()
     with pytest.raises(ValueError, match="head_dim=64"):
         lib_mod.check(status)
-    del strides
 
 
 def test_cpu_tensors_are_rejected():

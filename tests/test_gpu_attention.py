@@ -98,3 +98,49 @@ def test_deterministic_run_twice(vgo, device):
     args = (q.to(device), k.to(device), v.to(device), mass.log().to(device))
     assert torch.equal(vgo.mass_bias_attention(*args), vgo.mass_bias_attention(*args))
     assert RTOL[torch.bfloat16] == 2e-2
+
+
+def _attention_split(vgo, q, k, v, bias, split):
+    from importlib import import_module
+    mba = import_module(vgo.__name__ + ".mass_bias_attention")
+    out = torch.empty_like(q)
+    return mba._attention_into(q, k, v, bias, out, split=split)
+
+
+@pytest.mark.parametrize("shape", [
+    (1, 16, 1044, 522),   # 80 tasks of 9 key tiles spread over ~90 work-groups
+    (1, 2, 100, 20000),   # 2 tasks of 313 tiles: each cut over dozens of work-groups
+    (2, 3, 700, 1333),    # batch > 1, ragged query and key tails
+])
+def test_stream_k_and_plain_schedules_match_oracle(vgo, device, shape):
+    b, h, nq, nk = shape
+    print(f"[attn schedules] shape={shape}", flush=True)
+    q, k, v, mass = _inputs(31 + nq, b, h, nq, nk, torch.bfloat16)
+    bias = mass.log().to(torch.bfloat16)
+    ref = oracle.mass_bias_attention(q, k, v, mass.log())
+    args = (q.to(device), k.to(device), v.to(device), bias.to(device))
+    for split in (True, False):
+        out = _attention_split(vgo, *args, split=split)
+        torch.cuda.synchronize()
+        assert_close(out, ref, torch.bfloat16, what=f"attention split={split} {shape}")
+
+
+def test_full_c4_size_rows_match_oracle(vgo, device):
+    """C4 global-attention size (16 heads x 16,464 compacted tokens): sampled query rows."""
+    b, h, n = 1, 16, 16464
+    print(f"[attn c4] heads={h} tokens={n}", flush=True)
+    g = torch.Generator().manual_seed(44)
+    q = (torch.randn(b, h, n, 64, generator=g) * 0.125).bfloat16()
+    k = (torch.randn(b, h, n, 64, generator=g) * 0.125).bfloat16()
+    v = torch.randn(b, h, n, 64, generator=g).bfloat16()
+    mass = torch.randint(1, 6, (n,), generator=g).float()
+    args = (q.to(device), k.to(device), v.to(device), mass.log().bfloat16().to(device))
+    split = _attention_split(vgo, *args, split=True)
+    plain = _attention_split(vgo, *args, split=False)
+    rows = torch.randperm(n, generator=g)[:97].sort().values
+    rows = torch.cat([rows, torch.tensor([0, 255, 256, n - 1])]).unique()
+    ref = oracle.mass_bias_attention(q[:, :, rows], k, v, mass.log())
+    assert_close(split[:, :, rows.to(device)], ref, torch.bfloat16, what="C4 stream-K rows")
+    assert_close(plain[:, :, rows.to(device)], ref, torch.bfloat16, what="C4 plain rows")
+    # Same math on every row: the two schedules differ only in summation order.
+    assert_close(split, plain.float(), torch.bfloat16, what="C4 stream-K vs plain")
