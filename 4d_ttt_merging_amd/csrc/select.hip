@@ -7,10 +7,11 @@
 //             removed -> compact id of its target.
 // Only the *set* of the r best sources matters (keep is re-sorted, inverse is
 // per token), so instead of a full sort one work-group per batch element runs
-// a four-pass radix select on the order-preserving 32-bit image of `best`,
-// then breaks ties at the threshold by source position (the stable sort's
-// rule) with a block-wide prefix count, and finally builds keep/inverse with
-// one block scan over the tokens.  Integer work, bit-exact, deterministic.
+// a four-pass radix select on the order-preserving 32-bit image of `best`
+// (coalesced histogram passes, parallel digit search), then breaks ties at the
+// threshold by source position (the stable sort's rule) and builds keep /
+// inverse, both with ballot-based ordered ranks (one block scan per 64 chunks
+// of 1024 elements).  Integer work, bit-exact, deterministic.
 #include "vgo_common.h"
 
 namespace vgo {
@@ -58,6 +59,64 @@ __device__ int block_exclusive_scan(int v, int* lds_waves, int* total) {
   return wave_base + x - v;
 }
 
+// Ranks, in index order, of the elements whose flag is set: element i = c*kThreads
+// + tid of chunk c.  Chunks are processed 64 at a time: per (chunk, wave) counts
+// from ballots go to LDS, one block scan over those 1024 counts gives every
+// (chunk, wave) its offset, and a lane adds the set flags of lower lanes.
+// `flag(c)` is evaluated twice per chunk; `emit(c, rank)` is called for every
+// set flag.  Returns the number of set flags.
+template <typename Flag, typename Emit>
+__device__ int ordered_ranks(int n_chunks, Flag flag, Emit emit, int* cnt_lds, int* scan_lds) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  int running = 0;
+  for (int c0 = 0; c0 < n_chunks; c0 += 64) {
+    const int nc = min(64, n_chunks - c0);
+    for (int c = 0; c < 64; ++c) {
+      const uint64_t m = c < nc ? __ballot(flag(c0 + c)) : 0ull;
+      if (lane == 0) cnt_lds[c * kWavesS + wave] = __popcll(m);
+    }
+    __syncthreads();
+    const int mine = cnt_lds[threadIdx.x];  // kThreads == 64 * kWavesS entries
+    int sum = 0;
+    const int pre = block_exclusive_scan(mine, scan_lds, &sum);
+    cnt_lds[threadIdx.x] = pre;
+    __syncthreads();
+    const uint64_t below = (1ull << lane) - 1ull;
+    for (int c = 0; c < nc; ++c) {
+      const bool f = flag(c0 + c);
+      const uint64_t m = __ballot(f);
+      if (f) emit(c0 + c, running + cnt_lds[c * kWavesS + wave] + __popcll(m & below));
+    }
+    running += sum;
+    __syncthreads();
+  }
+  return running;
+}
+
+// hist[digit] += 1 for every lane with `valid`.  Keys here cluster in a few
+// digits (bf16-rounded scores), and same-address LDS atomics serialise, so a
+// wave first adds whole groups of equal digits through a leader lane; after a
+// few groups the remaining lanes fall back to one atomic each.
+__device__ __forceinline__ void hist_add(int* hist, bool valid, uint32_t digit) {
+  const int lane = threadIdx.x & 63;
+  uint64_t active = __ballot(valid);
+#pragma unroll
+  for (int round = 0; round < 4; ++round) {
+    if (active == 0) return;
+    const int leader = __ffsll(static_cast<long long>(active)) - 1;
+    const uint32_t d = __shfl(digit, leader);
+    const uint64_t same = __ballot(valid && digit == d) & active;
+    if (lane == leader) atomicAdd(&hist[d], __popcll(same));
+    active &= ~same;
+  }
+  if ((active >> lane) & 1ull) atomicAdd(&hist[digit], 1);
+}
+
+// Keys per thread held in registers (sources beyond kThreads * kKeyRegs are
+// re-read from global memory in batches of the same size).
+constexpr int kKeyRegs = 32;
+
 __global__ __launch_bounds__(kThreads) void fastvggt_assemble_kernel(
     const float* __restrict__ best, const int32_t* __restrict__ target,
     const int64_t* __restrict__ source_ids, const int64_t* __restrict__ dest_ids, int ns, int nd,
@@ -65,23 +124,34 @@ __global__ __launch_bounds__(kThreads) void fastvggt_assemble_kernel(
     uint8_t* __restrict__ removed_flag) {
   __shared__ int hist[256];
   __shared__ int scan_lds[kWavesS];
+  __shared__ int cnt_lds[kThreads];
   __shared__ uint32_t sel_prefix;
   __shared__ int sel_above;
 
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
+  const int lane = tid & 63;
   const float* bb = best + static_cast<int64_t>(b) * ns;
   const int32_t* tb = target + static_cast<int64_t>(b) * ns;
   int64_t* inv = inverse + static_cast<int64_t>(b) * total;
   int64_t* kp = keep + static_cast<int64_t>(b) * (total - removed);
   uint8_t* flag = removed_flag + static_cast<int64_t>(b) * ns;
+  const int s_chunks = (ns + kThreads - 1) / kThreads;
+  const int t_chunks = (total + kThreads - 1) / kThreads;
 
-  const int es = (ns + kThreads - 1) / kThreads;  // sources per thread (contiguous run)
-  const int s_begin = min(ns, tid * es), s_end = min(ns, s_begin + es);
-  const int et = (total + kThreads - 1) / kThreads;  // tokens per thread
-  const int t_begin = min(total, tid * et), t_end = min(total, t_begin + et);
+  // Keys of chunks [0, kKeyRegs) in registers; key(c) reads further chunks from global.
+  uint32_t kreg[kKeyRegs];
+#pragma unroll
+  for (int c = 0; c < kKeyRegs; ++c) {
+    const int i = c * kThreads + tid;
+    kreg[c] = i < ns ? ord32(bb[i]) : 0u;
+  }
+  auto key = [&](int c) -> uint32_t {  // chunks >= kKeyRegs
+    const int i = c * kThreads + tid;
+    return i < ns ? ord32(bb[i]) : 0u;
+  };
 
-  // ---- radix select: find the r-th largest key T and how many keys exceed it.
+  // ---- radix select (8-bit digits, most significant first) of the r-th largest key.
   if (tid == 0) {
     sel_prefix = 0;
     sel_above = 0;
@@ -92,66 +162,157 @@ __global__ __launch_bounds__(kThreads) void fastvggt_assemble_kernel(
     __syncthreads();
     const uint32_t prefix = sel_prefix;
     const uint32_t pmask = pass == 0 ? 0u : (0xFFFFFFFFu << (32 - 8 * pass));
-    for (int i = s_begin; i < s_end; ++i) {
-      const uint32_t o = ord32(bb[i]);
-      if ((o & pmask) == prefix) atomicAdd(&hist[(o >> shift) & 0xFF], 1);
+#pragma unroll
+    for (int c = 0; c < kKeyRegs; ++c) {
+      if (c < s_chunks)  // wave-uniform
+        hist_add(hist, c * kThreads + tid < ns && (kreg[c] & pmask) == prefix, (kreg[c] >> shift) & 0xFF);
+    }
+    for (int c = kKeyRegs; c < s_chunks; ++c) {
+      const int i = c * kThreads + tid;
+      const uint32_t o = i < ns ? ord32(bb[i]) : 0u;
+      hist_add(hist, i < ns && (o & pmask) == prefix, (o >> shift) & 0xFF);
     }
     __syncthreads();
-    if (tid == 0) {
-      const int need = removed - sel_above;  // >= 1 while we are still inside the run
-      int above = 0;
-      int digit = 255;
-      for (; digit > 0; --digit) {
-        if (above + hist[digit] >= need) break;
-        above += hist[digit];
+    if (tid < 64) {
+      // Lane l owns digits 4l..4l+3; c(d) = keys with digit >= d.  The digit
+      // sought is the largest d with c(d) >= need.
+      const int need = removed - sel_above;
+      int h[4], local = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        h[q] = hist[4 * lane + q];
+        local += h[q];
       }
-      sel_above += above;
-      sel_prefix = prefix | (static_cast<uint32_t>(digit) << shift);
+      int suffix = local;  // inclusive suffix sum over lanes >= lane
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_down(suffix, off);
+        if (lane + off < 64) suffix += y;
+      }
+      int c = suffix - local;  // keys in digits above this lane's range
+      int found = -1, above = 0;
+#pragma unroll
+      for (int q = 3; q >= 0; --q) {
+        if (found < 0 && c + h[q] >= need) {
+          found = 4 * lane + q;
+          above = c;
+        }
+        c += h[q];
+      }
+      const uint64_t hit = __ballot(found >= 0);
+      const int top = 63 - __clzll(hit);  // highest lane holding the digit
+      if (lane == top) {
+        sel_above += above;
+        sel_prefix = prefix | (static_cast<uint32_t>(found) << shift);
+      }
     }
     __syncthreads();
   }
   const uint32_t thresh = sel_prefix;
   const int need_ties = removed - sel_above;  // ties at the threshold to remove, lowest position first
 
-  // ---- tie ranks in source order, then mark removed sources.
-  int my_ties = 0;
-  for (int i = s_begin; i < s_end; ++i) my_ties += ord32(bb[i]) == thresh;
-  int ties_total = 0;
-  int tie_rank = block_exclusive_scan(my_ties, scan_lds, &ties_total);
-  for (int t = t_begin; t < t_end; ++t) inv[t] = 0;  // 0 = kept
-  __syncthreads();
-  for (int i = s_begin; i < s_end; ++i) {
-    const uint32_t o = ord32(bb[i]);
-    bool rm = o > thresh;
-    if (o == thresh) rm = (tie_rank++) < need_ties;
-    flag[i] = rm ? 1 : 0;
-    const int64_t sid = source_ids[i];
-    if (rm && sid >= 0 && sid < total) inv[sid] = -1;
-  }
-  __syncthreads();
-
-  // ---- compact ids of kept tokens, keep list.
-  int my_kept = 0;
-  for (int t = t_begin; t < t_end; ++t) my_kept += inv[t] == 0;
-  int kept_total = 0;
-  int base = block_exclusive_scan(my_kept, scan_lds, &kept_total);
-  const int n_keep = total - removed;
-  for (int t = t_begin; t < t_end; ++t) {
-    if (inv[t] == 0) {
-      inv[t] = base;
-      if (base < n_keep) kp[base] = t;  // always true for a valid (disjoint) source list
-      ++base;
+  // ---- removed sources: keys above the threshold, and the first need_ties ties.
+  // inv[t] holds 0 for kept tokens and -1 for removed ones until compaction.
+  for (int t0 = 0; t0 < total; t0 += kThreads * 8) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int t = t0 + q * kThreads + tid;
+      if (t < total) inv[t] = 0;
     }
   }
   __syncthreads();
+#pragma unroll
+  for (int c = 0; c < kKeyRegs; ++c) {
+    const int i = c * kThreads + tid;
+    if (i < ns) flag[i] = kreg[c] > thresh ? 1 : 0;
+  }
+#pragma unroll
+  for (int c = 0; c < kKeyRegs; ++c) {
+    const int i = c * kThreads + tid;
+    const int64_t sid = (i < ns && kreg[c] > thresh) ? source_ids[i] : -1;
+    if (sid >= 0 && sid < total) inv[sid] = -1;
+  }
+  for (int c = kKeyRegs; c < s_chunks; ++c) {
+    const int i = c * kThreads + tid;
+    if (i < ns) {
+      const bool rm = key(c) > thresh;
+      flag[i] = rm ? 1 : 0;
+      if (rm) {
+        const int64_t sid = source_ids[i];
+        if (sid >= 0 && sid < total) inv[sid] = -1;
+      }
+    }
+  }
+  __syncthreads();
+  uint32_t tie_bits = 0;  // chunks < kKeyRegs
+#pragma unroll
+  for (int c = 0; c < kKeyRegs; ++c)
+    tie_bits |= (c * kThreads + tid < ns && kreg[c] == thresh ? 1u : 0u) << c;
+  ordered_ranks(
+      s_chunks,
+      [&](int c) {
+        if (c < kKeyRegs) return ((tie_bits >> c) & 1u) != 0u;
+        return c * kThreads + tid < ns && key(c) == thresh;
+      },
+      [&](int c, int rank) {
+        if (rank < need_ties) {
+          const int i = c * kThreads + tid;
+          flag[i] = 1;
+          const int64_t sid = source_ids[i];
+          if (sid >= 0 && sid < total) inv[sid] = -1;
+        }
+      },
+      cnt_lds, scan_lds);
 
-  // ---- removed sources point at their target's compact id.
-  for (int i = s_begin; i < s_end; ++i) {
-    const int64_t sid = source_ids[i];
-    if (flag[i] && sid >= 0 && sid < total) {
-      const int32_t d = tb[i];
-      const int64_t dst = (d >= 0 && d < nd) ? dest_ids[d] : -1;
-      inv[sid] = (dst >= 0 && dst < total) ? inv[dst] : -1;
+  // ---- compact ids of kept tokens (ascending), keep list.  Kept flags of the
+  // first 64 token chunks are read once into a bit mask.
+  uint64_t kept_bits = 0;
+  {
+    const int nc = min(t_chunks, 64);
+    for (int c0 = 0; c0 < nc; c0 += 8) {
+      int64_t v[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int t = (c0 + q) * kThreads + tid;
+        v[q] = (c0 + q < nc && t < total) ? inv[t] : -1;
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) kept_bits |= (v[q] == 0 ? 1ull : 0ull) << (c0 + q);
+    }
+  }
+  const int n_keep = total - removed;
+  ordered_ranks(
+      t_chunks,
+      [&](int c) {
+        if (c < 64) return ((kept_bits >> c) & 1ull) != 0ull;
+        const int t = c * kThreads + tid;
+        return t < total && inv[t] == 0;
+      },
+      [&](int c, int rank) {
+        const int t = c * kThreads + tid;
+        inv[t] = rank;
+        if (rank < n_keep) kp[rank] = t;  // always true for a valid (disjoint) source list
+      },
+      cnt_lds, scan_lds);
+
+  // ---- removed sources point at their target's compact id (eight independent
+  // load chains per thread in flight).
+  for (int c0 = 0; c0 < s_chunks; c0 += 8) {
+    int64_t sid[8], dst[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int i = (c0 + q) * kThreads + tid;
+      sid[q] = -1;
+      dst[q] = -1;
+      if (i < ns && flag[i]) {
+        sid[q] = source_ids[i];
+        const int32_t d = tb[i];
+        dst[q] = (d >= 0 && d < nd) ? dest_ids[d] : -1;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      if (sid[q] >= 0 && sid[q] < total) inv[sid[q]] = (dst[q] >= 0 && dst[q] < total) ? inv[dst[q]] : -1;
     }
   }
 }

@@ -12,7 +12,9 @@
 //
 // The score matrix is never materialised.  A work-group computes 128 dict x 128
 // source scores per step on v_mfma_f32_32x32x16_bf16 with both operands staged
-// through LDS in 64-wide K chunks; the accumulators are laid out transposed
+// through double-buffered, XOR-swizzled LDS in 64-wide K chunks (the next
+// chunk -- across dictionary tiles too -- is loaded into registers while the
+// current one is multiplied; one barrier per chunk); the accumulators are laid out transposed
 // (lane = source row, registers = dictionary rows) so each lane folds its 16
 // scores per tile into a register-resident top-K of packed 64-bit keys
 // (orderable bf16 score << 32 | ~j).  Work-groups split the dictionary into
@@ -25,7 +27,6 @@ namespace {
 
 constexpr int kTile = 128;       // dictionary rows and source rows per work-group step
 constexpr int kKc = 64;          // K chunk staged in LDS
-constexpr int kRowE = kKc + 8;   // padded LDS row (elements)
 
 __device__ __forceinline__ uint32_t bf16_bits(float x) {
   const bf16_t b = static_cast<bf16_t>(x);
@@ -39,6 +40,11 @@ __device__ __forceinline__ uint32_t ord16(uint32_t b) {
 }
 __host__ __device__ __forceinline__ uint32_t unord16(uint32_t o) {
   return (o & 0x8000u) ? (o & 0x7FFFu) : (~o & 0xFFFFu);
+}
+
+// fp32 value of x rounded to bf16 (round to nearest even, as the conversion).
+__device__ __forceinline__ float bf16_round(float x) {
+  return __builtin_bit_cast(float, bf16_bits(x) << 16);
 }
 
 __device__ __forceinline__ uint64_t make_key(float score, int j) {
@@ -67,6 +73,13 @@ struct TopK {
   }
 };
 
+// LDS operand tiles: 128 rows x 64 elements (128 B), no padding; the eight
+// 16-byte chunks of a row are XOR-permuted by swz(row) so that the MFMA
+// operand reads (eight consecutive rows at one logical chunk) and the staging
+// stores (eight chunks of one row) fall in distinct banks.
+__device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 7); }
+constexpr int kTileElems = kTile * kKc;
+
 template <int K>
 __global__ __launch_bounds__(256, 2) void sim_topk_kernel(
     const bf16_t* __restrict__ src, int64_t src_stride, int64_t src_capacity,
@@ -75,16 +88,21 @@ __global__ __launch_bounds__(256, 2) void sim_topk_kernel(
     int64_t dict_stride, int n0, int off1, int n_dict, int dim, int tiles_per_part,
     uint64_t* __restrict__ partial, int parts, bf16_t* __restrict__ scores,
     int64_t scores_stride) {
-  __shared__ __attribute__((aligned(16))) bf16_t a_lds[kTile * kRowE];  // dictionary chunk
-  __shared__ __attribute__((aligned(16))) bf16_t b_lds[kTile * kRowE];  // source chunk
+  // Double-buffered dictionary (a) and source (b) chunks.
+  __shared__ __attribute__((aligned(16))) bf16_t a_lds[2 * kTileElems];
+  __shared__ __attribute__((aligned(16))) bf16_t b_lds[2 * kTileElems];
 
   int ns = n_src;
   if (n_src_dev) ns = min(ns, *n_src_dev);
-  const int s0 = blockIdx.x * kTile;
+  // 1-D grid, dictionary part fastest, XCD-remapped: the work-groups resident
+  // on one XCD at a time cover a few source tiles (kept in its L2 across their
+  // dictionary tiles) against all dictionary parts.
+  const int task = xcd_remap(blockIdx.x, gridDim.x);
+  const int s0 = (task / parts) * kTile;
   if (s0 >= ns) return;
-  const int part = blockIdx.y;
+  const int part = task % parts;
   const int d_begin = part * tiles_per_part * kTile;
-  const int d_end = min(n_dict, d_begin + tiles_per_part * kTile);
+  const int d_end = min(n_dict, d_begin + tiles_per_part * kTile);  // may be empty: lists stay empty
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -95,99 +113,182 @@ __global__ __launch_bounds__(256, 2) void sim_topk_kernel(
   const int hh = lane >> 5;
   const bf16x8 zero8 = {};
 
-  // Staging: rows (tid>>3) + 32p, 8 columns at (tid&7)*8, for both operands.
-  const int st_row = tid >> 3;
-  const int st_col = (tid & 7) * 8;
-  int64_t src_off[4];
+  // Staging: rows st + 32p (p = 0..3), chunk sc of the 64-wide K chunk, both operands.
+  const int st = tid >> 3;
+  const int sc = tid & 7;
+  int wr[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) wr[p] = (st + 32 * p) * kKc + ((sc ^ swz(st + 32 * p)) << 3);
+  const bf16_t* src_ptr[4];
   bool src_ok[4];
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
-    const int i = s0 + st_row + 32 * p;
-    int64_t row = i < ns ? (src_rows ? src_rows[i] : i) : -1;
+    const int i = s0 + st + 32 * p;
+    const int64_t row = i < ns ? (src_rows ? src_rows[i] : i) : -1;
     src_ok[p] = row >= 0 && row < src_capacity;  // an invalid row id reads as zeros
-    src_off[p] = (src_ok[p] ? row : 0) * src_stride;
+    src_ptr[p] = src + (src_ok[p] ? row : 0) * src_stride + 8 * sc;
   }
+  // Operand read offsets: row (x*32 + l32) of a 64-row half, logical chunk 2t+hh;
+  // x = 1 uses off[t ^ 2] (swz flips bit 2 of the chunk there).
+  int off[4];
+  {
+    const int s0w = swz(l32);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) off[t] = l32 * kKc + (((2 * t + hh) ^ s0w) << 3);
+  }
+
+  const int n_chunks = (dim + kKc - 1) / kKc;
+  const int n_dtiles = d_end > d_begin ? (d_end - d_begin + kTile - 1) / kTile : 0;
+
+  // Global -> register staging.  Row pointers of the dictionary tile being
+  // loaded are set once per tile; a chunk only adds its column offset.  Rows
+  // and columns past the ends read a valid address and are zeroed when the
+  // registers are stored to LDS, so the loads stay in flight across the MFMAs
+  // of the current chunk.
+  bf16x8 ga[4], gb[4];
+  const bf16_t* dptr[4];
+  unsigned row_mask = 0;  // bit p: dictionary row valid; bit 4+p: source row valid
+  unsigned ok_mask = 0;   // row_mask of the loaded chunk, columns included
+  int ld_dt = 0, ld_kc = 0;
+  auto set_dtile = [&](int dt) {
+    row_mask &= 0xF0u;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int jj = d_begin + dt * kTile + st + 32 * p;
+      const bool ok = jj < d_end;
+      const int row = jj < n0 ? jj : off1 + (jj - n0);
+      dptr[p] = dict + static_cast<int64_t>(ok ? row : 0) * dict_stride + 8 * sc;
+      row_mask |= (ok ? 1u : 0u) << p;
+    }
+  };
+#pragma unroll
+  for (int p = 0; p < 4; ++p) row_mask |= (src_ok[p] ? 1u : 0u) << (4 + p);
+  set_dtile(0);
+  auto load = [&]() {
+    const int kc = ld_kc * kKc;
+    const bool col_ok = kc + 8 * sc < dim;
+    const int col = col_ok ? kc : 0;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      ga[p] = *reinterpret_cast<const bf16x8*>(dptr[p] + col);
+      gb[p] = *reinterpret_cast<const bf16x8*>(src_ptr[p] + col);
+    }
+    ok_mask = col_ok ? row_mask : 0u;
+    if (++ld_kc == n_chunks) {
+      ld_kc = 0;
+      if (++ld_dt < n_dtiles) set_dtile(ld_dt);
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      *reinterpret_cast<bf16x8*>(&a_lds[buf * kTileElems + wr[p]]) = (ok_mask >> p) & 1u ? ga[p] : zero8;
+      *reinterpret_cast<bf16x8*>(&b_lds[buf * kTileElems + wr[p]]) = (ok_mask >> (4 + p)) & 1u ? gb[p] : zero8;
+    }
+  };
 
   TopK<K> best[2];
   best[0].init();
   best[1].init();
+  float top_v[2] = {-__builtin_inff(), -__builtin_inff()};  // K == 1 running best
+  int top_j[2] = {-1, -1};
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) acc[x][y] = f32x16{};
 
-  for (int d0 = d_begin; d0 < d_end; d0 += kTile) {
-    int64_t dict_off[4];
-    bool dict_ok[4];
+  const int n_steps = n_dtiles * n_chunks;
+  load();
+  store(0);
+  __syncthreads();
+  int dt = 0, kcs = 0;  // dictionary tile and K chunk of the step being computed
+  for (int step = 0; step < n_steps; ++step) {
+    const int buf = step & 1;
+    const bool more = step + 1 < n_steps;
+    if (more) load();
+    const bf16_t* al = a_lds + buf * kTileElems + wd * 64 * kKc;
+    const bf16_t* bl = b_lds + buf * kTileElems + ws * 64 * kKc;
+    bf16x8 a[kKc / 16][2], b[kKc / 16][2];
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int j = d0 + st_row + 32 * p;
-      dict_ok[p] = j < d_end;
-      const int row = j < n0 ? j : off1 + (j - n0);
-      dict_off[p] = static_cast<int64_t>(dict_ok[p] ? row : 0) * dict_stride;
-    }
-    f32x16 acc[2][2];
+    for (int t = 0; t < kKc / 16; ++t)
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
-
-    for (int kc = 0; kc < dim; kc += kKc) {
-      const bool col_ok = kc + st_col < dim;
-      bf16x8 av[4], bv[4];
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        av[p] = (dict_ok[p] && col_ok)
-                    ? *reinterpret_cast<const bf16x8*>(dict + dict_off[p] + kc + st_col)
-                    : zero8;
-        bv[p] = (src_ok[p] && col_ok)
-                    ? *reinterpret_cast<const bf16x8*>(src + src_off[p] + kc + st_col)
-                    : zero8;
+      for (int x = 0; x < 2; ++x) {
+        a[t][x] = *reinterpret_cast<const bf16x8*>(al + x * 32 * kKc + off[t ^ (2 * x)]);
+        b[t][x] = *reinterpret_cast<const bf16x8*>(bl + x * 32 * kKc + off[t ^ (2 * x)]);
       }
-      __syncthreads();
 #pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        *reinterpret_cast<bf16x8*>(&a_lds[(st_row + 32 * p) * kRowE + st_col]) = av[p];
-        *reinterpret_cast<bf16x8*>(&b_lds[(st_row + 32 * p) * kRowE + st_col]) = bv[p];
-      }
-      __syncthreads();
+    for (int t = 0; t < kKc / 16; ++t)
 #pragma unroll
-      for (int t = 0; t < kKc / 16; ++t) {
-        bf16x8 a[2], b[2];
+      for (int x = 0; x < 2; ++x)
 #pragma unroll
-        for (int x = 0; x < 2; ++x) {
-          a[x] = *reinterpret_cast<const bf16x8*>(
-              &a_lds[(64 * wd + 32 * x + l32) * kRowE + 16 * t + 8 * hh]);
-          b[x] = *reinterpret_cast<const bf16x8*>(
-              &b_lds[(64 * ws + 32 * x + l32) * kRowE + 16 * t + 8 * hh]);
-        }
+        for (int y = 0; y < 2; ++y)
+          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[t][x], b[t][y], acc[x][y], 0, 0, 0);
+    if (kcs == n_chunks - 1) {
+      // Epilogue of a dictionary tile: lane = source (64*ws + 32*sb + l32),
+      // registers = dictionary rows in increasing order.
+      const int d0 = d_begin + dt * kTile;
+      if (scores) {
 #pragma unroll
-        for (int x = 0; x < 2; ++x)
+        for (int sb = 0; sb < 2; ++sb) {
+          const int i = s0 + 64 * ws + 32 * sb + l32;
 #pragma unroll
-          for (int y = 0; y < 2; ++y)
-            acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[x], b[y], acc[x][y], 0, 0, 0);
-      }
-    }
-
-    // Epilogue: lane = source (64*ws + 32*sb + l32), registers = dictionary rows.
+          for (int db = 0; db < 2; ++db)
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
-      const int i = s0 + 64 * ws + 32 * sb + l32;
-#pragma unroll
-      for (int db = 0; db < 2; ++db) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int j = d0 + 64 * wd + 32 * db + 8 * (r >> 2) + 4 * hh + (r & 3);
-          if (j < d_end) {
-            best[sb].insert(make_key(acc[db][sb][r], j));
-            if (scores && i < ns)
-              scores[static_cast<int64_t>(i) * scores_stride + j] = static_cast<bf16_t>(acc[db][sb][r]);
-          }
+            for (int r = 0; r < 16; ++r) {
+              const int jj = d0 + 64 * wd + 32 * db + 8 * (r >> 2) + 4 * hh + (r & 3);
+              if (jj < d_end && i < ns)
+                scores[static_cast<int64_t>(i) * scores_stride + jj] = static_cast<bf16_t>(acc[db][sb][r]);
+            }
         }
       }
+      const int jl = d0 + 64 * wd + 4 * hh;  // this lane's first dictionary row
+      if (K == 1) {
+        // Running top-1 on the bf16-rounded score: a later (higher) j wins only
+        // when strictly greater, which is the lower-index rule for ties; a NaN
+        // wins over numbers and the first NaN is kept (ranking of the keys).
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+          for (int db = 0; db < 2; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int jj = jl + 32 * db + 8 * (r >> 2) + (r & 3);
+              const float v = bf16_round(acc[db][sb][r]);
+              const bool take = (jj < d_end) & ((v > top_v[sb]) | ((v != v) & (top_v[sb] == top_v[sb])));
+              top_v[sb] = take ? v : top_v[sb];
+              top_j[sb] = take ? jj : top_j[sb];
+            }
+      } else {
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+          for (int db = 0; db < 2; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int jj = jl + 32 * db + 8 * (r >> 2) + (r & 3);
+              if (jj < d_end) best[sb].insert(make_key(acc[db][sb][r], jj));
+            }
+      }
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int db = 0; db < 2; ++db) acc[db][sb] = f32x16{};
+      kcs = 0;
+      ++dt;
+    } else {
+      ++kcs;
     }
+    if (more) store(buf ^ 1);
+    __syncthreads();
   }
 
+  if (K == 1) {
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb)
+      if (top_j[sb] >= 0) best[sb].k[0] = make_key(top_v[sb], top_j[sb]);
+  }
   // Merge the four lists of every source row (two dictionary halves x two lane halves).
-  __syncthreads();
   uint64_t* m_lds = reinterpret_cast<uint64_t*>(a_lds);  // [128 sources][4 lists][K]
 #pragma unroll
   for (int sb = 0; sb < 2; ++sb) {
@@ -245,14 +346,41 @@ __global__ __launch_bounds__(256) void topk_finalize_kernel(
   }
 }
 
-int choose_parts(int64_t n_src, int64_t n_dict) {
+// Resident work-groups of sim_topk_kernel<K> on the current device, cached.
+template <int K>
+int64_t resident_groups() {
+  static int cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
+  if (cache[dev] == 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, sim_topk_kernel<K>, 256, 0) != hipSuccess)
+      return 512;
+    cache[dev] = cus * (per_cu > 0 ? per_cu : 1);
+  }
+  return cache[dev];
+}
+
+// Dictionary split: the number of parts that minimises (rounds of resident
+// work-groups) x (dictionary tiles per work-group + a half-tile fixed cost).
+int choose_parts(int64_t n_src, int64_t n_dict, int topk) {
   const int64_t src_tiles = (n_src + kTile - 1) / kTile;
   const int64_t dict_tiles = (n_dict + kTile - 1) / kTile;
-  // Aim for about 1024 work-groups (4 per CU) without splitting below one tile.
-  int64_t parts = (1024 + src_tiles - 1) / (src_tiles > 0 ? src_tiles : 1);
-  if (parts > dict_tiles) parts = dict_tiles;
-  if (parts < 1) parts = 1;
-  return static_cast<int>(parts);
+  if (src_tiles <= 0 || dict_tiles <= 0) return 1;
+  const int64_t slots = topk == 1 ? resident_groups<1>() : resident_groups<4>();
+  int best = 1;
+  double best_cost = 1e300;
+  for (int64_t p = 1; p <= dict_tiles && p <= 4096; ++p) {
+    const int64_t rounds = (src_tiles * p + slots - 1) / slots;
+    const int64_t tpp = (dict_tiles + p - 1) / p;
+    const double cost = static_cast<double>(rounds) * (static_cast<double>(tpp) + 0.5);
+    if (cost < best_cost) {
+      best_cost = cost;
+      best = static_cast<int>(p);
+    }
+  }
+  return best;
 }
 
 }  // namespace
@@ -263,7 +391,7 @@ extern "C" int vgo_similarity_topk_workspace(int64_t n_src, int64_t n_dict, int 
   using namespace vgo;
   VGO_REQUIRE(topk == 1 || topk == 4, "similarity_topk: topk must be 1 or 4");
   VGO_REQUIRE(n_src >= 0 && n_dict >= 0, "similarity_topk: negative size");
-  const int p = choose_parts(n_src, n_dict);
+  const int p = choose_parts(n_src, n_dict, topk);
   if (parts) *parts = p;
   if (bytes) *bytes = static_cast<size_t>(n_src) * p * topk * sizeof(uint64_t);
   return VGO_OK;
@@ -299,7 +427,9 @@ extern "C" int vgo_similarity_topk(const void* src, int64_t src_row_stride, int6
   const int64_t dict_tiles = (n_dict + kTile - 1) / kTile;
   const int tiles_per_part = static_cast<int>((dict_tiles + parts - 1) / parts);
   hipStream_t s = as_stream(stream);
-  dim3 grid(static_cast<unsigned>((n_src + kTile - 1) / kTile), static_cast<unsigned>(parts));
+  const int64_t src_tiles = (n_src + kTile - 1) / kTile;
+  VGO_REQUIRE(src_tiles * parts < (1LL << 31), "similarity_topk: grid too large");
+  dim3 grid(static_cast<unsigned>(src_tiles * parts));
   uint64_t* partial = static_cast<uint64_t*>(workspace);
   const bf16_t* sp = static_cast<const bf16_t*>(src);
   const bf16_t* dp = static_cast<const bf16_t*>(dict);

@@ -130,7 +130,8 @@ def test_streaming_top4_api(vgo, device):
 
 # ------------------------------------------------------ rank and select ----
 @pytest.mark.parametrize("batch,ns,nd,removed", [(1, 50, 20, 1), (2, 3000, 900, 1700),
-                                                 (1, 5000, 100, 5000), (1, 20000, 7000, 12345)])
+                                                 (1, 5000, 100, 5000), (1, 20000, 7000, 12345),
+                                                 (1, 70000, 3000, 40000)])
 def test_fastvggt_assemble_exact(vgo, kern, device, batch, ns, nd, removed):
     print(f"[assemble] batch={batch} ns={ns} removed={removed}", flush=True)
     g = torch.Generator().manual_seed(ns + removed)
