@@ -26,9 +26,12 @@
 //    sum is accumulated from those rounded values with v_dot2 (fp32 accumulate).
 //  * The O / row-sum rescale runs only when some lane's running max moved
 //    (otherwise its factor is exactly 1, so skipping it changes no bit).
-//  * Scheduling: the (task, key tile) units of a call are split evenly over
-//    the work-groups the chip holds at once (stream-K); tasks cut between two
-//    work-groups are finished by attn_merge_kernel from fp32 partial states.
+//  * Scheduling: with G work-groups resident at once, every work-group runs
+//    whole tasks w, w+G, ... for floor(tasks/G) rounds (neighbouring groups,
+//    i.e. one XCD's, share a head's K/V in L2), and the (task, key tile)
+//    units of the remaining tasks are split evenly over all G (stream-K on
+//    the last round only); tasks cut between work-groups are finished by
+//    attn_merge_kernel from fp32 partial states.
 // fp32 path: exact fp32 arithmetic, one query row per lane, K/V tiles in LDS.
 #include <algorithm>
 #include <type_traits>
@@ -117,7 +120,12 @@ struct AttnArgs {
   T* out;
   float* partial;  // stream-K partial states, 2 per work-group (may be null)
   int heads, nq, nk, n_qblocks, ntiles;
-  int64_t units, groups;  // stream-K: `units` (task, tile) pairs over `groups` work-groups
+  // Schedule: `groups` work-groups; work-group w first runs the whole tasks
+  // w, w + groups, ... (`full_rounds` of them), then its share of the
+  // (task, key tile) units of the remaining tasks tail_task0.. (`units` in
+  // all, split evenly over the first `tail_groups` work-groups: stream-K on
+  // the last round only).
+  int64_t units, groups, full_rounds, tail_task0, tail_groups;
   int64_t qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn, osb, osh, osn;
   float c;  // log2(e) / 8: S'' -> exp2 domain
 };
@@ -365,14 +373,25 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attn_mfma_kernel(AttnArgs<T> a
   __shared__ __attribute__((aligned(16))) T vt_lds[2 * kTileElems];
   __shared__ __attribute__((aligned(16))) T b_lds[2 * kBN];
   const int64_t w = xcd_remap(blockIdx.x, gridDim.x);
-  int64_t u = sk_begin(w, a.units, a.groups);
-  const int64_t u_end = sk_begin(w + 1, a.units, a.groups);
+  // Whole tasks: consecutive work-groups (one XCD's, after the remap) take
+  // consecutive tasks of a round, so they stream one head's K/V in step and
+  // share it in that XCD's L2.
+  for (int64_t r = 0; r < a.full_rounds; ++r) {
+    const int64_t task = w + r * a.groups;
+    const int bh = static_cast<int>(task / a.n_qblocks);
+    const int qblk = static_cast<int>(task - static_cast<int64_t>(bh) * a.n_qblocks);
+    attn_segment<T>(a, k_lds, vt_lds, b_lds, bh, qblk, 0, a.ntiles, nullptr);
+  }
+  if (w >= a.tail_groups) return;
+  int64_t u = sk_begin(w, a.units, a.tail_groups);
+  const int64_t u_end = sk_begin(w + 1, a.units, a.tail_groups);
   bool first = true;
   while (u < u_end) {
-    const int64_t task = u / a.ntiles;
-    const int tile0 = static_cast<int>(u - task * a.ntiles);
-    const int64_t seg_end = min(u_end, (task + 1) * a.ntiles);
-    const int tile1 = static_cast<int>(seg_end - task * a.ntiles);
+    const int64_t tt = u / a.ntiles;  // tail task
+    const int tile0 = static_cast<int>(u - tt * a.ntiles);
+    const int64_t seg_end = min(u_end, (tt + 1) * a.ntiles);
+    const int tile1 = static_cast<int>(seg_end - tt * a.ntiles);
+    const int64_t task = a.tail_task0 + tt;
     const int bh = static_cast<int>(task / a.n_qblocks);
     const int qblk = static_cast<int>(task - static_cast<int64_t>(bh) * a.n_qblocks);
     float* partial = nullptr;
@@ -384,52 +403,71 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attn_mfma_kernel(AttnArgs<T> a
   }
 }
 
-// Combines the partial states of every task split across work-groups.  Block
-// j handles the task that starts inside the range of work-group j (if that
-// task is split); 16 threads per query, 4 dims each.
+// Combines the partial states of every tail task split across work-groups.
+// Block b handles tail task b / kMergeSplit, queries (b % kMergeSplit) *
+// kQBlock / kMergeSplit onwards; 16 threads per query, 4 dims each.  Partial
+// states are read eight at a time so their loads overlap.
+constexpr int kMergeSplit = 8;
 template <typename T>
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs<T> a) {
-  const int64_t w0 = blockIdx.x;
-  const int64_t ub = sk_begin(w0, a.units, a.groups);
-  const int64_t ue = sk_begin(w0 + 1, a.units, a.groups);
-  if (ub >= ue) return;
-  // Only the last task that starts inside [ub, ue) can continue past ue.
-  const int64_t task = (ue - 1) / a.ntiles;
-  const int64_t t0 = task * a.ntiles;
-  if (t0 < ub) return;  // no task starts here
-  const int64_t w1 = sk_owner(t0 + a.ntiles - 1, a.units, a.groups);
-  if (w1 == w0) return;  // whole inside w0: already written
-  const int first_slot = ub < t0 ? 1 : 0;  // w0's segment is its last (or only) one
+  const int64_t tt = blockIdx.x / kMergeSplit;
+  const int qpart = blockIdx.x % kMergeSplit;
+  const int64_t t0 = tt * a.ntiles;
+  const int64_t w0 = sk_owner(t0, a.units, a.tail_groups);
+  const int64_t w1 = sk_owner(t0 + a.ntiles - 1, a.units, a.tail_groups);
+  if (w1 == w0) return;  // whole inside one work-group: already written
+  const int first_slot = sk_begin(w0, a.units, a.tail_groups) < t0 ? 1 : 0;
+  const int64_t task = a.tail_task0 + tt;
   const int bh = static_cast<int>(task / a.n_qblocks);
   const int qblk = static_cast<int>(task - static_cast<int64_t>(bh) * a.n_qblocks);
   const int b = bh / a.heads;
   const int h = bh - b * a.heads;
   T* ob_ptr = a.out + b * a.osb + h * a.osh;
   const int d0 = (threadIdx.x & 15) * 4;
-  for (int ql = threadIdx.x >> 4; ql < kQBlock; ql += 16) {
+  auto slot_ptr = [&](int64_t w) {
+    const int slot = w == w0 ? first_slot : 0;
+    return a.partial + (2 * w + slot) * static_cast<int64_t>(kPartialFloats);
+  };
+  for (int ql = qpart * (kQBlock / kMergeSplit) + (threadIdx.x >> 4);
+       ql < (qpart + 1) * (kQBlock / kMergeSplit); ql += 16) {
     const int row = qblk * kQBlock + ql;
     if (row >= a.nq) break;
     float mmax = -__builtin_inff();
-    for (int64_t w = w0; w <= w1; ++w) {
-      const int slot = w == w0 ? first_slot : 0;
-      const float* p = a.partial + (2 * w + slot) * static_cast<int64_t>(kPartialFloats);
-      mmax = fmaxf(mmax, p[kQBlock * kD + ql]);
+    for (int64_t wb = w0; wb <= w1; wb += 8) {
+      float mv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mv[e] = wb + e <= w1 ? slot_ptr(wb + e)[kQBlock * kD + ql] : -__builtin_inff();
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mmax = fmaxf(mmax, mv[e]);
     }
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     float l = 0.0f;
-    for (int64_t w = w0; w <= w1; ++w) {
-      const int slot = w == w0 ? first_slot : 0;
-      const float* p = a.partial + (2 * w + slot) * static_cast<int64_t>(kPartialFloats);
-      const float f = __builtin_amdgcn_exp2f((p[kQBlock * kD + ql] - mmax) * a.c);
-      const f32x4 x = *reinterpret_cast<const f32x4*>(p + ql * kD + d0);
+    for (int64_t wb = w0; wb <= w1; wb += 8) {
+      float mv[8], lv[8];
+      f32x4 xv[8];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc[e] = fmaf(x[e], f, acc[e]);
-      l = fmaf(p[kQBlock * kD + kQBlock + ql], f, l);
+      for (int e = 0; e < 8; ++e) {
+        if (wb + e <= w1) {
+          const float* p = slot_ptr(wb + e);
+          mv[e] = p[kQBlock * kD + ql];
+          lv[e] = p[kQBlock * kD + kQBlock + ql];
+          xv[e] = *reinterpret_cast<const f32x4*>(p + ql * kD + d0);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (wb + e <= w1) {
+          const float f = __builtin_amdgcn_exp2f((mv[e] - mmax) * a.c);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) acc[q] = fmaf(xv[e][q], f, acc[q]);
+          l = fmaf(lv[e], f, l);
+        }
+      }
     }
     typedef typename Mma<T>::op4 op4;
     op4 val;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) val[e] = static_cast<T>(acc[e] / l);
+    for (int q = 0; q < 4; ++q) val[q] = static_cast<T>(acc[q] / l);
     *reinterpret_cast<op4*>(ob_ptr + row * a.osn + d0) = val;
   }
 }
@@ -560,30 +598,40 @@ int launch_mfma(const void* q, const void* k, const void* v, const void* bias, v
   a.nk = static_cast<int>(nk);
   a.n_qblocks = static_cast<int>(n_qblocks);
   a.ntiles = static_cast<int>(ntiles);
-  a.units = tasks * ntiles;
   a.groups = tasks;
+  a.full_rounds = 1;
+  a.tail_task0 = tasks;
+  a.units = 0;
+  a.tail_groups = 0;
   a.qsb = qs[0], a.qsh = qs[1], a.qsn = qs[2];
   a.ksb = ks[0], a.ksh = ks[1], a.ksn = ks[2];
   a.vsb = vs[0], a.vsh = vs[1], a.vsn = vs[2];
   a.osb = os[0], a.osh = os[1], a.osn = os[2];
   a.c = kLog2e / 8.0f;
   if (split) {
-    const int64_t groups = stream_groups<T>(tasks, a.units);
+    const int64_t groups = stream_groups<T>(tasks, tasks * ntiles);
     if (groups > 0) {
       const size_t need = static_cast<size_t>(groups) * 2 * kPartialFloats * sizeof(float);
       if (workspace == nullptr || workspace_bytes < need)
         return fail(VGO_EWORKSPACE, "mass_bias_attention: workspace too small");
       VGO_REQUIRE(aligned(workspace, 16), "mass_bias_attention: workspace must be 16-byte aligned");
       a.groups = groups;
+      a.full_rounds = tasks / groups;
+      a.tail_task0 = a.full_rounds * groups;
+      a.units = (tasks - a.tail_task0) * ntiles;
+      // At most ~8 pieces per tail task: a work-group takes >= ntiles/8 key tiles.
+      const int64_t min_units = std::max<int64_t>(kMinUnitsPerGroup, (ntiles + 7) / 8);
+      a.tail_groups = std::min<int64_t>(groups, std::max<int64_t>(1, a.units / min_units));
       a.partial = static_cast<float*>(workspace);
     }
   }
   hipLaunchKernelGGL((attn_mfma_kernel<T>), dim3(static_cast<unsigned>(a.groups)), dim3(kWaves * 64),
                      0, stream, a);
   int status = check_launch("mass_bias_attention");
-  if (status != VGO_OK || a.partial == nullptr) return status;
-  hipLaunchKernelGGL((attn_merge_kernel<T>), dim3(static_cast<unsigned>(a.groups)), dim3(256), 0,
-                     stream, a);
+  if (status != VGO_OK || a.partial == nullptr || a.units == 0) return status;
+  const int64_t tail_tasks = a.units / ntiles;
+  hipLaunchKernelGGL((attn_merge_kernel<T>), dim3(static_cast<unsigned>(tail_tasks * kMergeSplit)),
+                     dim3(256), 0, stream, a);
   return check_launch("mass_bias_attention(merge)");
 }
 

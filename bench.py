@@ -312,6 +312,52 @@ def cpu_baseline(budget_s: float = 30.0):
                         "proj_restore_mlp": t_tail, "frame_block_scaled": t_frame}}
 
 
+# ----------------------------------------------------- counter workloads ----
+TRAFFIC_PROFILE = ROOT / "profiles" / "c4_attention_hbm_traffic.md"
+
+
+def attention_traffic() -> int | None:
+    """HBM bytes per C4 attention launch from the committed rocprofv3 counter summary.
+
+    FETCH_SIZE and WRITE_SIZE of the kernel (two --pmc passes), each scaled by
+    what the counter reads for a plain copy of known size; the summary holds the
+    raw counters, the calibration and a `traffic_bytes_per_launch = N` line.
+    """
+    try:
+        for line in TRAFFIC_PROFILE.read_text().splitlines():
+            if line.strip().startswith("traffic_bytes_per_launch"):
+                return int(line.split("=", 1)[1].strip().replace(",", ""))
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def only_workload(which: str) -> int:
+    device = torch.device("cuda", 0)
+    if which == "copy":
+        n = 256 * 1024 * 1024
+        src = torch.empty(n, dtype=torch.uint8, device=device).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"workload": "copy", "bytes": n, "launches": 3}), flush=True)
+        return 0
+    vgo = importlib.import_module("4d_ttt_merging_amd")
+    n = 16464  # C4 compacted tokens
+    g = torch.Generator().manual_seed(5)
+    q = (torch.randn(1, HEADS, n, 64, generator=g) * 0.125).bfloat16().to(device)
+    k = (torch.randn(1, HEADS, n, 64, generator=g) * 0.125).bfloat16().to(device)
+    v = torch.randn(1, HEADS, n, 64, generator=g).bfloat16().to(device)
+    mass = torch.randint(1, 9, (n,), generator=g).float().log().to(device)
+    for _ in range(3):
+        vgo.mass_bias_attention(q, k, v, mass)
+    torch.cuda.synchronize()
+    print(json.dumps({"workload": "attention", "heads": HEADS, "n_query": n, "n_key": n,
+                      "launches": 3}), flush=True)
+    return 0
+
+
 # --------------------------------------------------------------------- main ----
 def main() -> int:
     ap = argparse.ArgumentParser()
@@ -320,11 +366,17 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-reference", action="store_true")
+    ap.add_argument("--only", choices=("attention", "copy"), default=None,
+                    help="run one kernel workload for rocprofv3 counter passes, then exit: "
+                         "'attention' = 3 C4-size mass-bias attention launches, 'copy' = 3 "
+                         "plain 256 MiB device copies (the FETCH_SIZE / WRITE_SIZE calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
               f"--gpus {args.gpus}); run with --gpus 1", file=sys.stderr, flush=True)
         return 2
+    if args.only:
+        return only_workload(args.only)
     vgo = importlib.import_module("4d_ttt_merging_amd")
     agg = importlib.import_module("4d_ttt_merging_amd.aggregator")
     prof = importlib.import_module("4d_ttt_merging_amd.profiling")
@@ -377,7 +429,7 @@ def main() -> int:
                      "achieved": round(attn_flops / (attn_ms / 1e3) / 1e12, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(attn_flops / (attn_ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None, "flops_per_launch": attn_flops,
+                     "traffic": attention_traffic(), "flops_per_launch": attn_flops,
                      "avg_launch_ms": round(attn_ms, 4)},
         "global_block_ms": round(block_ms, 3),
         "global_block_breakdown_ms": breakdown,
