@@ -18,14 +18,19 @@
 //    and 16 keys of every 32-key sub-tile: the row max/sum of the online
 //    softmax stay in registers except for one v_permlane32_swap, and the
 //    exponentiated scores are already laid out as the B operand of O^T = V^T P^T.
-//  * The per-key bias rides in the MFMA: a fifth k-step multiplies a Q-side
-//    column of ones with a K-side column holding 8*log(m) (exact in bf16/f16),
-//    so S'' = q.k + 8 log m and logit*log2(e) = S'' * log2(e)/8.  The reference
-//    rounds log(m) to the input dtype first (mass_bias_attention.py:109); so do
-//    we.  P is rounded to the input dtype before P.V (reference :74) and the row
-//    sum is accumulated from those rounded values with v_dot2 (fp32 accumulate).
-//  * The O / row-sum rescale runs only when some lane's running max moved
-//    (otherwise its factor is exactly 1, so skipping it changes no bit).
+//  * Q is scaled by log2(e)/8 as it is loaded (rounded to the input dtype), so
+//    the MFMA yields logits in the exp2 domain.  The per-key bias and the
+//    softmax offset ride in the MFMA too: a fifth k-step multiplies the
+//    key-side column pair (hi, lo) = log2(e)*log m split into two input-dtype
+//    values (exact to ~2^-17) and a column of ones with the query-side
+//    (1, 1, -mref).  The reference rounds log(m) to the input dtype first
+//    (mass_bias_attention.py:109); so do we.
+//  * Lazy online softmax: P = 2^S straight from the accumulator while no
+//    logit exceeds the reference max mref by more than 8 (checked through the
+//    per-lane sums); only then, and on a segment's first tile, are the tile's
+//    logits recomputed, mref moved and O / the row sum rescaled.  P is rounded
+//    to the input dtype before P.V (reference :74) and the row sum is
+//    accumulated from those rounded values with v_dot2 (fp32 accumulate).
 //  * Scheduling: with G work-groups resident at once, every work-group runs
 //    whole tasks w, w+G, ... for floor(tasks/G) rounds (neighbouring groups,
 //    i.e. one XCD's, share a head's K/V in L2), and the (task, key tile)
@@ -111,6 +116,32 @@ __device__ __forceinline__ int vt_pos(int kk) {
 // written by one store, all fall in distinct banks.
 __device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 7); }
 
+// ------------------------------------------------------------ LDS DMA ----
+// global_load_lds_dword{,x4}: lane i of the wave writes 4 (16) bytes at LDS
+// byte address M0 + 4i (16i).  Issued from inline asm so the compiler does not
+// track these loads (its tracking would wait for all of them before any LDS
+// read); the kernel waits for them itself with s_waitcnt vmcnt.  None of this
+// library's kernels otherwise uses M0.  An SALU write of M0 needs one wait
+// state before an LDS-DMA instruction reads it (the s_nop).
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  typedef const __attribute__((address_space(3))) char* lds_ptr;
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr)(p)));
+}
+__device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :: "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(g) : "memory");
+}
+__device__ __forceinline__ void lds_dma4(const void* g, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
+               :: "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(g) : "memory");
+}
+// Wait until at most N vector-memory operations of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
 template <typename T>
 struct AttnArgs {
   const T* q;
@@ -127,7 +158,13 @@ struct AttnArgs {
   // the last round only).
   int64_t units, groups, full_rounds, tail_task0, tail_groups;
   int64_t qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn, osb, osh, osn;
-  float c;  // log2(e) / 8: S'' -> exp2 domain
+  float c;  // log2(e) / 8, folded into Q
+  // LDS-DMA kernel only: V^T packed per (batch*head) as [64][npad] in the MFMA
+  // key order, and per key the pair (hi, lo) = log2(e)*bias split into two T
+  // values ((-inf, 0) past n_key), 2*npad long.
+  const T* vt;
+  const T* bias2;
+  int npad;
 };
 
 // First unit of work-group w under the static stream-K partition.
@@ -139,7 +176,14 @@ __host__ __device__ __forceinline__ int64_t sk_owner(int64_t u, int64_t units, i
   return ((u + 1) * groups - 1) / units;
 }
 
-template <typename T>
+// LDS stages: 2 (register-staged kernel) or 3 (DMA kernel); a stage holds a
+// K tile, a V^T tile and the tile's 64 bias pairs (hi, lo).
+constexpr int kBiasSlot = 2 * kBN;
+// Largest per-lane sum of 32 probabilities the lazy softmax accepts without
+// moving its reference max (bounds every P by 2^8).
+constexpr float kLazyLimit = 256.0f;
+
+template <typename T, bool kDma>
 __device__ __forceinline__ void attn_segment(const AttnArgs<T>& a, T* k_lds, T* vt_lds, T* b_lds,
                                              int bh, int qblk, int tile0, int tile1, float* partial) {
   typedef typename Mma<T>::op8 op8;
@@ -158,19 +202,39 @@ __device__ __forceinline__ void attn_segment(const AttnArgs<T>& a, T* k_lds, T* 
   const T* kb_ptr = a.k + b * a.ksb + h * a.ksh;
   const T* vb_ptr = a.v + b * a.vsb + h * a.vsh;
 
-  // Q rows as MFMA B operands (rows past n_query read a valid row; never stored).
+  // Q' = Q * log2(e)/8 rounded to T, as MFMA B operands (rows past n_query
+  // read a valid row; never stored): K Q'^T is then in the exp2 domain.
   op8 qreg[kQB][4];
 #pragma unroll
   for (int qb = 0; qb < kQB; ++qb) {
     const int row = min(qw0 + qb * 32 + l32, a.nq - 1);
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
-      qreg[qb][t] = *reinterpret_cast<const op8*>(qb_ptr + row * a.qsn + 16 * t + 8 * hh);
+    for (int t = 0; t < 4; ++t) {
+      const op8 raw = *reinterpret_cast<const op8*>(qb_ptr + row * a.qsn + 16 * t + 8 * hh);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qreg[qb][t][e] = static_cast<T>(to_f32(raw[e]) * a.c);
+    }
   }
-  const op8 zero8 = {};
-  op8 qone = zero8;
-  qone[0] = hh == 0 ? static_cast<T>(1.0f) : static_cast<T>(0.0f);
   const op2 ones2 = {static_cast<T>(1.0f), static_cast<T>(1.0f)};
+
+  // The bias k-step.  A (keys; lanes 0-31 hold k-slots 0-7 of key l32, lanes
+  // 32-63 slots 8-15): {bias_hi, bias_lo, 1, 0, ...}, the key's log2(e)*bias
+  // split into two T values.  B (queries): {1, 1, -offset, 0, ...}, where the
+  // offset is the query's running reference max (a T value).
+  const uint32_t low_lanes = hh == 0 ? 0xffffffffu : 0u;
+  const uint32_t one_bits = __builtin_bit_cast(uint16_t, static_cast<T>(1.0f));
+  auto bias_a = [&](const T* bl, int sub) {
+    const uint32_t bw = *reinterpret_cast<const uint32_t*>(bl + 2 * (sub * 32 + l32));
+    const i32x4 w = {static_cast<int>(bw & low_lanes), static_cast<int>(one_bits & low_lanes), 0, 0};
+    return __builtin_bit_cast(op8, w);
+  };
+  auto offset_b = [&](float offset) {
+    const uint32_t neg = __builtin_bit_cast(uint16_t, static_cast<T>(-offset));
+    const i32x4 w = {static_cast<int>((one_bits | (one_bits << 16)) & low_lanes),
+                     static_cast<int>(neg & low_lanes), 0, 0};
+    return __builtin_bit_cast(op8, w);
+  };
+  const op8 no_offset = offset_b(0.0f);
 
   // Per-lane LDS read offsets (elements) of logical chunk pair t of row l32;
   // row l32 + 32 uses off[t ^ 2] (swz flips bit 2 of the chunk there).
@@ -180,130 +244,112 @@ __device__ __forceinline__ void attn_segment(const AttnArgs<T>& a, T* k_lds, T* 
 #pragma unroll
     for (int t = 0; t < 4; ++t) off[t] = l32 * kD + (((2 * t + hh) ^ s0) << 3);
   }
-
-  // Staging roles.  K: rows st and st+32, chunk sc.  V: keys 2st, 2st+1, dims 8sc..8sc+7.
-  const int st = tid >> 3;
-  const int sc = tid & 7;
-  const int kw0 = st * kD + ((sc ^ swz(st)) << 3);
-  const int kw1 = (st + 32) * kD + ((sc ^ swz(st + 32)) << 3);
-  const int vpos = vt_pos(2 * st);
-  const int vphys = (vpos >> 3) ^ sc;  // chunk of dim 8sc+i is vphys ^ i
-  const int vbase = 8 * sc * kD + (vpos & 7);
   const int last_key = a.nk - 1;
-  // Row offsets fit in 32 bits (checked on the host): one multiply per row.
   const int ksn = static_cast<int>(a.ksn), vsn = static_cast<int>(a.vsn);
-  const T* kcol = kb_ptr + 8 * sc;
-  const T* vcol = vb_ptr + 8 * sc;
 
-  // The next tile's rows are loaded into registers while the current tile is
-  // computed (rows past n_key read a valid row; their bias is -inf).
-  op8 pk0, pk1, pv0, pv1;
-  T pb = static_cast<T>(0.0f);
-  auto stage_load = [&](int tile) {
-    const int kt = tile * kBN;
-    pk0 = *reinterpret_cast<const op8*>(kcol + min(kt + st, last_key) * ksn);
-    pk1 = *reinterpret_cast<const op8*>(kcol + min(kt + st + 32, last_key) * ksn);
-    pv0 = *reinterpret_cast<const op8*>(vcol + min(kt + 2 * st, last_key) * vsn);
-    pv1 = *reinterpret_cast<const op8*>(vcol + min(kt + 2 * st + 1, last_key) * vsn);
-    if (a.bias) pb = a.bias[min(kt + lane, last_key)];
-  };
-  // Every wave writes the same 64 bias values (branch-free; identical data).
-  auto stage_store = [&](int tile, int buf) {
-    T* kl = k_lds + buf * kTileElems;
-    T* vl = vt_lds + buf * kTileElems;
-    *reinterpret_cast<op8*>(kl + kw0) = pk0;
-    *reinterpret_cast<op8*>(kl + kw1) = pk1;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const op2 pr = {pv0[i], pv1[i]};
-      *reinterpret_cast<op2*>(vl + vbase + i * kD + ((vphys ^ i) << 3)) = pr;
-    }
-    const bool valid = tile * kBN + lane < a.nk;
-    const float bv = a.bias ? 8.0f * to_f32(pb) : 0.0f;
-    b_lds[buf * kBN + lane] = static_cast<T>(valid ? bv : -__builtin_inff());
-  };
-
-  float m[kQB], lsum[kQB];
+  // Online-softmax state per query: the reference max `mref` (a T value, -inf
+  // until a finite logit is seen), the running sum and O, both relative to
+  // 2^mref.  qoff carries -mref into the bias k-step.
+  float mref[kQB], lsum[kQB];
+  op8 qoff[kQB];
   f32x16 o[kQB][2];
 #pragma unroll
   for (int qb = 0; qb < kQB; ++qb) {
-    m[qb] = -__builtin_inff();
+    mref[qb] = -__builtin_inff();
+    qoff[qb] = offset_b(mref[qb]);
     lsum[qb] = 0.0f;
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[qb][dt][r] = 0.0f;
+    for (int dt = 0; dt < 2; ++dt) o[qb][dt] = f32x16{};
   }
 
-  stage_load(tile0);
-  stage_store(tile0, 0);
-  __syncthreads();
+  // P = exp2(x - shift) rounded to T and packed as the four B operands of
+  // O^T += V^T P^T; returns this lane's sum of the rounded values.
+  auto exp_pack = [&](const f32x16 (&x)[2], float shift, op8 (&p)[4]) {
+    float part = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      i32x4 packed;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = (t & 1) * 8 + 2 * j;
+        const op2 pr = {static_cast<T>(__builtin_amdgcn_exp2f(x[t >> 1][r] - shift)),
+                        static_cast<T>(__builtin_amdgcn_exp2f(x[t >> 1][r + 1] - shift))};
+        part = Mma<T>::dot2(pr, ones2, part);
+        packed[j] = __builtin_bit_cast(int, pr);
+      }
+      p[t] = __builtin_bit_cast(op8, packed);
+    }
+    return part;
+  };
 
-  for (int tile = tile0; tile < tile1; ++tile) {
-    const int buf = (tile - tile0) & 1;
-    const bool more = tile + 1 < tile1;
-    if (more) stage_load(tile + 1);
-    const T* kl = k_lds + buf * kTileElems;
-    const T* vl = vt_lds + buf * kTileElems;
-
-    // S^T = K' Q'^T for two 32-key sub-tiles, bias in a fifth k-step.
+  // One 64-key tile from LDS (K at kl, V^T at vl, bias pairs at bl).
+  auto compute_tile = [&](const T* kl, const T* vl, const T* bl) {
+    // S^T = K Q'^T + log2(e) bias - mref for two 32-key sub-tiles.
     f32x16 s[kQB][2];
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
 #pragma unroll
-      for (int qb = 0; qb < kQB; ++qb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[qb][sub][r] = 0.0f;
+      for (int qb = 0; qb < kQB; ++qb) s[qb][sub] = f32x16{};
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const op8 ka = *reinterpret_cast<const op8*>(kl + sub * 32 * kD + off[t ^ (2 * sub)]);
 #pragma unroll
         for (int qb = 0; qb < kQB; ++qb) s[qb][sub] = Mma<T>::mma(ka, qreg[qb][t], s[qb][sub]);
       }
-      const T bv = b_lds[buf * kBN + sub * 32 + l32];
-      op8 ba = zero8;
-      ba[0] = hh == 0 ? bv : static_cast<T>(0.0f);
+      const op8 ba = bias_a(bl, sub);
 #pragma unroll
-      for (int qb = 0; qb < kQB; ++qb) s[qb][sub] = Mma<T>::mma(ba, qone, s[qb][sub]);
+      for (int qb = 0; qb < kQB; ++qb) s[qb][sub] = Mma<T>::mma(ba, qoff[qb], s[qb][sub]);
     }
 
-    // Online softmax in the exp2 domain.  The O/l rescale is skipped when no
-    // lane's running max moved (the factor would be exactly 1).
+    // Lazy online softmax.  P = 2^S directly while every lane's sum of its 32
+    // probabilities stays <= 2^8 (so no logit exceeds mref by more than 8):
+    // the reference max then need not move.  Otherwise (and on the first tile,
+    // when mref = -inf makes S non-finite) the tile's logits are recomputed
+    // without the offset, mref moves to the T value nearest the running max,
+    // O and the sum are rescaled, and P is recomputed.
     op8 p[kQB][4];
+    float part[kQB];
 #pragma unroll
-    for (int qb = 0; qb < kQB; ++qb) {
-      float mx = s[qb][0][0];
+    for (int qb = 0; qb < kQB; ++qb) part[qb] = exp_pack(s[qb], 0.0f, p[qb]);
+    if (__builtin_expect(__ballot(!(part[0] <= kLazyLimit) | !(part[1] <= kLazyLimit)) != 0, 0)) {
+      // Reload K here rather than keep the fast path's operands alive.
+      asm volatile("" ::: "memory");
 #pragma unroll
-      for (int sub = 0; sub < 2; ++sub)
+      for (int qb = 0; qb < kQB; ++qb) {
+        f32x16 x[2];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[qb][sub][r]);
-      const float mnew = fmaxf(m[qb], half_max(mx));
-      if (__ballot(mnew > m[qb])) {
-        const float corr = __builtin_amdgcn_exp2f((m[qb] - mnew) * a.c);
-        lsum[qb] *= corr;
+        for (int sub = 0; sub < 2; ++sub) {
+          x[sub] = f32x16{};
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) o[qb][dt][r] *= corr;
-        m[qb] = mnew;
-      }
-      const float mc = m[qb] * a.c;
-      float part = 0.0f;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        i32x4 packed;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int r = (t & 1) * 8 + 2 * j;
-          const op2 pr = {static_cast<T>(__builtin_amdgcn_exp2f(fmaf(s[qb][t >> 1][r], a.c, -mc))),
-                          static_cast<T>(__builtin_amdgcn_exp2f(fmaf(s[qb][t >> 1][r + 1], a.c, -mc)))};
-          part = Mma<T>::dot2(pr, ones2, part);
-          packed[j] = __builtin_bit_cast(int, pr);
+          for (int t = 0; t < 4; ++t) {
+            const op8 ka = *reinterpret_cast<const op8*>(kl + sub * 32 * kD + off[t ^ (2 * sub)]);
+            x[sub] = Mma<T>::mma(ka, qreg[qb][t], x[sub]);
+          }
+          x[sub] = Mma<T>::mma(bias_a(bl, sub), no_offset, x[sub]);
         }
-        p[qb][t] = __builtin_bit_cast(op8, packed);
+        float mx = x[0][0];
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, x[sub][r]);
+        // Rounding is monotone and mref is a T value, so mnew >= mref.
+        const float mnew = to_f32(static_cast<T>(fmaxf(mref[qb], half_max(mx))));
+        if (__ballot(mnew != mref[qb])) {
+          const float corr = mnew == -__builtin_inff() ? 1.0f : __builtin_amdgcn_exp2f(mref[qb] - mnew);
+          lsum[qb] *= corr;
+#pragma unroll
+          for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[qb][dt][r] *= corr;
+          mref[qb] = mnew;
+          qoff[qb] = offset_b(mnew);
+        }
+        // No finite logit yet: every P is 0 (x = -inf).
+        part[qb] = exp_pack(x, mref[qb] == -__builtin_inff() ? 0.0f : mref[qb], p[qb]);
       }
-      lsum[qb] += part;
     }
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb) lsum[qb] += part[qb];
 
     // O^T += V^T P^T.
 #pragma unroll
@@ -315,9 +361,107 @@ __device__ __forceinline__ void attn_segment(const AttnArgs<T>& a, T* k_lds, T* 
         for (int qb = 0; qb < kQB; ++qb) o[qb][dt] = Mma<T>::mma(va, p[qb][t], o[qb][dt]);
       }
     }
+  };
 
-    if (more) stage_store(tile + 1, buf ^ 1);
+  if constexpr (kDma) {
+    // The Q loads complete here, so no later compiler-inserted wait for them
+    // (which would count the untracked DMAs too) lands inside the tile loop.
+    wait_vmem<0>();
+    // Three-stage LDS ring filled by DMA two tiles ahead.  Per tile each wave
+    // issues 2 K and 2 V^T blocks of 8 rows x 128 B (lane i: row i/8, physical
+    // chunk i%8, i.e. the global chunk (i%8) ^ swz(row)) and the tile's 64
+    // bias pairs (every wave the same, so the count is uniform): 5 DMAs.
+    constexpr int kDmaPerTile = 5;
+    const int dr = lane >> 3;         // row within an 8-row block
+    const int dc = lane & 7;          // physical chunk
+    const T* vt_head = a.vt + static_cast<int64_t>(bh) * kD * a.npad;
+    auto issue = [&](int tile, int stage) {
+      const int kt = min(tile, a.ntiles - 1) * kBN;
+      T* kl = k_lds + stage * kTileElems;
+      T* vl = vt_lds + stage * kTileElems;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int row = 16 * wave + 8 * j + dr;
+        const int lc = dc ^ swz(row);
+        lds_dma16(kb_ptr + min(kt + row, last_key) * ksn + lc * 8, lds_offset(kl + (16 * wave + 8 * j) * kD));
+        lds_dma16(vt_head + static_cast<int64_t>(row) * a.npad + kt + lc * 8,
+                  lds_offset(vl + (16 * wave + 8 * j) * kD));
+      }
+      lds_dma4(a.bias2 + 2 * (kt + lane), lds_offset(b_lds + stage * kBiasSlot));
+    };
+    issue(tile0, 0);
+    issue(tile0 + 1, 1);
+    wait_vmem<kDmaPerTile>();
+    __builtin_amdgcn_s_barrier();
+    int stage = 0;
+    for (int tile = tile0; tile < tile1; ++tile) {
+      const int ahead = stage == 0 ? 2 : stage - 1;  // (stage + 2) % 3: held tile - 1
+      issue(tile + 2, ahead);
+      compute_tile(k_lds + stage * kTileElems, vt_lds + stage * kTileElems, b_lds + stage * kBiasSlot);
+      // This wave's reads of the stage are complete (the next DMA overwrites
+      // it once every wave has passed the barrier) and its DMA of tile + 1
+      // has landed.
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      wait_vmem<kDmaPerTile>();
+      __builtin_amdgcn_s_barrier();
+      stage = stage == 2 ? 0 : stage + 1;
+    }
+    wait_vmem<0>();  // drain the look-ahead DMA before the ring is reused
+  } else {
+    // Register staging.  K: rows st and st+32, chunk sc.  V: keys 2st, 2st+1,
+    // dims 8sc..8sc+7.  Row offsets fit in 32 bits (checked on the host).
+    const int st = tid >> 3;
+    const int sc = tid & 7;
+    const int kw0 = st * kD + ((sc ^ swz(st)) << 3);
+    const int kw1 = (st + 32) * kD + ((sc ^ swz(st + 32)) << 3);
+    const int vpos = vt_pos(2 * st);
+    const int vphys = (vpos >> 3) ^ sc;  // chunk of dim 8sc+i is vphys ^ i
+    const int vbase = 8 * sc * kD + (vpos & 7);
+    const T* kcol = kb_ptr + 8 * sc;
+    const T* vcol = vb_ptr + 8 * sc;
+
+    // The next tile's rows are loaded into registers while the current tile is
+    // computed (rows past n_key read a valid row; their bias is -inf).
+    op8 pk0, pk1, pv0, pv1;
+    T pb = static_cast<T>(0.0f);
+    auto stage_load = [&](int tile) {
+      const int kt = tile * kBN;
+      pk0 = *reinterpret_cast<const op8*>(kcol + min(kt + st, last_key) * ksn);
+      pk1 = *reinterpret_cast<const op8*>(kcol + min(kt + st + 32, last_key) * ksn);
+      pv0 = *reinterpret_cast<const op8*>(vcol + min(kt + 2 * st, last_key) * vsn);
+      pv1 = *reinterpret_cast<const op8*>(vcol + min(kt + 2 * st + 1, last_key) * vsn);
+      if (a.bias) pb = a.bias[min(kt + lane, last_key)];
+    };
+    // Every wave writes the same 64 bias pairs (branch-free; identical data).
+    auto stage_store = [&](int tile, int buf) {
+      T* kl = k_lds + buf * kTileElems;
+      T* vl = vt_lds + buf * kTileElems;
+      *reinterpret_cast<op8*>(kl + kw0) = pk0;
+      *reinterpret_cast<op8*>(kl + kw1) = pk1;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const op2 pr = {pv0[i], pv1[i]};
+        *reinterpret_cast<op2*>(vl + vbase + i * kD + ((vphys ^ i) << 3)) = pr;
+      }
+      const bool valid = tile * kBN + lane < a.nk;
+      const float bv = valid ? (a.bias ? kLog2e * to_f32(pb) : 0.0f) : -__builtin_inff();
+      const T hi = static_cast<T>(bv);
+      const T lo = static_cast<T>(__builtin_isfinite(bv) ? bv - to_f32(hi) : 0.0f);
+      const op2 pair = {hi, lo};
+      *reinterpret_cast<op2*>(b_lds + buf * kBiasSlot + 2 * lane) = pair;
+    };
+
+    stage_load(tile0);
+    stage_store(tile0, 0);
     __syncthreads();
+    for (int tile = tile0; tile < tile1; ++tile) {
+      const int buf = (tile - tile0) & 1;
+      const bool more = tile + 1 < tile1;
+      if (more) stage_load(tile + 1);
+      compute_tile(k_lds + buf * kTileElems, vt_lds + buf * kTileElems, b_lds + buf * kBiasSlot);
+      if (more) stage_store(tile + 1, buf ^ 1);
+      __syncthreads();
+    }
   }
 
   if (partial == nullptr) {
@@ -354,7 +498,7 @@ __device__ __forceinline__ void attn_segment(const AttnArgs<T>& a, T* k_lds, T* 
         }
       const float ltot = half_sum(lsum[qb]);
       if (hh == 0) {
-        partial[kQBlock * kD + ql] = m[qb];
+        partial[kQBlock * kD + ql] = mref[qb];
         partial[kQBlock * kD + kQBlock + ql] = ltot;
       }
     }
@@ -367,11 +511,12 @@ __device__ __forceinline__ void attn_segment(const AttnArgs<T>& a, T* k_lds, T* 
 // part writes its partial state (slot 0: the work-group's first segment, slot
 // 1: its last), which attn_merge_kernel combines.  With groups == tasks every
 // work-group owns exactly one whole task (no partial states).
-template <typename T>
+template <typename T, bool kDma>
 __global__ __launch_bounds__(kWaves * 64, 2) void attn_mfma_kernel(AttnArgs<T> a) {
-  __shared__ __attribute__((aligned(16))) T k_lds[2 * kTileElems];
-  __shared__ __attribute__((aligned(16))) T vt_lds[2 * kTileElems];
-  __shared__ __attribute__((aligned(16))) T b_lds[2 * kBN];
+  constexpr int kStages = kDma ? 3 : 2;
+  __shared__ __attribute__((aligned(16))) T k_lds[kStages * kTileElems];
+  __shared__ __attribute__((aligned(16))) T vt_lds[kStages * kTileElems];
+  __shared__ __attribute__((aligned(16))) T b_lds[kStages * kBiasSlot];
   const int64_t w = xcd_remap(blockIdx.x, gridDim.x);
   // Whole tasks: consecutive work-groups (one XCD's, after the remap) take
   // consecutive tasks of a round, so they stream one head's K/V in step and
@@ -380,7 +525,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attn_mfma_kernel(AttnArgs<T> a
     const int64_t task = w + r * a.groups;
     const int bh = static_cast<int>(task / a.n_qblocks);
     const int qblk = static_cast<int>(task - static_cast<int64_t>(bh) * a.n_qblocks);
-    attn_segment<T>(a, k_lds, vt_lds, b_lds, bh, qblk, 0, a.ntiles, nullptr);
+    attn_segment<T, kDma>(a, k_lds, vt_lds, b_lds, bh, qblk, 0, a.ntiles, nullptr);
   }
   if (w >= a.tail_groups) return;
   int64_t u = sk_begin(w, a.units, a.tail_groups);
@@ -397,7 +542,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attn_mfma_kernel(AttnArgs<T> a
     float* partial = nullptr;
     if (tile0 != 0 || tile1 != a.ntiles)
       partial = a.partial + (2 * w + (first ? 0 : 1)) * static_cast<int64_t>(kPartialFloats);
-    attn_segment<T>(a, k_lds, vt_lds, b_lds, bh, qblk, tile0, tile1, partial);
+    attn_segment<T, kDma>(a, k_lds, vt_lds, b_lds, bh, qblk, tile0, tile1, partial);
     u = seg_end;
     first = false;
   }
@@ -457,7 +602,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs<T> a) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         if (wb + e <= w1) {
-          const float f = __builtin_amdgcn_exp2f((mv[e] - mmax) * a.c);
+          const float f = __builtin_amdgcn_exp2f(mv[e] - mmax);
 #pragma unroll
           for (int q = 0; q < 4; ++q) acc[q] = fmaf(xv[e][q], f, acc[q]);
           l = fmaf(lv[e], f, l);
@@ -545,6 +690,59 @@ __global__ __launch_bounds__(64) void attn_f32_kernel(
   }
 }
 
+// Packs V of every (batch, head) into V^T tiles for the DMA kernel:
+// vt[bh][d][j'] = V[bh][key j][d] with j' = vt_pos(j) inside each 16-key group
+// (the key order of the P operand), zeros past n_key, npad = ntiles * 64
+// columns; and bias2[2j], bias2[2j+1] = hi, lo of log2(e) * bias[j] (0, 0
+// without a bias) for j < n_key, (-inf, 0) up to npad.  One block per
+// (64-key tile, bh).
+template <typename T>
+__global__ __launch_bounds__(256) void vt_pack_kernel(const T* __restrict__ v, int heads, int nk,
+                                                      int ntiles, int npad, int64_t vsb, int64_t vsh,
+                                                      int64_t vsn, const T* __restrict__ bias,
+                                                      T* __restrict__ vt, T* __restrict__ bias2) {
+  typedef typename Mma<T>::op8 op8;
+  constexpr int kRow = kD + 2;  // padded LDS row
+  __shared__ T tile[kBN * kRow];
+  const int tix = blockIdx.x;
+  const int bh = blockIdx.y;
+  const int b = bh / heads;
+  const int h = bh - b * heads;
+  const int kt = tix * kBN;
+  const int tid = threadIdx.x;
+  const T* vb = v + b * vsb + h * vsh;
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int r = (tid >> 3) + 32 * p;
+    const int c0 = (tid & 7) * 8;
+    op8 x = {};
+    if (kt + r < nk) x = *reinterpret_cast<const op8*>(vb + static_cast<int64_t>(kt + r) * vsn + c0);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) tile[r * kRow + c0 + e] = x[e];
+  }
+  __syncthreads();
+  {
+    const int d = tid >> 2;
+    const int g = (tid & 3) * 16;  // 16 positions g..g+15 of row d
+    op8 lo, hi;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      lo[e] = tile[vt_pos(g + e) * kRow + d];
+      hi[e] = tile[vt_pos(g + 8 + e) * kRow + d];
+    }
+    T* dst = vt + (static_cast<int64_t>(bh) * kD + d) * npad + kt + g;
+    *reinterpret_cast<op8*>(dst) = lo;
+    *reinterpret_cast<op8*>(dst + 8) = hi;
+  }
+  if (bh == 0 && tid < kBN) {
+    const int j = kt + tid;
+    const float bv = j < nk ? (bias ? kLog2e * to_f32(bias[j]) : 0.0f) : -__builtin_inff();
+    const T hi = static_cast<T>(bv);
+    bias2[2 * j] = hi;
+    bias2[2 * j + 1] = static_cast<T>(__builtin_isfinite(bv) ? bv - to_f32(hi) : 0.0f);
+  }
+}
+
 // Resident work-groups of attn_mfma_kernel<T> on the current device (CUs x
 // blocks per CU), cached per device.
 template <typename T>
@@ -556,8 +754,8 @@ int64_t resident_groups() {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
       return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attn_mfma_kernel<T>, kWaves * 64, 0) !=
-        hipSuccess)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attn_mfma_kernel<T, true>, kWaves * 64,
+                                                     0) != hipSuccess)
       return 0;
     cache[dev] = cus * (per_cu > 0 ? per_cu : 1);
   }
@@ -576,6 +774,22 @@ int64_t stream_groups(int64_t tasks, int64_t units) {
   return groups;
 }
 
+// Workspace of the DMA path: V^T, bias pairs, then the partial states (each
+// part 256-byte aligned).
+struct AttnWorkspace {
+  size_t vt, bias2, partial, total;
+};
+inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+inline AttnWorkspace attn_workspace(int64_t bh, int64_t ntiles, int64_t groups, size_t elem) {
+  AttnWorkspace w;
+  const int64_t npad = ntiles * kBN;
+  w.vt = 0;
+  w.bias2 = align256(static_cast<size_t>(bh) * kD * npad * elem);
+  w.partial = w.bias2 + align256(static_cast<size_t>(2 * npad) * elem);
+  w.total = w.partial + static_cast<size_t>(groups) * 2 * kPartialFloats * sizeof(float);
+  return w;
+}
+
 template <typename T>
 int launch_mfma(const void* q, const void* k, const void* v, const void* bias, void* out,
                 int64_t batch, int64_t heads, int64_t nq, int64_t nk, const int64_t* qs,
@@ -584,7 +798,7 @@ int launch_mfma(const void* q, const void* k, const void* v, const void* bias, v
   const int64_t n_qblocks = (nq + kQBlock - 1) / kQBlock;
   const int64_t ntiles = (nk + kBN - 1) / kBN;
   const int64_t tasks = n_qblocks * batch * heads;
-  VGO_REQUIRE(tasks <= 0x7fffffff && batch * heads <= 0x7fffffff,
+  VGO_REQUIRE(tasks <= 0x7fffffff && batch * heads <= 0xffff && ntiles < 0x7fffffff / kBN,
               "mass_bias_attention: grid too large");
   AttnArgs<T> a;
   a.q = static_cast<const T*>(q);
@@ -608,26 +822,43 @@ int launch_mfma(const void* q, const void* k, const void* v, const void* bias, v
   a.vsb = vs[0], a.vsh = vs[1], a.vsn = vs[2];
   a.osb = os[0], a.osh = os[1], a.osn = os[2];
   a.c = kLog2e / 8.0f;
-  if (split) {
-    const int64_t groups = stream_groups<T>(tasks, tasks * ntiles);
-    if (groups > 0) {
-      const size_t need = static_cast<size_t>(groups) * 2 * kPartialFloats * sizeof(float);
-      if (workspace == nullptr || workspace_bytes < need)
-        return fail(VGO_EWORKSPACE, "mass_bias_attention: workspace too small");
-      VGO_REQUIRE(aligned(workspace, 16), "mass_bias_attention: workspace must be 16-byte aligned");
-      a.groups = groups;
-      a.full_rounds = tasks / groups;
-      a.tail_task0 = a.full_rounds * groups;
-      a.units = (tasks - a.tail_task0) * ntiles;
-      // At most ~8 pieces per tail task: a work-group takes >= ntiles/8 key tiles.
-      const int64_t min_units = std::max<int64_t>(kMinUnitsPerGroup, (ntiles + 7) / 8);
-      a.tail_groups = std::min<int64_t>(groups, std::max<int64_t>(1, a.units / min_units));
-      a.partial = static_cast<float*>(workspace);
-    }
+  a.vt = nullptr;
+  a.bias2 = nullptr;
+  a.npad = static_cast<int>(ntiles * kBN);
+  if (!split) {
+    hipLaunchKernelGGL((attn_mfma_kernel<T, false>), dim3(static_cast<unsigned>(a.groups)),
+                       dim3(kWaves * 64), 0, stream, a);
+    return check_launch("mass_bias_attention");
   }
-  hipLaunchKernelGGL((attn_mfma_kernel<T>), dim3(static_cast<unsigned>(a.groups)), dim3(kWaves * 64),
+  // Workspace path: pack V^T and the bias, then the LDS-DMA kernel.
+  const int64_t groups = stream_groups<T>(tasks, tasks * ntiles);
+  const AttnWorkspace ws = attn_workspace(batch * heads, ntiles, groups, sizeof(T));
+  if (workspace == nullptr || workspace_bytes < ws.total)
+    return fail(VGO_EWORKSPACE, "mass_bias_attention: workspace too small");
+  VGO_REQUIRE(aligned(workspace, 256), "mass_bias_attention: workspace must be 256-byte aligned");
+  char* base = static_cast<char*>(workspace);
+  T* vt = reinterpret_cast<T*>(base + ws.vt);
+  T* bias2 = reinterpret_cast<T*>(base + ws.bias2);
+  a.vt = vt;
+  a.bias2 = bias2;
+  if (groups > 0) {
+    a.groups = groups;
+    a.full_rounds = tasks / groups;
+    a.tail_task0 = a.full_rounds * groups;
+    a.units = (tasks - a.tail_task0) * ntiles;
+    // At most ~8 pieces per tail task: a work-group takes >= ntiles/8 key tiles.
+    const int64_t min_units = std::max<int64_t>(kMinUnitsPerGroup, (ntiles + 7) / 8);
+    a.tail_groups = std::min<int64_t>(groups, std::max<int64_t>(1, a.units / min_units));
+    a.partial = reinterpret_cast<float*>(base + ws.partial);
+  }
+  hipLaunchKernelGGL((vt_pack_kernel<T>), dim3(static_cast<unsigned>(ntiles), static_cast<unsigned>(batch * heads)),
+                     dim3(256), 0, stream, a.v, a.heads, a.nk, a.ntiles, a.npad, a.vsb, a.vsh, a.vsn,
+                     a.bias, vt, bias2);
+  int status = check_launch("mass_bias_attention(pack)");
+  if (status != VGO_OK) return status;
+  hipLaunchKernelGGL((attn_mfma_kernel<T, true>), dim3(static_cast<unsigned>(a.groups)), dim3(kWaves * 64),
                      0, stream, a);
-  int status = check_launch("mass_bias_attention");
+  status = check_launch("mass_bias_attention");
   if (status != VGO_OK || a.partial == nullptr || a.units == 0) return status;
   const int64_t tail_tasks = a.units / ntiles;
   hipLaunchKernelGGL((attn_merge_kernel<T>), dim3(static_cast<unsigned>(tail_tasks * kMergeSplit)),
@@ -718,10 +949,10 @@ extern "C" int vgo_mass_bias_attn_workspace(int64_t batch, int64_t heads, int64_
   if (batch == 0 || heads == 0 || n_query == 0 || n_key == 0 || dtype == VGO_F32) return VGO_OK;
   VGO_REQUIRE(dtype == VGO_BF16 || dtype == VGO_F16, "mass_bias_attention: unsupported dtype");
   const int64_t tasks = (n_query + kQBlock - 1) / kQBlock * batch * heads;
-  const int64_t units = tasks * ((n_key + kBN - 1) / kBN);
-  const int64_t groups =
-      dtype == VGO_BF16 ? stream_groups<bf16_t>(tasks, units) : stream_groups<f16_t>(tasks, units);
-  *bytes = static_cast<size_t>(groups) * 2 * kPartialFloats * sizeof(float);
+  const int64_t ntiles = (n_key + kBN - 1) / kBN;
+  const int64_t groups = dtype == VGO_BF16 ? stream_groups<bf16_t>(tasks, tasks * ntiles)
+                                           : stream_groups<f16_t>(tasks, tasks * ntiles);
+  *bytes = attn_workspace(batch * heads, ntiles, groups, 2).total;
   return VGO_OK;
 }
 
