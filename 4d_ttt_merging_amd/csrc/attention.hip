@@ -29,8 +29,8 @@
 //    logit exceeds the reference max mref by more than 8 (checked through the
 //    per-lane sums); only then, and on a segment's first tile, are the tile's
 //    logits recomputed, mref moved and O / the row sum rescaled.  P is rounded
-//    to the input dtype before P.V (reference :74) and the row sum is
-//    accumulated from those rounded values with v_dot2 (fp32 accumulate).
+//    to the input dtype before P.V (reference :74); the row sum adds the
+//    unrounded fp32 values, as the reference's does (:62).
 //  * Scheduling: with G work-groups resident at once, every work-group runs
 //    whole tasks w, w+G, ... for floor(tasks/G) rounds (neighbouring groups,
 //    i.e. one XCD's, share a head's K/V in L2), and the (task, key tile)
@@ -54,9 +54,6 @@ constexpr int kQPerWave = 32 * kQB;          // 64
 constexpr int kQBlock = kWaves * kQPerWave;  // 256 queries per work-group task
 constexpr int kTileElems = kBN * kD;         // one K (or V^T) tile, elements
 constexpr float kLog2e = 1.4426950408889634f;
-// Partial state of one stream-K segment: O (fp32, unnormalised) then the
-// running max and sum of every query of the task.
-constexpr int kPartialFloats = kQBlock * kD + 2 * kQBlock;
 
 template <typename T>
 struct Mma;
@@ -68,9 +65,6 @@ struct Mma<bf16_t> {
   static __device__ __forceinline__ f32x16 mma(op8 a, op8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
-  static __device__ __forceinline__ float dot2(op2 a, op2 b, float c) {
-    return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false);
-  }
 };
 template <>
 struct Mma<f16_t> {
@@ -79,9 +73,6 @@ struct Mma<f16_t> {
   typedef f16x4 op4;
   static __device__ __forceinline__ f32x16 mma(op8 a, op8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ float dot2(op2 a, op2 b, float c) {
-    return __builtin_amdgcn_fdot2(a, b, c, false);
   }
 };
 
@@ -127,13 +118,14 @@ __device__ __forceinline__ uint32_t lds_offset(const void* p) {
   typedef const __attribute__((address_space(3))) char* lds_ptr;
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr)(p)));
 }
-__device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-               :: "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(g) : "memory");
+// Global address = base (wave-uniform, SGPRs) + 32-bit byte offset (per lane).
+__device__ __forceinline__ void lds_dma16(const void* base, uint32_t offset, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :: "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(offset), "s"(base) : "memory");
 }
-__device__ __forceinline__ void lds_dma4(const void* g, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
-               :: "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(g) : "memory");
+__device__ __forceinline__ void lds_dma4(const void* base, uint32_t offset, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2"
+               :: "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(offset), "s"(base) : "memory");
 }
 // Wait until at most N vector-memory operations of this wave are outstanding.
 template <int N>
@@ -183,155 +175,182 @@ constexpr int kBiasSlot = 2 * kBN;
 // moving its reference max (bounds every P by 2^8).
 constexpr float kLazyLimit = 256.0f;
 
-template <typename T, bool kDma>
-__device__ __forceinline__ void attn_segment(const AttnArgs<T>& a, T* k_lds, T* vt_lds, T* b_lds,
-                                             int bh, int qblk, int tile0, int tile1, float* partial) {
+// Per-wave state of the bf16/f16 kernels: 64 queries as two 32-column MFMA
+// blocks -- their scaled Q operands, the online-softmax state and the O^T
+// accumulators -- and the tile-level steps on LDS-resident K / V^T / bias.
+template <typename T>
+struct WaveAttn {
   typedef typename Mma<T>::op8 op8;
   typedef typename Mma<T>::op2 op2;
   typedef typename Mma<T>::op4 op4;
-  const int b = bh / a.heads;
-  const int h = bh - b * a.heads;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int l32 = lane & 31;
-  const int hh = lane >> 5;
-  const int qw0 = qblk * kQBlock + wave * kQPerWave;
 
-  const T* qb_ptr = a.q + b * a.qsb + h * a.qsh;
-  const T* kb_ptr = a.k + b * a.ksb + h * a.ksh;
-  const T* vb_ptr = a.v + b * a.vsb + h * a.vsh;
+  op8 qreg[kQB][4];  // Q' = Q * log2(e)/8, B operands
+  uint32_t qneg[kQB];  // -mref as a T bit pattern (lanes 0-31; 0 elsewhere)
+  // Reference max per query (a T value; -inf until a finite logit is seen);
+  // the running sum and O are relative to 2^mref.
+  float mref[kQB], lsum[kQB];
+  f32x16 o[kQB][2];
+  int off[4];  // LDS element offsets of logical chunk pair t of row l32
+  uint32_t low_lanes, one_bits;
+  int l32, hh;
 
-  // Q' = Q * log2(e)/8 rounded to T, as MFMA B operands (rows past n_query
-  // read a valid row; never stored): K Q'^T is then in the exp2 domain.
-  op8 qreg[kQB][4];
+  // Q' = Q * c rounded to T for the wave's rows qw0.. (rows past n_query read
+  // a valid row; never stored): K Q'^T is then in the exp2 domain.
+  __device__ __forceinline__ void init(const T* qb_ptr, int64_t qsn, int qw0, int nq, float c) {
+    const int lane = threadIdx.x & 63;
+    l32 = lane & 31;
+    hh = lane >> 5;
 #pragma unroll
-  for (int qb = 0; qb < kQB; ++qb) {
-    const int row = min(qw0 + qb * 32 + l32, a.nq - 1);
+    for (int qb = 0; qb < kQB; ++qb) {
+      const int row = min(qw0 + qb * 32 + l32, nq - 1);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const op8 raw = *reinterpret_cast<const op8*>(qb_ptr + row * a.qsn + 16 * t + 8 * hh);
+      for (int t = 0; t < 4; ++t) {
+        const op8 raw = *reinterpret_cast<const op8*>(qb_ptr + row * qsn + 16 * t + 8 * hh);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) qreg[qb][t][e] = static_cast<T>(to_f32(raw[e]) * a.c);
+        for (int e = 0; e < 8; ++e) qreg[qb][t][e] = static_cast<T>(to_f32(raw[e]) * c);
+      }
     }
-  }
-  const op2 ones2 = {static_cast<T>(1.0f), static_cast<T>(1.0f)};
-
-  // The bias k-step.  A (keys; lanes 0-31 hold k-slots 0-7 of key l32, lanes
-  // 32-63 slots 8-15): {bias_hi, bias_lo, 1, 0, ...}, the key's log2(e)*bias
-  // split into two T values.  B (queries): {1, 1, -offset, 0, ...}, where the
-  // offset is the query's running reference max (a T value).
-  const uint32_t low_lanes = hh == 0 ? 0xffffffffu : 0u;
-  const uint32_t one_bits = __builtin_bit_cast(uint16_t, static_cast<T>(1.0f));
-  auto bias_a = [&](const T* bl, int sub) {
-    const uint32_t bw = *reinterpret_cast<const uint32_t*>(bl + 2 * (sub * 32 + l32));
-    const i32x4 w = {static_cast<int>(bw & low_lanes), static_cast<int>(one_bits & low_lanes), 0, 0};
-    return __builtin_bit_cast(op8, w);
-  };
-  auto offset_b = [&](float offset) {
-    const uint32_t neg = __builtin_bit_cast(uint16_t, static_cast<T>(-offset));
-    const i32x4 w = {static_cast<int>((one_bits | (one_bits << 16)) & low_lanes),
-                     static_cast<int>(neg & low_lanes), 0, 0};
-    return __builtin_bit_cast(op8, w);
-  };
-  const op8 no_offset = offset_b(0.0f);
-
-  // Per-lane LDS read offsets (elements) of logical chunk pair t of row l32;
-  // row l32 + 32 uses off[t ^ 2] (swz flips bit 2 of the chunk there).
-  int off[4];
-  {
+    low_lanes = hh == 0 ? 0xffffffffu : 0u;
+    one_bits = __builtin_bit_cast(uint16_t, static_cast<T>(1.0f));
+    // Row l32 + 32 uses off[t ^ 2] (swz flips bit 2 of the chunk there).
     const int s0 = swz(l32);
 #pragma unroll
     for (int t = 0; t < 4; ++t) off[t] = l32 * kD + (((2 * t + hh) ^ s0) << 3);
-  }
-  const int last_key = a.nk - 1;
-  const int ksn = static_cast<int>(a.ksn), vsn = static_cast<int>(a.vsn);
-
-  // Online-softmax state per query: the reference max `mref` (a T value, -inf
-  // until a finite logit is seen), the running sum and O, both relative to
-  // 2^mref.  qoff carries -mref into the bias k-step.
-  float mref[kQB], lsum[kQB];
-  op8 qoff[kQB];
-  f32x16 o[kQB][2];
 #pragma unroll
-  for (int qb = 0; qb < kQB; ++qb) {
-    mref[qb] = -__builtin_inff();
-    qoff[qb] = offset_b(mref[qb]);
-    lsum[qb] = 0.0f;
+    for (int qb = 0; qb < kQB; ++qb) {
+      mref[qb] = -__builtin_inff();
+      qneg[qb] = neg_bits(mref[qb]);
+      lsum[qb] = 0.0f;
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt) o[qb][dt] = f32x16{};
-  }
-
-  // P = exp2(x - shift) rounded to T and packed as the four B operands of
-  // O^T += V^T P^T; returns this lane's sum of the rounded values.
-  auto exp_pack = [&](const f32x16 (&x)[2], float shift, op8 (&p)[4]) {
-    float part = 0.0f;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      i32x4 packed;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int r = (t & 1) * 8 + 2 * j;
-        const op2 pr = {static_cast<T>(__builtin_amdgcn_exp2f(x[t >> 1][r] - shift)),
-                        static_cast<T>(__builtin_amdgcn_exp2f(x[t >> 1][r + 1] - shift))};
-        part = Mma<T>::dot2(pr, ones2, part);
-        packed[j] = __builtin_bit_cast(int, pr);
-      }
-      p[t] = __builtin_bit_cast(op8, packed);
+      for (int dt = 0; dt < 2; ++dt) o[qb][dt] = f32x16{};
     }
-    return part;
-  };
+  }
 
-  // One 64-key tile from LDS (K at kl, V^T at vl, bias pairs at bl).
-  auto compute_tile = [&](const T* kl, const T* vl, const T* bl) {
-    // S^T = K Q'^T + log2(e) bias - mref for two 32-key sub-tiles.
-    f32x16 s[kQB][2];
+  // The bias k-step.  A (keys; lanes 0-31 hold k-slots 0-7 of key l32, lanes
+  // 32-63 slots 8-15): {bias_hi, bias_lo, 1, 0, ...}, the key's log2(e)*bias
+  // split into two T values.  B (queries): {1, 1, -offset, 0, ...}.
+  __device__ __forceinline__ uint32_t neg_bits(float offset) const {
+    return __builtin_bit_cast(uint16_t, static_cast<T>(-offset)) & low_lanes;
+  }
+  // Built where it is used (it is needed once per tile) rather than held.
+  __device__ __forceinline__ op8 offset_b(uint32_t neg) const {
+    const i32x4 w = {static_cast<int>((one_bits | (one_bits << 16)) & low_lanes), static_cast<int>(neg), 0, 0};
+    return __builtin_bit_cast(op8, w);
+  }
+  __device__ __forceinline__ op8 bias_a(const T* bl, int sub) const {
+    const uint32_t bw = *reinterpret_cast<const uint32_t*>(bl + 2 * (sub * 32 + l32));
+    const i32x4 w = {static_cast<int>(bw & low_lanes), static_cast<int>(one_bits & low_lanes), 0, 0};
+    return __builtin_bit_cast(op8, w);
+  }
+  // A operand of rows 32*half.. of a K or V^T tile, k-chunk pair t.
+  __device__ __forceinline__ op8 tile_op(const T* tl, int half, int t) const {
+    return *reinterpret_cast<const op8*>(tl + half * 32 * kD + off[t ^ (2 * half)]);
+  }
+
+  // Operands of one tile, read from LDS in one batch ahead of their MFMAs (so
+  // the reads overlap each other rather than each MFMA waiting for its own).
+  struct KOps {
+    op8 k[2][4];  // K rows 32*sub.., k-chunk pair t
+    op8 b[2];     // bias k-step A operands
+  };
+  struct VOps {
+    op8 v[4][2];  // V^T rows (dims) 32*dt.., key chunk pair t
+  };
+  __device__ __forceinline__ void load_k(const T* kl, const T* bl, KOps& ops) const {
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) ops.k[sub][t] = tile_op(kl, sub, t);
+      ops.b[sub] = bias_a(bl, sub);
+    }
+  }
+  __device__ __forceinline__ void load_v(const T* vl, VOps& ops) const {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) ops.v[t][dt] = tile_op(vl, dt, t);
+  }
+
+  // S^T = K Q'^T + log2(e) bias - mref for the tile's two 32-key sub-tiles.
+  __device__ __forceinline__ void scores(const KOps& ops, f32x16 (&s)[kQB][2]) const {
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
 #pragma unroll
       for (int qb = 0; qb < kQB; ++qb) s[qb][sub] = f32x16{};
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const op8 ka = *reinterpret_cast<const op8*>(kl + sub * 32 * kD + off[t ^ (2 * sub)]);
+      for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int qb = 0; qb < kQB; ++qb) s[qb][sub] = Mma<T>::mma(ka, qreg[qb][t], s[qb][sub]);
-      }
-      const op8 ba = bias_a(bl, sub);
+        for (int qb = 0; qb < kQB; ++qb) s[qb][sub] = Mma<T>::mma(ops.k[sub][t], qreg[qb][t], s[qb][sub]);
 #pragma unroll
-      for (int qb = 0; qb < kQB; ++qb) s[qb][sub] = Mma<T>::mma(ba, qoff[qb], s[qb][sub]);
+      for (int qb = 0; qb < kQB; ++qb) s[qb][sub] = Mma<T>::mma(ops.b[sub], offset_b(qneg[qb]), s[qb][sub]);
     }
+  }
+  __device__ __forceinline__ void scores(const T* kl, const T* bl, f32x16 (&s)[kQB][2]) const {
+    KOps ops;
+    load_k(kl, bl, ops);
+    __builtin_amdgcn_sched_barrier(0);
+    scores(ops, s);
+  }
 
-    // Lazy online softmax.  P = 2^S directly while every lane's sum of its 32
-    // probabilities stays <= 2^8 (so no logit exceeds mref by more than 8):
-    // the reference max then need not move.  Otherwise (and on the first tile,
-    // when mref = -inf makes S non-finite) the tile's logits are recomputed
-    // without the offset, mref moves to the T value nearest the running max,
-    // O and the sum are rescaled, and P is recomputed.
-    op8 p[kQB][4];
+  // P = exp2(x - shift) for one 32-key sub-tile (x), rounded to T and packed
+  // into B operands p[2*sub], p[2*sub+1] of O^T += V^T P^T; returns this
+  // lane's sum of the unrounded values (the reference sums its fp32
+  // probabilities).  The sum uses fp32 adds: dot instructions would share the
+  // matrix pipe with the other wave's MFMAs.
+  __device__ __forceinline__ float exp_pack(const f32x16& x, int sub, float shift, op8 (&p)[4]) const {
+    float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      i32x4 packed;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = u * 8 + 2 * j;
+        const float e0 = __builtin_amdgcn_exp2f(x[r] - shift);
+        const float e1 = __builtin_amdgcn_exp2f(x[r + 1] - shift);
+        part[j] += e0;
+        part[j] += e1;
+        const op2 pr = {static_cast<T>(e0), static_cast<T>(e1)};
+        packed[j] = __builtin_bit_cast(int, pr);
+      }
+      p[2 * sub + u] = __builtin_bit_cast(op8, packed);
+    }
+    return (part[0] + part[1]) + (part[2] + part[3]);
+  }
+
+  // Logits of query block qb against the sub-tile's 32 keys, no offset.
+  __device__ __forceinline__ f32x16 logits(const T* kl, const T* bl, int qb, int sub) const {
+    f32x16 x = {};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) x = Mma<T>::mma(tile_op(kl, sub, t), qreg[qb][t], x);
+    return Mma<T>::mma(bias_a(bl, sub), offset_b(0u), x);
+  }
+
+  // Lazy online softmax of one tile's scores.  P = 2^S directly while every
+  // lane's sum of its 32 probabilities stays <= kLazyLimit (so no logit
+  // exceeds mref by more than 8): the reference max then need not move.
+  // Otherwise (and on a segment's first tile, when mref = -inf makes S
+  // non-finite) the tile's logits are recomputed without the offset from K
+  // (at kl, bias at bl), mref moves to the T value nearest the running max,
+  // O and the sum are rescaled, and P is recomputed.  That path works one
+  // 32-key sub-tile at a time (logits computed twice) to stay within the
+  // registers the fast path leaves free.
+  __device__ __forceinline__ void softmax(const f32x16 (&s)[kQB][2], const T* kl, const T* bl,
+                                          op8 (&p)[kQB][4]) {
     float part[kQB];
 #pragma unroll
-    for (int qb = 0; qb < kQB; ++qb) part[qb] = exp_pack(s[qb], 0.0f, p[qb]);
+    for (int qb = 0; qb < kQB; ++qb) part[qb] = exp_pack(s[qb][0], 0, 0.0f, p[qb]) + exp_pack(s[qb][1], 1, 0.0f, p[qb]);
     if (__builtin_expect(__ballot(!(part[0] <= kLazyLimit) | !(part[1] <= kLazyLimit)) != 0, 0)) {
-      // Reload K here rather than keep the fast path's operands alive.
+      // Reload K here rather than keep the score operands alive.
       asm volatile("" ::: "memory");
 #pragma unroll
       for (int qb = 0; qb < kQB; ++qb) {
-        f32x16 x[2];
+        float mx = -__builtin_inff();
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub) {
-          x[sub] = f32x16{};
+          const f32x16 x = logits(kl, bl, qb, sub);
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const op8 ka = *reinterpret_cast<const op8*>(kl + sub * 32 * kD + off[t ^ (2 * sub)]);
-            x[sub] = Mma<T>::mma(ka, qreg[qb][t], x[sub]);
-          }
-          x[sub] = Mma<T>::mma(bias_a(bl, sub), no_offset, x[sub]);
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, x[r]);
         }
-        float mx = x[0][0];
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, x[sub][r]);
         // Rounding is monotone and mref is a T value, so mnew >= mref.
         const float mnew = to_f32(static_cast<T>(fmaxf(mref[qb], half_max(mx))));
         if (__ballot(mnew != mref[qb])) {
@@ -342,135 +361,90 @@ __device__ __forceinline__ void attn_segment(const AttnArgs<T>& a, T* k_lds, T* 
 #pragma unroll
             for (int r = 0; r < 16; ++r) o[qb][dt][r] *= corr;
           mref[qb] = mnew;
-          qoff[qb] = offset_b(mnew);
+          qneg[qb] = neg_bits(mnew);
         }
         // No finite logit yet: every P is 0 (x = -inf).
-        part[qb] = exp_pack(x, mref[qb] == -__builtin_inff() ? 0.0f : mref[qb], p[qb]);
+        const float shift = mref[qb] == -__builtin_inff() ? 0.0f : mref[qb];
+        asm volatile("" ::: "memory");
+        part[qb] = exp_pack(logits(kl, bl, qb, 0), 0, shift, p[qb]);
+        part[qb] += exp_pack(logits(kl, bl, qb, 1), 1, shift, p[qb]);
       }
     }
 #pragma unroll
     for (int qb = 0; qb < kQB; ++qb) lsum[qb] += part[qb];
+  }
 
-    // O^T += V^T P^T.
+  // O^T += V^T P^T.
+  __device__ __forceinline__ void pv(const VOps& ops, const op8 (&p)[kQB][4]) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int dt = 0; dt < 2; ++dt) {
-        const op8 va = *reinterpret_cast<const op8*>(vl + dt * 32 * kD + off[t ^ (2 * dt)]);
+      for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-        for (int qb = 0; qb < kQB; ++qb) o[qb][dt] = Mma<T>::mma(va, p[qb][t], o[qb][dt]);
-      }
+        for (int qb = 0; qb < kQB; ++qb) o[qb][dt] = Mma<T>::mma(ops.v[t][dt], p[qb][t], o[qb][dt]);
+  }
+  __device__ __forceinline__ void pv(const T* vl, const op8 (&p)[kQB][4]) {
+    VOps ops;
+    load_v(vl, ops);
+    __builtin_amdgcn_sched_barrier(0);
+    pv(ops, p);
+  }
+
+  // O^T += V^T P^T with the tile at vl, then the scores of the tile at kl / bl.
+  // K reads go out in two halves (one per 32-key sub-tile), each while MFMAs
+  // of the previous step run: their latency is hidden and at most about half
+  // of the operands are held at once.
+  __device__ __forceinline__ void pv_scores(const T* vl, const op8 (&p)[kQB][4], const T* kl,
+                                            const T* bl, f32x16 (&s)[kQB][2]) {
+    VOps vops;
+    load_v(vl, vops);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int qb = 0; qb < kQB; ++qb) o[qb][dt] = Mma<T>::mma(vops.v[t][dt], p[qb][t], o[qb][dt]);
+    __builtin_amdgcn_sched_barrier(0);
+    op8 ka[4], kb[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) ka[t] = tile_op(kl, 0, t);
+    const op8 ba = bias_a(bl, 0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 2; t < 4; ++t)
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int qb = 0; qb < kQB; ++qb) o[qb][dt] = Mma<T>::mma(vops.v[t][dt], p[qb][t], o[qb][dt]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) kb[t] = tile_op(kl, 1, t);
+    const op8 bb = bias_a(bl, 1);
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb) {
+      s[qb][0] = f32x16{};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) s[qb][0] = Mma<T>::mma(ka[t], qreg[qb][t], s[qb][0]);
+      s[qb][0] = Mma<T>::mma(ba, offset_b(qneg[qb]), s[qb][0]);
     }
-  };
-
-  if constexpr (kDma) {
-    // The Q loads complete here, so no later compiler-inserted wait for them
-    // (which would count the untracked DMAs too) lands inside the tile loop.
-    wait_vmem<0>();
-    // Three-stage LDS ring filled by DMA two tiles ahead.  Per tile each wave
-    // issues 2 K and 2 V^T blocks of 8 rows x 128 B (lane i: row i/8, physical
-    // chunk i%8, i.e. the global chunk (i%8) ^ swz(row)) and the tile's 64
-    // bias pairs (every wave the same, so the count is uniform): 5 DMAs.
-    constexpr int kDmaPerTile = 5;
-    const int dr = lane >> 3;         // row within an 8-row block
-    const int dc = lane & 7;          // physical chunk
-    const T* vt_head = a.vt + static_cast<int64_t>(bh) * kD * a.npad;
-    auto issue = [&](int tile, int stage) {
-      const int kt = min(tile, a.ntiles - 1) * kBN;
-      T* kl = k_lds + stage * kTileElems;
-      T* vl = vt_lds + stage * kTileElems;
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int row = 16 * wave + 8 * j + dr;
-        const int lc = dc ^ swz(row);
-        lds_dma16(kb_ptr + min(kt + row, last_key) * ksn + lc * 8, lds_offset(kl + (16 * wave + 8 * j) * kD));
-        lds_dma16(vt_head + static_cast<int64_t>(row) * a.npad + kt + lc * 8,
-                  lds_offset(vl + (16 * wave + 8 * j) * kD));
-      }
-      lds_dma4(a.bias2 + 2 * (kt + lane), lds_offset(b_lds + stage * kBiasSlot));
-    };
-    issue(tile0, 0);
-    issue(tile0 + 1, 1);
-    wait_vmem<kDmaPerTile>();
-    __builtin_amdgcn_s_barrier();
-    int stage = 0;
-    for (int tile = tile0; tile < tile1; ++tile) {
-      const int ahead = stage == 0 ? 2 : stage - 1;  // (stage + 2) % 3: held tile - 1
-      issue(tile + 2, ahead);
-      compute_tile(k_lds + stage * kTileElems, vt_lds + stage * kTileElems, b_lds + stage * kBiasSlot);
-      // This wave's reads of the stage are complete (the next DMA overwrites
-      // it once every wave has passed the barrier) and its DMA of tile + 1
-      // has landed.
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      wait_vmem<kDmaPerTile>();
-      __builtin_amdgcn_s_barrier();
-      stage = stage == 2 ? 0 : stage + 1;
-    }
-    wait_vmem<0>();  // drain the look-ahead DMA before the ring is reused
-  } else {
-    // Register staging.  K: rows st and st+32, chunk sc.  V: keys 2st, 2st+1,
-    // dims 8sc..8sc+7.  Row offsets fit in 32 bits (checked on the host).
-    const int st = tid >> 3;
-    const int sc = tid & 7;
-    const int kw0 = st * kD + ((sc ^ swz(st)) << 3);
-    const int kw1 = (st + 32) * kD + ((sc ^ swz(st + 32)) << 3);
-    const int vpos = vt_pos(2 * st);
-    const int vphys = (vpos >> 3) ^ sc;  // chunk of dim 8sc+i is vphys ^ i
-    const int vbase = 8 * sc * kD + (vpos & 7);
-    const T* kcol = kb_ptr + 8 * sc;
-    const T* vcol = vb_ptr + 8 * sc;
-
-    // The next tile's rows are loaded into registers while the current tile is
-    // computed (rows past n_key read a valid row; their bias is -inf).
-    op8 pk0, pk1, pv0, pv1;
-    T pb = static_cast<T>(0.0f);
-    auto stage_load = [&](int tile) {
-      const int kt = tile * kBN;
-      pk0 = *reinterpret_cast<const op8*>(kcol + min(kt + st, last_key) * ksn);
-      pk1 = *reinterpret_cast<const op8*>(kcol + min(kt + st + 32, last_key) * ksn);
-      pv0 = *reinterpret_cast<const op8*>(vcol + min(kt + 2 * st, last_key) * vsn);
-      pv1 = *reinterpret_cast<const op8*>(vcol + min(kt + 2 * st + 1, last_key) * vsn);
-      if (a.bias) pb = a.bias[min(kt + lane, last_key)];
-    };
-    // Every wave writes the same 64 bias pairs (branch-free; identical data).
-    auto stage_store = [&](int tile, int buf) {
-      T* kl = k_lds + buf * kTileElems;
-      T* vl = vt_lds + buf * kTileElems;
-      *reinterpret_cast<op8*>(kl + kw0) = pk0;
-      *reinterpret_cast<op8*>(kl + kw1) = pk1;
+    for (int qb = 0; qb < kQB; ++qb) {
+      s[qb][1] = f32x16{};
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const op2 pr = {pv0[i], pv1[i]};
-        *reinterpret_cast<op2*>(vl + vbase + i * kD + ((vphys ^ i) << 3)) = pr;
-      }
-      const bool valid = tile * kBN + lane < a.nk;
-      const float bv = valid ? (a.bias ? kLog2e * to_f32(pb) : 0.0f) : -__builtin_inff();
-      const T hi = static_cast<T>(bv);
-      const T lo = static_cast<T>(__builtin_isfinite(bv) ? bv - to_f32(hi) : 0.0f);
-      const op2 pair = {hi, lo};
-      *reinterpret_cast<op2*>(b_lds + buf * kBiasSlot + 2 * lane) = pair;
-    };
-
-    stage_load(tile0);
-    stage_store(tile0, 0);
-    __syncthreads();
-    for (int tile = tile0; tile < tile1; ++tile) {
-      const int buf = (tile - tile0) & 1;
-      const bool more = tile + 1 < tile1;
-      if (more) stage_load(tile + 1);
-      compute_tile(k_lds + buf * kTileElems, vt_lds + buf * kTileElems, b_lds + buf * kBiasSlot);
-      if (more) stage_store(tile + 1, buf ^ 1);
-      __syncthreads();
+      for (int t = 0; t < 4; ++t) s[qb][1] = Mma<T>::mma(kb[t], qreg[qb][t], s[qb][1]);
+      s[qb][1] = Mma<T>::mma(bb, offset_b(qneg[qb]), s[qb][1]);
     }
   }
 
-  if (partial == nullptr) {
-    T* ob_ptr = a.out + b * a.osb + h * a.osh;
+  // Normalised output rows qw0.. (rows past n_query are not stored).
+  __device__ __forceinline__ void store_out(T* ob_ptr, int64_t osn, int qw0, int nq) const {
 #pragma unroll
     for (int qb = 0; qb < kQB; ++qb) {
       const float ltot = half_sum(lsum[qb]);
       const int row = qw0 + qb * 32 + l32;
-      if (row < a.nq) {
+      if (row < nq) {
 #pragma unroll
         for (int dt = 0; dt < 2; ++dt) {
 #pragma unroll
@@ -478,15 +452,19 @@ __device__ __forceinline__ void attn_segment(const AttnArgs<T>& a, T* k_lds, T* 
             op4 val;
 #pragma unroll
             for (int e = 0; e < 4; ++e) val[e] = static_cast<T>(o[qb][dt][4 * g + e] / ltot);
-            *reinterpret_cast<op4*>(ob_ptr + row * a.osn + dt * 32 + 8 * g + 4 * hh) = val;
+            *reinterpret_cast<op4*>(ob_ptr + row * osn + dt * 32 + 8 * g + 4 * hh) = val;
           }
         }
       }
     }
-  } else {
+  }
+
+  // Partial state of a task of `qblock` queries (O unnormalised, then mref,
+  // then the sum of every query); this wave's queries start at ql0.
+  __device__ __forceinline__ void store_partial(float* partial, int qblock, int ql0) const {
 #pragma unroll
     for (int qb = 0; qb < kQB; ++qb) {
-      const int ql = wave * kQPerWave + qb * 32 + l32;
+      const int ql = ql0 + qb * 32 + l32;
       float* po = partial + ql * kD;
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt)
@@ -498,25 +476,302 @@ __device__ __forceinline__ void attn_segment(const AttnArgs<T>& a, T* k_lds, T* 
         }
       const float ltot = half_sum(lsum[qb]);
       if (hh == 0) {
-        partial[kQBlock * kD + ql] = mref[qb];
-        partial[kQBlock * kD + kQBlock + ql] = ltot;
+        partial[qblock * kD + ql] = mref[qb];
+        partial[qblock * kD + qblock + ql] = ltot;
       }
     }
   }
+};
+
+// ------------------------------------------- register-staged kernel -------
+// One work-group (4 waves x 64 queries) per 256-query task of one (batch,
+// head), no workspace.  K/V tiles are double-buffered in LDS: the next tile's
+// rows are loaded into registers while the current tile is computed, then
+// stored to the other buffer (K row-major, V transposed into V^T in the MFMA
+// key order) -- one barrier per tile.
+template <typename T>
+__global__ __launch_bounds__(kWaves * 64, 2) void attn_reg_kernel(AttnArgs<T> a) {
+  typedef typename Mma<T>::op8 op8;
+  typedef typename Mma<T>::op2 op2;
+  __shared__ __attribute__((aligned(16))) T k_lds[2 * kTileElems];
+  __shared__ __attribute__((aligned(16))) T vt_lds[2 * kTileElems];
+  __shared__ __attribute__((aligned(16))) T b_lds[2 * kBiasSlot];
+  const int task = static_cast<int>(xcd_remap(blockIdx.x, gridDim.x));
+  const int bh = task / a.n_qblocks;
+  const int qblk = task - bh * a.n_qblocks;
+  const int b = bh / a.heads;
+  const int h = bh - b * a.heads;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int qw0 = qblk * kQBlock + wave * kQPerWave;
+  const T* kb_ptr = a.k + b * a.ksb + h * a.ksh;
+  const T* vb_ptr = a.v + b * a.vsb + h * a.vsh;
+
+  WaveAttn<T> w;
+  w.init(a.q + b * a.qsb + h * a.qsh, a.qsn, qw0, a.nq, a.c);
+
+  // K: rows st and st+32, chunk sc.  V: keys 2st, 2st+1, dims 8sc..8sc+7.
+  // Row offsets fit in 32 bits (checked on the host).
+  const int last_key = a.nk - 1;
+  const int ksn = static_cast<int>(a.ksn), vsn = static_cast<int>(a.vsn);
+  const int st = tid >> 3;
+  const int sc = tid & 7;
+  const int kw0 = st * kD + ((sc ^ swz(st)) << 3);
+  const int kw1 = (st + 32) * kD + ((sc ^ swz(st + 32)) << 3);
+  const int vpos = vt_pos(2 * st);
+  const int vphys = (vpos >> 3) ^ sc;  // chunk of dim 8sc+i is vphys ^ i
+  const int vbase = 8 * sc * kD + (vpos & 7);
+  const T* kcol = kb_ptr + 8 * sc;
+  const T* vcol = vb_ptr + 8 * sc;
+
+  // Rows past n_key read a valid row; their bias is -inf.
+  op8 pk0, pk1, pv0, pv1;
+  T pb = static_cast<T>(0.0f);
+  auto stage_load = [&](int tile) {
+    const int kt = tile * kBN;
+    pk0 = *reinterpret_cast<const op8*>(kcol + min(kt + st, last_key) * ksn);
+    pk1 = *reinterpret_cast<const op8*>(kcol + min(kt + st + 32, last_key) * ksn);
+    pv0 = *reinterpret_cast<const op8*>(vcol + min(kt + 2 * st, last_key) * vsn);
+    pv1 = *reinterpret_cast<const op8*>(vcol + min(kt + 2 * st + 1, last_key) * vsn);
+    if (a.bias) pb = a.bias[min(kt + lane, last_key)];
+  };
+  // Every wave writes the same 64 bias pairs (branch-free; identical data).
+  auto stage_store = [&](int tile, int buf) {
+    T* kl = k_lds + buf * kTileElems;
+    T* vl = vt_lds + buf * kTileElems;
+    *reinterpret_cast<op8*>(kl + kw0) = pk0;
+    *reinterpret_cast<op8*>(kl + kw1) = pk1;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const op2 pr = {pv0[i], pv1[i]};
+      *reinterpret_cast<op2*>(vl + vbase + i * kD + ((vphys ^ i) << 3)) = pr;
+    }
+    const bool valid = tile * kBN + lane < a.nk;
+    const float bv = valid ? (a.bias ? kLog2e * to_f32(pb) : 0.0f) : -__builtin_inff();
+    const T hi = static_cast<T>(bv);
+    const T lo = static_cast<T>(__builtin_isfinite(bv) ? bv - to_f32(hi) : 0.0f);
+    const op2 pair = {hi, lo};
+    *reinterpret_cast<op2*>(b_lds + buf * kBiasSlot + 2 * lane) = pair;
+  };
+
+  stage_load(0);
+  stage_store(0, 0);
+  __syncthreads();
+  for (int tile = 0; tile < a.ntiles; ++tile) {
+    const int buf = tile & 1;
+    const bool more = tile + 1 < a.ntiles;
+    if (more) stage_load(tile + 1);
+    const T* kl = k_lds + buf * kTileElems;
+    const T* bl = b_lds + buf * kBiasSlot;
+    f32x16 s[kQB][2];
+    w.scores(kl, bl, s);
+    op8 p[kQB][4];
+    w.softmax(s, kl, bl, p);
+    w.pv(vt_lds + buf * kTileElems, p);
+    if (more) stage_store(tile + 1, buf ^ 1);
+    __syncthreads();
+  }
+  w.store_out(a.out + b * a.osb + h * a.osh, a.osn, qw0, a.nq);
+}
+
+// ------------------------------------------------- ping-pong kernel -------
+// Workspace path.  A task is 512 queries of one (batch, head): 8 waves x 64
+// queries in two groups of four; a SIMD holds one wave of each group (waves w
+// and w + 4).  Half-periods end at work-group barriers, and in each one group
+// runs its softmax (VALU) while the other runs its MFMAs, so both pipes of
+// every SIMD stay busy:
+//   H0:   group 0 S(0)                group 1 --
+//   A_j:  group 0 softmax(j)          group 1 P.V(j-1), S(j)
+//   B_j:  group 0 P.V(j), S(j+1)      group 1 softmax(j)
+//   H_n:  group 0 --                  group 1 P.V(n-1)
+// K/V^T/bias tiles arrive by LDS DMA in a 4-stage ring (tile j in stage
+// j & 3), tile j + 2 issued by group 0 at the start of A_j; tile j is read
+// from B_{j-1} to A_{j+1}.  Only group 0 issues DMAs: the compiler does not
+// see them, and a wait it inserts for its own memory operations (a register
+// reload, say) would also wait for every DMA in flight; group 0's loop has
+// none, group 1 then has no DMA to wait for.
+constexpr int kPPWaves = 8;
+constexpr int kPPQBlock = kPPWaves * kQPerWave;  // 512 queries per task
+constexpr int kPPStages = 4;
+// Per group-0 wave and tile: two K blocks, two V^T blocks, the bias.
+constexpr int kPPDmaPerTile = 5;
+// Partial state of one stream-K segment: O (fp32, unnormalised), then the
+// reference max and the sum of every query of the task.
+constexpr int kPartialFloats = kPPQBlock * kD + 2 * kPPQBlock;
+
+// Keep x computed before this point / treat it as redefined after it: holds
+// each phase's work on its side of a barrier.
+template <typename V>
+__device__ __forceinline__ void pin_in(const V& x) {
+#if __HIP_DEVICE_COMPILE__
+  asm volatile("" ::"v"(x));
+#endif
+}
+template <typename V>
+__device__ __forceinline__ void pin_out(V& x) {
+#if __HIP_DEVICE_COMPILE__
+  asm volatile("" : "+v"(x));
+#endif
+}
+
+// Work-group barrier of the DMA ring: this wave's LDS reads are complete (a
+// stage is overwritten only after every wave has passed a later barrier), at
+// most N of its DMAs are outstanding (N < 0: no wait; the wave issues none),
+// and no memory access moves across.
+template <int N>
+__device__ __forceinline__ void ring_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  if constexpr (N >= 0) wait_vmem<N>();
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <typename T>
+__device__ __forceinline__ void attn_pp_segment(const AttnArgs<T>& a, T* k_lds, T* vt_lds, T* b_lds,
+                                                int bh, int qblk, int tile0, int tile1, float* partial) {
+  typedef typename Mma<T>::op8 op8;
+  const int b = bh / a.heads;
+  const int h = bh - b * a.heads;
+  const int lane = threadIdx.x & 63;
+  // Wave-uniform (scalar) so the two groups' paths are plain branches.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int group = wave >> 2;
+  const int qw0 = qblk * kPPQBlock + wave * kQPerWave;
+  const T* kb_ptr = a.k + b * a.ksb + h * a.ksh;
+  const T* vt_head = a.vt + static_cast<int64_t>(bh) * kD * a.npad;
+  const int last_key = a.nk - 1;
+  const int ksn = static_cast<int>(a.ksn);
+
+  WaveAttn<T> w;
+  w.init(a.q + b * a.qsb + h * a.qsh, a.qsn, qw0, a.nq, a.c);
+  // The Q loads complete here, so no compiler-inserted wait for them (which
+  // would count the untracked DMAs too) lands inside the ring.
+  wait_vmem<0>();
+
+  // Per tile each group-0 wave issues rows 16*wave.. 16*wave+15 of K and of
+  // V^T as two 8-row blocks (lane i: row i/8, physical chunk i%8, i.e. the
+  // global chunk (i%8) ^ swz(row)) and the tile's 64 bias pairs (every wave
+  // the same, so the count is uniform).
+  const int dr = lane >> 3;
+  const int dc = lane & 7;
+  const int row0 = 16 * wave + dr;
+  const int lc0 = dc ^ swz(row0), lc1 = dc ^ swz(row0 + 8);
+  // Byte offsets from the (scalar) bases; they fit in 32 bits (checked on the host).
+  const uint32_t v_off0 = (static_cast<uint32_t>(row0) * a.npad + lc0 * 8) * sizeof(T);
+  const uint32_t v_off1 = (static_cast<uint32_t>(row0 + 8) * a.npad + lc1 * 8) * sizeof(T);
+  auto issue = [&](int tile) {
+    const int stage = tile & (kPPStages - 1);
+    const int kt = min(tile, a.ntiles - 1) * kBN;
+    T* kst = k_lds + stage * kTileElems + 16 * wave * kD;
+    T* vst = vt_lds + stage * kTileElems + 16 * wave * kD;
+    lds_dma16(kb_ptr, (static_cast<uint32_t>(min(kt + row0, last_key) * ksn) + lc0 * 8) * sizeof(T),
+              lds_offset(kst));
+    lds_dma16(kb_ptr, (static_cast<uint32_t>(min(kt + row0 + 8, last_key) * ksn) + lc1 * 8) * sizeof(T),
+              lds_offset(kst + 8 * kD));
+    lds_dma16(vt_head, v_off0 + kt * sizeof(T), lds_offset(vst));
+    lds_dma16(vt_head, v_off1 + kt * sizeof(T), lds_offset(vst + 8 * kD));
+    lds_dma4(a.bias2, (lane + kt) * 2 * sizeof(T), lds_offset(b_lds + stage * kBiasSlot));
+  };
+  auto kl = [&](int tile) { return k_lds + (tile & (kPPStages - 1)) * kTileElems; };
+  auto vl = [&](int tile) { return vt_lds + (tile & (kPPStages - 1)) * kTileElems; };
+  auto bl = [&](int tile) { return b_lds + (tile & (kPPStages - 1)) * kBiasSlot; };
+
+  f32x16 s[kQB][2];
+  op8 p[kQB][4];
+  auto pin_scores = [&]() {
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb)
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) {
+        pin_in(s[qb][sub]);
+        pin_in(w.o[qb][sub]);
+      }
+  };
+  auto pin_probs = [&]() {
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) pin_in(p[qb][t]);
+      pin_in(w.lsum[qb]);
+    }
+  };
+  auto renew_scores = [&]() {
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb)
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) pin_out(s[qb][sub]);
+  };
+  auto renew_probs = [&]() {
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) pin_out(p[qb][t]);
+  };
+
+  if (group == 0) {
+    issue(tile0);
+    issue(tile0 + 1);
+    ring_barrier<kPPDmaPerTile>();  // tile0 has landed
+    w.scores(kl(tile0), bl(tile0), s);  // H0
+    pin_scores();
+    ring_barrier<kPPDmaPerTile>();
+    renew_scores();
+    for (int tile = tile0; tile < tile1; ++tile) {
+      issue(tile + 2);  // A_j
+      w.softmax(s, kl(tile), bl(tile), p);
+      pin_probs();
+      ring_barrier<kPPDmaPerTile>();  // tile + 1 has landed
+      renew_probs();
+      // B_j.  After the last tile the scores of the look-ahead tile go unused.
+      w.pv_scores(vl(tile), p, kl(tile + 1), bl(tile + 1), s);
+      pin_scores();
+      ring_barrier<2 * kPPDmaPerTile>();
+      renew_scores();
+    }
+    ring_barrier<0>();  // H_n; the look-ahead DMAs have landed
+  } else {
+    ring_barrier<-1>();  // tile0 has landed
+    ring_barrier<-1>();  // H0
+    w.scores(kl(tile0), bl(tile0), s);  // A_0 (no P.V yet)
+    pin_scores();
+    ring_barrier<-1>();
+    renew_scores();
+    w.softmax(s, kl(tile0), bl(tile0), p);  // B_0
+    pin_probs();
+    ring_barrier<-1>();
+    for (int tile = tile0 + 1; tile < tile1; ++tile) {
+      renew_probs();
+      w.pv_scores(vl(tile - 1), p, kl(tile), bl(tile), s);  // A_j
+      pin_scores();
+      ring_barrier<-1>();
+      renew_scores();
+      w.softmax(s, kl(tile), bl(tile), p);  // B_j
+      pin_probs();
+      ring_barrier<-1>();
+    }
+    renew_probs();
+    w.pv(vl(tile1 - 1), p);  // H_n
+    pin_scores();
+    ring_barrier<-1>();
+  }
+
+  if (partial == nullptr)
+    w.store_out(a.out + b * a.osb + h * a.osh, a.osn, qw0, a.nq);
+  else
+    w.store_partial(partial, kPPQBlock, wave * kQPerWave);
 }
 
 // One work-group walks the units [sk_begin(w), sk_begin(w+1)) of the flattened
-// (task, key tile) space; a task is a (batch*head, 256-query block) pair.  A
+// (task, key tile) space; a task is a (batch*head, 512-query block) pair.  A
 // segment that covers a whole task writes the output; a segment that covers a
 // part writes its partial state (slot 0: the work-group's first segment, slot
-// 1: its last), which attn_merge_kernel combines.  With groups == tasks every
-// work-group owns exactly one whole task (no partial states).
-template <typename T, bool kDma>
-__global__ __launch_bounds__(kWaves * 64, 2) void attn_mfma_kernel(AttnArgs<T> a) {
-  constexpr int kStages = kDma ? 3 : 2;
-  __shared__ __attribute__((aligned(16))) T k_lds[kStages * kTileElems];
-  __shared__ __attribute__((aligned(16))) T vt_lds[kStages * kTileElems];
-  __shared__ __attribute__((aligned(16))) T b_lds[kStages * kBiasSlot];
+// 1: its last), which attn_merge_kernel combines.
+template <typename T>
+__global__ __launch_bounds__(kPPWaves * 64, 1) void attn_pp_kernel(AttnArgs<T> a) {
+  __shared__ __attribute__((aligned(16))) T k_lds[kPPStages * kTileElems];
+  __shared__ __attribute__((aligned(16))) T vt_lds[kPPStages * kTileElems];
+  __shared__ __attribute__((aligned(16))) T b_lds[kPPStages * kBiasSlot];
   const int64_t w = xcd_remap(blockIdx.x, gridDim.x);
   // Whole tasks: consecutive work-groups (one XCD's, after the remap) take
   // consecutive tasks of a round, so they stream one head's K/V in step and
@@ -525,7 +780,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attn_mfma_kernel(AttnArgs<T> a
     const int64_t task = w + r * a.groups;
     const int bh = static_cast<int>(task / a.n_qblocks);
     const int qblk = static_cast<int>(task - static_cast<int64_t>(bh) * a.n_qblocks);
-    attn_segment<T, kDma>(a, k_lds, vt_lds, b_lds, bh, qblk, 0, a.ntiles, nullptr);
+    attn_pp_segment<T>(a, k_lds, vt_lds, b_lds, bh, qblk, 0, a.ntiles, nullptr);
   }
   if (w >= a.tail_groups) return;
   int64_t u = sk_begin(w, a.units, a.tail_groups);
@@ -542,7 +797,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attn_mfma_kernel(AttnArgs<T> a
     float* partial = nullptr;
     if (tile0 != 0 || tile1 != a.ntiles)
       partial = a.partial + (2 * w + (first ? 0 : 1)) * static_cast<int64_t>(kPartialFloats);
-    attn_segment<T, kDma>(a, k_lds, vt_lds, b_lds, bh, qblk, tile0, tile1, partial);
+    attn_pp_segment<T>(a, k_lds, vt_lds, b_lds, bh, qblk, tile0, tile1, partial);
     u = seg_end;
     first = false;
   }
@@ -550,7 +805,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attn_mfma_kernel(AttnArgs<T> a
 
 // Combines the partial states of every tail task split across work-groups.
 // Block b handles tail task b / kMergeSplit, queries (b % kMergeSplit) *
-// kQBlock / kMergeSplit onwards; 16 threads per query, 4 dims each.  Partial
+// kPPQBlock / kMergeSplit onwards; 16 threads per query, 4 dims each.  Partial
 // states are read eight at a time so their loads overlap.
 constexpr int kMergeSplit = 8;
 template <typename T>
@@ -573,15 +828,15 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs<T> a) {
     const int slot = w == w0 ? first_slot : 0;
     return a.partial + (2 * w + slot) * static_cast<int64_t>(kPartialFloats);
   };
-  for (int ql = qpart * (kQBlock / kMergeSplit) + (threadIdx.x >> 4);
-       ql < (qpart + 1) * (kQBlock / kMergeSplit); ql += 16) {
-    const int row = qblk * kQBlock + ql;
+  for (int ql = qpart * (kPPQBlock / kMergeSplit) + (threadIdx.x >> 4);
+       ql < (qpart + 1) * (kPPQBlock / kMergeSplit); ql += 16) {
+    const int row = qblk * kPPQBlock + ql;
     if (row >= a.nq) break;
     float mmax = -__builtin_inff();
     for (int64_t wb = w0; wb <= w1; wb += 8) {
       float mv[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) mv[e] = wb + e <= w1 ? slot_ptr(wb + e)[kQBlock * kD + ql] : -__builtin_inff();
+      for (int e = 0; e < 8; ++e) mv[e] = wb + e <= w1 ? slot_ptr(wb + e)[kPPQBlock * kD + ql] : -__builtin_inff();
 #pragma unroll
       for (int e = 0; e < 8; ++e) mmax = fmaxf(mmax, mv[e]);
     }
@@ -594,8 +849,8 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs<T> a) {
       for (int e = 0; e < 8; ++e) {
         if (wb + e <= w1) {
           const float* p = slot_ptr(wb + e);
-          mv[e] = p[kQBlock * kD + ql];
-          lv[e] = p[kQBlock * kD + kQBlock + ql];
+          mv[e] = p[kPPQBlock * kD + ql];
+          lv[e] = p[kPPQBlock * kD + kPPQBlock + ql];
           xv[e] = *reinterpret_cast<const f32x4*>(p + ql * kD + d0);
         }
       }
@@ -743,7 +998,7 @@ __global__ __launch_bounds__(256) void vt_pack_kernel(const T* __restrict__ v, i
   }
 }
 
-// Resident work-groups of attn_mfma_kernel<T> on the current device (CUs x
+// Resident work-groups of attn_pp_kernel<T> on the current device (CUs x
 // blocks per CU), cached per device.
 template <typename T>
 int64_t resident_groups() {
@@ -754,8 +1009,8 @@ int64_t resident_groups() {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
       return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attn_mfma_kernel<T, true>, kWaves * 64,
-                                                     0) != hipSuccess)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attn_pp_kernel<T>, kPPWaves * 64, 0) !=
+        hipSuccess)
       return 0;
     cache[dev] = cus * (per_cu > 0 ? per_cu : 1);
   }
@@ -795,7 +1050,8 @@ int launch_mfma(const void* q, const void* k, const void* v, const void* bias, v
                 int64_t batch, int64_t heads, int64_t nq, int64_t nk, const int64_t* qs,
                 const int64_t* ks, const int64_t* vs, const int64_t* os, void* workspace,
                 size_t workspace_bytes, bool split, hipStream_t stream) {
-  const int64_t n_qblocks = (nq + kQBlock - 1) / kQBlock;
+  const int64_t qblock = split ? kPPQBlock : kQBlock;
+  const int64_t n_qblocks = (nq + qblock - 1) / qblock;
   const int64_t ntiles = (nk + kBN - 1) / kBN;
   const int64_t tasks = n_qblocks * batch * heads;
   VGO_REQUIRE(tasks <= 0x7fffffff && batch * heads <= 0xffff && ntiles < 0x7fffffff / kBN,
@@ -826,11 +1082,11 @@ int launch_mfma(const void* q, const void* k, const void* v, const void* bias, v
   a.bias2 = nullptr;
   a.npad = static_cast<int>(ntiles * kBN);
   if (!split) {
-    hipLaunchKernelGGL((attn_mfma_kernel<T, false>), dim3(static_cast<unsigned>(a.groups)),
-                       dim3(kWaves * 64), 0, stream, a);
+    hipLaunchKernelGGL((attn_reg_kernel<T>), dim3(static_cast<unsigned>(a.groups)), dim3(kWaves * 64),
+                       0, stream, a);
     return check_launch("mass_bias_attention");
   }
-  // Workspace path: pack V^T and the bias, then the LDS-DMA kernel.
+  // Workspace path: pack V^T and the bias, then the ping-pong LDS-DMA kernel.
   const int64_t groups = stream_groups<T>(tasks, tasks * ntiles);
   const AttnWorkspace ws = attn_workspace(batch * heads, ntiles, groups, sizeof(T));
   if (workspace == nullptr || workspace_bytes < ws.total)
@@ -856,7 +1112,7 @@ int launch_mfma(const void* q, const void* k, const void* v, const void* bias, v
                      a.bias, vt, bias2);
   int status = check_launch("mass_bias_attention(pack)");
   if (status != VGO_OK) return status;
-  hipLaunchKernelGGL((attn_mfma_kernel<T, true>), dim3(static_cast<unsigned>(a.groups)), dim3(kWaves * 64),
+  hipLaunchKernelGGL((attn_pp_kernel<T>), dim3(static_cast<unsigned>(a.groups)), dim3(kPPWaves * 64),
                      0, stream, a);
   status = check_launch("mass_bias_attention");
   if (status != VGO_OK || a.partial == nullptr || a.units == 0) return status;
@@ -948,7 +1204,7 @@ extern "C" int vgo_mass_bias_attn_workspace(int64_t batch, int64_t heads, int64_
   *bytes = 0;
   if (batch == 0 || heads == 0 || n_query == 0 || n_key == 0 || dtype == VGO_F32) return VGO_OK;
   VGO_REQUIRE(dtype == VGO_BF16 || dtype == VGO_F16, "mass_bias_attention: unsupported dtype");
-  const int64_t tasks = (n_query + kQBlock - 1) / kQBlock * batch * heads;
+  const int64_t tasks = (n_query + kPPQBlock - 1) / kPPQBlock * batch * heads;
   const int64_t ntiles = (n_key + kBN - 1) / kBN;
   const int64_t groups = dtype == VGO_BF16 ? stream_groups<bf16_t>(tasks, tasks * ntiles)
                                            : stream_groups<f16_t>(tasks, tasks * ntiles);
