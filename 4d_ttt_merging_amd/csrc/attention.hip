@@ -293,12 +293,12 @@ struct WaveAttn {
   }
 
   // P = exp2(x - shift) for one 32-key sub-tile (x), rounded to T and packed
-  // into B operands p[2*sub], p[2*sub+1] of O^T += V^T P^T; returns this
-  // lane's sum of the unrounded values (the reference sums its fp32
-  // probabilities).  The sum uses fp32 adds: dot instructions would share the
-  // matrix pipe with the other wave's MFMAs.
-  __device__ __forceinline__ float exp_pack(const f32x16& x, int sub, float shift, op8 (&p)[4]) const {
-    float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  // into B operands p[2*sub], p[2*sub+1] of O^T += V^T P^T.  The unrounded
+  // values are summed into part[4] (started by sub 0), as the reference sums
+  // its fp32 probabilities; the sum uses fp32 adds because dot instructions
+  // would share the matrix pipe with the other wave's MFMAs.
+  __device__ __forceinline__ void exp_pack(const f32x16& x, int sub, float shift, op8 (&p)[4],
+                                           float (&part)[4]) const {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       i32x4 packed;
@@ -307,13 +307,15 @@ struct WaveAttn {
         const int r = u * 8 + 2 * j;
         const float e0 = __builtin_amdgcn_exp2f(x[r] - shift);
         const float e1 = __builtin_amdgcn_exp2f(x[r + 1] - shift);
-        part[j] += e0;
+        part[j] = sub == 0 && u == 0 ? e0 : part[j] + e0;
         part[j] += e1;
         const op2 pr = {static_cast<T>(e0), static_cast<T>(e1)};
         packed[j] = __builtin_bit_cast(int, pr);
       }
       p[2 * sub + u] = __builtin_bit_cast(op8, packed);
     }
+  }
+  __device__ __forceinline__ static float sum4(const float (&part)[4]) {
     return (part[0] + part[1]) + (part[2] + part[3]);
   }
 
@@ -338,7 +340,12 @@ struct WaveAttn {
                                           op8 (&p)[kQB][4]) {
     float part[kQB];
 #pragma unroll
-    for (int qb = 0; qb < kQB; ++qb) part[qb] = exp_pack(s[qb][0], 0, 0.0f, p[qb]) + exp_pack(s[qb][1], 1, 0.0f, p[qb]);
+    for (int qb = 0; qb < kQB; ++qb) {
+      float acc[4];
+      exp_pack(s[qb][0], 0, 0.0f, p[qb], acc);
+      exp_pack(s[qb][1], 1, 0.0f, p[qb], acc);
+      part[qb] = sum4(acc);
+    }
     if (__builtin_expect(__ballot(!(part[0] <= kLazyLimit) | !(part[1] <= kLazyLimit)) != 0, 0)) {
       // Reload K here rather than keep the score operands alive.
       asm volatile("" ::: "memory");
@@ -366,8 +373,10 @@ struct WaveAttn {
         // No finite logit yet: every P is 0 (x = -inf).
         const float shift = mref[qb] == -__builtin_inff() ? 0.0f : mref[qb];
         asm volatile("" ::: "memory");
-        part[qb] = exp_pack(logits(kl, bl, qb, 0), 0, shift, p[qb]);
-        part[qb] += exp_pack(logits(kl, bl, qb, 1), 1, shift, p[qb]);
+        float acc[4];
+        exp_pack(logits(kl, bl, qb, 0), 0, shift, p[qb], acc);
+        exp_pack(logits(kl, bl, qb, 1), 1, shift, p[qb], acc);
+        part[qb] = sum4(acc);
       }
     }
 #pragma unroll
