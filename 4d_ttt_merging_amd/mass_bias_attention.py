@@ -20,9 +20,11 @@ def _attention_into(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                     split: bool = True) -> torch.Tensor:
     """Run the kernel on [B,H,N,64] views (any batch/head/token strides) into `out`.
 
-    split=True lets the library balance (query block, key tile) work over the
-    resident work-groups (stream-K, partial states in a workspace merged by a
-    second kernel); split=False runs one work-group per 256-query block.
+    split=True takes the workspace entry: V^T packed per head, 512-query
+    blocks on the 8-wave kernel, (query block, key tile) work balanced over
+    the resident work-groups (stream-K, partial states merged by a third
+    kernel); split=False takes the entry without a workspace (one
+    work-group per 256-query block).
     """
     lib = _lib.load()
     _lib.require_gpu(q, k, v, bias, out)

@@ -64,15 +64,16 @@ int vgo_mass_bias_attn_fwd(const void* q, const void* k, const void* v, const vo
 
 /*
  * Workspace variant of vgo_mass_bias_attn_fwd, same arguments and result.
- * The library schedules the call's 256-query blocks over the G work-groups
- * the device holds resident at once: whole blocks for floor(blocks / G)
- * rounds, then the (block, 64-key tile) units of the remaining blocks split
- * evenly (stream-K); a block whose key range is shared by several
- * work-groups is finished by a second, small kernel from fp32 partial states
- * kept in `workspace`.  Query the size with vgo_mass_bias_attn_workspace on
- * the device that will run the call; 0 bytes means no split is needed
- * (workspace may be NULL).  Replaces the same reference function as
- * vgo_mass_bias_attn_fwd.
+ * `workspace` receives V transposed per head and the key bias (packed by a
+ * first small kernel) and the fp32 partial states of split blocks.  The
+ * library schedules the call's 512-query blocks over the G work-groups the
+ * device holds resident at once: whole blocks for floor(blocks / G) rounds,
+ * then the (block, 64-key tile) units of the remaining blocks split evenly
+ * (stream-K); a block whose key range is shared by several work-groups is
+ * finished by a third, small kernel from those partial states.  Query the
+ * size with vgo_mass_bias_attn_workspace on the device that will run the
+ * call; it is 0 bytes only for empty inputs and fp32 (workspace may then be
+ * NULL).  Replaces the same reference function as vgo_mass_bias_attn_fwd.
  */
 int vgo_mass_bias_attn_workspace(int64_t batch, int64_t heads, int64_t n_query, int64_t n_key,
                                  int dtype, size_t* bytes);
