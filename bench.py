@@ -229,6 +229,29 @@ def c2_projection(vgo, device, steps):
     return out
 
 
+def simplex_solvers(device, steps):
+    """The two four-support simplex solvers on 1,048,576 rows (Gram/rhs of unit vectors).
+
+    Each row reads 80 B (G, r) and writes 16 B, so `frac` is against HBM.
+    """
+    sck = importlib.import_module("4d_ttt_merging_amd.sparse_convex_kernels")
+    n, dim = 1 << 20, 32
+    g = torch.Generator(device=device).manual_seed(9)
+    s = torch.randn(n, 4, dim, device=device, generator=g)
+    s = s / s.norm(dim=-1, keepdim=True)
+    x = torch.nn.functional.normalize(s[:, 0] + 0.7 * torch.randn(n, dim, device=device, generator=g), dim=-1)
+    gram = (s @ s.transpose(1, 2)).contiguous()
+    rhs = (s @ x.unsqueeze(-1)).squeeze(-1).contiguous()
+    del s, x
+    out = {}
+    for name, fn in (("active_set", lambda: sck.four_support_active_set(gram, rhs)),
+                     ("projected_gradient_32", lambda: sck.four_support_projected_gradient(gram, rhs, steps=32))):
+        sec = event_time(fn, steps, 3)
+        out[name] = {"rows": n, "ms": sec * 1e3, "gbs": 96 * n / sec / 1e9,
+                     "frac": 96 * n / sec / 1e9 / PEAK_HBM_GBS}
+    return out
+
+
 # ------------------------------------------------------------ CPU baseline ----
 def cpu_baseline(budget_s: float = 30.0):
     """The CPU oracle on a bounded sample of the C4 workload, extrapolated.
@@ -439,6 +462,8 @@ def main() -> int:
     result["c3_attention"] = c3_attention(vgo, device, 20)
     log("C2 projection microbench")
     result["c2_projection"] = c2_projection(vgo, device, 10)
+    log("simplex solvers microbench")
+    result["simplex_solvers"] = simplex_solvers(device, 20)
     if not args.no_reference:
         log("torch restatement of the reference path on the GPU")
         ref = TorchReferenceGlobal(FRAMES, SPECIALS + 1024, SPECIALS, GRID, 0.5, tm)

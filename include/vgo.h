@@ -261,6 +261,27 @@ int vgo_convex_fit(const void* tokens, int64_t token_row_stride, int64_t n_token
                    int64_t n, int64_t dim, float eps, float ridge, float* fit, float* alpha,
                    void* stream);
 
+/*
+ * Exact 15-active-set simplex least squares on given inputs: for each row,
+ * min_a a^T G a - 2 r^T a over the probability simplex with G + ridge I in the
+ * reduced solves, the one-hot (1,0,0,0) when r_0 beats the fit's cosine.
+ * gram [rows,4,4], rhs [rows,4], out [rows,4]: contiguous fp32, 16-byte
+ * aligned.  Replaces `four_support_active_set`
+ * (vggt_omega/models/sparse_convex_kernels.py:332-353; kernels :102-212).
+ */
+int vgo_four_support_active_set(const float* gram, const float* rhs, int64_t rows, float ridge,
+                                float* out, void* stream);
+
+/*
+ * `steps` projected-gradient iterations of the same problem (no ridge) from
+ * (1,0,0,0), step 0.95 / max(max_i sum_j |G_ij|, 1e-4), simplex projection by a
+ * four-value sorting network.  Same layouts.  Replaces
+ * `four_support_projected_gradient` (sparse_convex_kernels.py:283-296; kernel
+ * :214-280).
+ */
+int vgo_four_support_projected_gradient(const float* gram, const float* rhs, int64_t rows,
+                                        int steps, float* out, void* stream);
+
 /* Stable list of hard rows with fit < threshold and its length (sparse_convex.py:2424). */
 int vgo_failed_rows(const float* fit, const float* top1, float easy_threshold, int64_t n,
                     float threshold, int32_t* list, int* count, void* stream);
