@@ -107,33 +107,6 @@ __device__ __forceinline__ int vt_pos(int kk) {
 // written by one store, all fall in distinct banks.
 __device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 7); }
 
-// ------------------------------------------------------------ LDS DMA ----
-// global_load_lds_dword{,x4}: lane i of the wave writes 4 (16) bytes at LDS
-// byte address M0 + 4i (16i).  Issued from inline asm so the compiler does not
-// track these loads (its tracking would wait for all of them before any LDS
-// read); the kernel waits for them itself with s_waitcnt vmcnt.  None of this
-// library's kernels otherwise uses M0.  An SALU write of M0 needs one wait
-// state before an LDS-DMA instruction reads it (the s_nop).
-__device__ __forceinline__ uint32_t lds_offset(const void* p) {
-  typedef const __attribute__((address_space(3))) char* lds_ptr;
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr)(p)));
-}
-// Global address = base (wave-uniform, SGPRs) + 32-bit byte offset (per lane).
-__device__ __forceinline__ void lds_dma16(const void* base, uint32_t offset, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
-               :: "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(offset), "s"(base) : "memory");
-}
-__device__ __forceinline__ void lds_dma4(const void* base, uint32_t offset, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2"
-               :: "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(offset), "s"(base) : "memory");
-}
-// Wait until at most N vector-memory operations of this wave are outstanding.
-template <int N>
-__device__ __forceinline__ void wait_vmem() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
 template <typename T>
 struct AttnArgs {
   const T* q;

@@ -313,6 +313,252 @@ __global__ __launch_bounds__(256, 2) void sim_topk_kernel(
   }
 }
 
+// ------------------------------------------------------ LDS-DMA ring ----
+// The same 128 x 128 work-group tile, per-wave 64 x 64 MFMA blocks and
+// epilogue, with operands brought in by LDS DMA (global_load_lds_dwordx4) in
+// 32-wide K chunks through a 4-stage ring, three chunks ahead: a dictionary
+// or source row that comes from MALL or HBM takes longer than one chunk's
+// MFMAs, which is all the register staging above can hide.  LDS rows are 64 B;
+// their four 16-byte chunks are XOR-permuted by sw4(row) = (row >> 2) & 3, so
+// the operand reads (16 rows at one logical chunk per quarter-wave) are
+// conflict-free.  Requires dim % 32 == 0.  Invalid source row ids read row 0
+// through the DMA and score 0 in the epilogue, as in the staged kernel.
+constexpr int kRKc = 32;
+constexpr int kRStages = 4;
+constexpr int kRTileElems = kTile * kRKc;
+constexpr int kRDmaPerStep = 4;  // per wave: two 16-row blocks of each operand
+__device__ __forceinline__ int sw4(int row) { return (row >> 2) & 3; }
+
+template <int K>
+__global__ __launch_bounds__(256, 2) void sim_topk_ring_kernel(
+    const bf16_t* __restrict__ src, int64_t src_stride, int64_t src_capacity,
+    const int64_t* __restrict__ src_rows, const int* __restrict__ n_src_dev, int n_src,
+    const bf16_t* __restrict__ dict,
+    int64_t dict_stride, int n0, int off1, int n_dict, int dim, int tiles_per_part,
+    uint64_t* __restrict__ partial, int parts, bf16_t* __restrict__ scores,
+    int64_t scores_stride) {
+  __shared__ __attribute__((aligned(16))) bf16_t a_lds[kRStages * kRTileElems];
+  __shared__ __attribute__((aligned(16))) bf16_t b_lds[kRStages * kRTileElems];
+
+  int ns = n_src;
+  if (n_src_dev) ns = min(ns, *n_src_dev);
+  const int task = xcd_remap(blockIdx.x, gridDim.x);
+  const int s0 = (task / parts) * kTile;
+  if (s0 >= ns) return;
+  const int part = task % parts;
+  const int d_begin = part * tiles_per_part * kTile;
+  const int d_end = min(n_dict, d_begin + tiles_per_part * kTile);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wd = wave & 1;
+  const int ws = wave >> 1;
+  const int l32 = lane & 31;
+  const int hh = lane >> 5;
+
+  // DMA lanes: a 1 KB block is 16 rows x 4 physical chunks; lane i fills row
+  // i/4, physical chunk i%4 with logical chunk (i%4) ^ sw4(row).  This wave
+  // loads rows 32*wave + 16*j + i/4 (j = 0, 1) of both operands.
+  const int dr = lane >> 2;
+  const int dpc = lane & 3;
+  const bf16_t* src_p[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int r = 32 * wave + 16 * j + dr;
+    const int i = s0 + r;
+    const int64_t row = i < ns ? (src_rows ? src_rows[i] : i) : 0;
+    const bool ok = row >= 0 && row < src_capacity;
+    src_p[j] = src + (ok ? row : 0) * src_stride + 8 * (dpc ^ sw4(r));
+  }
+  // Epilogue sources of this lane (lane = source row): an invalid row id scores 0.
+  bool src_ok[2];
+#pragma unroll
+  for (int sb = 0; sb < 2; ++sb) {
+    const int i = s0 + 64 * ws + 32 * sb + l32;
+    const int64_t row = i < ns ? (src_rows ? src_rows[i] : i) : 0;
+    src_ok[sb] = row >= 0 && row < src_capacity;
+  }
+  const bool all_src_ok = __ballot(!(src_ok[0] & src_ok[1])) == 0;
+
+  const int n_chunks = dim / kRKc;
+  const int n_dtiles = d_end > d_begin ? (d_end - d_begin + kTile - 1) / kTile : 0;
+  const int n_steps = n_dtiles * n_chunks;
+
+  const bf16_t* dict_p[2] = {dict, dict};
+  int cur_dt = -1;
+  auto set_dtile = [&](int dt) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int r = 32 * wave + 16 * j + dr;
+      const int jj = min(d_begin + dt * kTile + r, d_end - 1);  // rows past the end repeat a valid row
+      const int row = jj < n0 ? jj : off1 + (jj - n0);
+      dict_p[j] = dict + static_cast<int64_t>(row) * dict_stride + 8 * (dpc ^ sw4(r));
+    }
+    cur_dt = dt;
+  };
+  // Issues step `st` (clamped to the last step: the look-ahead past the end
+  // re-reads valid rows into a stage nobody reads again) into stage st & 3.
+  auto issue = [&](int st) {
+    const int sc = min(st, n_steps - 1);
+    const int dt = sc / n_chunks;
+    const int kc = (sc - dt * n_chunks) * kRKc;
+    if (dt != cur_dt) set_dtile(dt);
+    const int stage = st & (kRStages - 1);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int blk = (32 * wave + 16 * j) * kRKc;
+      lds_dma16_addr(dict_p[j] + kc, lds_offset(a_lds + stage * kRTileElems + blk));
+      lds_dma16_addr(src_p[j] + kc, lds_offset(b_lds + stage * kRTileElems + blk));
+    }
+  };
+  // Operand read offsets (elements) within a 32-row block: logical chunk 2t+hh
+  // of row l32; sw4 of rows x*32 + l32 + 64*half depends on l32 only.
+  int off[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) off[t] = l32 * kRKc + (((2 * t + hh) ^ sw4(l32)) << 3);
+
+  TopK<K> best[2];
+  best[0].init();
+  best[1].init();
+  float top_v[2] = {-__builtin_inff(), -__builtin_inff()};
+  int top_j[2] = {-1, -1};
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) acc[x][y] = f32x16{};
+
+  if (n_steps > 0) {
+    // The index loads above complete here, so no compiler-inserted wait for
+    // them (which would count the untracked DMAs too) lands in the ring.
+    wait_vmem<0>();
+    issue(0);
+    issue(1);
+    issue(2);
+    wait_vmem<2 * kRDmaPerStep>();  // step 0 has landed
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  }
+  int dt = 0, kcs = 0;
+  for (int step = 0; step < n_steps; ++step) {
+    issue(step + 3);
+    const int stage = step & (kRStages - 1);
+    const bf16_t* al = a_lds + stage * kRTileElems + wd * 64 * kRKc;
+    const bf16_t* bl = b_lds + stage * kRTileElems + ws * 64 * kRKc;
+    bf16x8 a[2][2], b[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        a[t][x] = *reinterpret_cast<const bf16x8*>(al + x * 32 * kRKc + off[t]);
+        b[t][x] = *reinterpret_cast<const bf16x8*>(bl + x * 32 * kRKc + off[t]);
+      }
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < 2; ++y)
+          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[t][x], b[t][y], acc[x][y], 0, 0, 0);
+    if (kcs == n_chunks - 1) {
+      if (!all_src_ok) {
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+          for (int db = 0; db < 2; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[db][sb][r] = src_ok[sb] ? acc[db][sb][r] : 0.0f;
+      }
+      const int d0 = d_begin + dt * kTile;
+      if (scores) {
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) {
+          const int i = s0 + 64 * ws + 32 * sb + l32;
+#pragma unroll
+          for (int db = 0; db < 2; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int jj = d0 + 64 * wd + 32 * db + 8 * (r >> 2) + 4 * hh + (r & 3);
+              if (jj < d_end && i < ns)
+                scores[static_cast<int64_t>(i) * scores_stride + jj] = static_cast<bf16_t>(acc[db][sb][r]);
+            }
+        }
+      }
+      const int jl = d0 + 64 * wd + 4 * hh;
+      if (K == 1) {
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+          for (int db = 0; db < 2; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int jj = jl + 32 * db + 8 * (r >> 2) + (r & 3);
+              const float v = bf16_round(acc[db][sb][r]);
+              const bool take = (jj < d_end) & ((v > top_v[sb]) | ((v != v) & (top_v[sb] == top_v[sb])));
+              top_v[sb] = take ? v : top_v[sb];
+              top_j[sb] = take ? jj : top_j[sb];
+            }
+      } else {
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+          for (int db = 0; db < 2; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int jj = jl + 32 * db + 8 * (r >> 2) + (r & 3);
+              if (jj < d_end) best[sb].insert(make_key(acc[db][sb][r], jj));
+            }
+      }
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int db = 0; db < 2; ++db) acc[db][sb] = f32x16{};
+      kcs = 0;
+      ++dt;
+    } else {
+      ++kcs;
+    }
+    // This wave's reads of the stage are complete and its DMAs of step + 1
+    // have landed; after the barrier every wave's have.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    wait_vmem<2 * kRDmaPerStep>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  }
+  // The look-ahead DMAs land before the ring's LDS is reused for the merge.
+  wait_vmem<0>();
+  __syncthreads();
+
+  if (K == 1) {
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb)
+      if (top_j[sb] >= 0) best[sb].k[0] = make_key(top_v[sb], top_j[sb]);
+  }
+  uint64_t* m_lds = reinterpret_cast<uint64_t*>(a_lds);  // [128 sources][4 lists][K]
+#pragma unroll
+  for (int sb = 0; sb < 2; ++sb) {
+    const int local = 64 * ws + 32 * sb + l32;
+#pragma unroll
+    for (int t = 0; t < K; ++t) m_lds[(local * 4 + wd * 2 + hh) * K + t] = best[sb].k[t];
+  }
+  __syncthreads();
+  if (tid < kTile) {
+    const int i = s0 + tid;
+    if (i < ns) {
+      TopK<K> m;
+      m.init();
+#pragma unroll
+      for (int l = 0; l < 4; ++l)
+#pragma unroll
+        for (int t = 0; t < K; ++t) m.insert(m_lds[(tid * 4 + l) * K + t]);
+      uint64_t* out = partial + (static_cast<int64_t>(i) * parts + part) * K;
+#pragma unroll
+      for (int t = 0; t < K; ++t) out[t] = m.k[t];
+    }
+  }
+}
+
 // Merge `parts` partial lists per source row; decode keys into the bf16 score
 // (as fp32) and the dictionary row (optionally mapped through index_map).
 template <int K>
@@ -346,29 +592,37 @@ __global__ __launch_bounds__(256) void topk_finalize_kernel(
   }
 }
 
-// Resident work-groups of sim_topk_kernel<K> on the current device, cached.
+// The ring kernel runs when the dimension is a whole number of its K chunks.
+inline bool use_ring(int64_t dim) { return dim % kRKc == 0; }
+
+// Resident work-groups of the similarity kernel on the current device, cached.
 template <int K>
-int64_t resident_groups() {
-  static int cache[64] = {};
+int64_t resident_groups(bool ring) {
+  static int cache[2][64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
-  if (cache[dev] == 0) {
+  if (cache[ring][dev] == 0) {
     int cus = 0, per_cu = 0;
+    const hipError_t occ =
+        ring ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, sim_topk_ring_kernel<K>, 256, 0)
+             : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, sim_topk_kernel<K>, 256, 0);
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, sim_topk_kernel<K>, 256, 0) != hipSuccess)
+        occ != hipSuccess)
       return 512;
-    cache[dev] = cus * (per_cu > 0 ? per_cu : 1);
+    cache[ring][dev] = cus * (per_cu > 0 ? per_cu : 1);
   }
-  return cache[dev];
+  return cache[ring][dev];
 }
 
 // Dictionary split: the number of parts that minimises (rounds of resident
 // work-groups) x (dictionary tiles per work-group + a half-tile fixed cost).
+// Both kernels hold 64 KB of LDS and run two work-groups per CU, so the split
+// does not depend on which one runs.
 int choose_parts(int64_t n_src, int64_t n_dict, int topk) {
   const int64_t src_tiles = (n_src + kTile - 1) / kTile;
   const int64_t dict_tiles = (n_dict + kTile - 1) / kTile;
   if (src_tiles <= 0 || dict_tiles <= 0) return 1;
-  const int64_t slots = topk == 1 ? resident_groups<1>() : resident_groups<4>();
+  const int64_t slots = topk == 1 ? resident_groups<1>(true) : resident_groups<4>(true);
   int best = 1;
   double best_cost = 1e300;
   for (int64_t p = 1; p <= dict_tiles && p <= 4096; ++p) {
@@ -435,24 +689,40 @@ extern "C" int vgo_similarity_topk(const void* src, int64_t src_row_stride, int6
   const bf16_t* dp = static_cast<const bf16_t*>(dict);
   bf16_t* sc = static_cast<bf16_t*>(scores);
   const int blocks2 = static_cast<int>((n_src + 255) / 256);
-  if (topk == 1) {
+  const bool ring = use_ring(dim);
+  if (ring) {
+    // 64-bit row addresses per lane; the DMA reads stay inside the buffers
+    // (rows are clamped, dim is a multiple of the chunk).
+    if (topk == 1)
+      hipLaunchKernelGGL((sim_topk_ring_kernel<1>), grid, dim3(256), 0, s, sp, src_row_stride, src_capacity,
+                         src_rows, n_src_device, static_cast<int>(n_src), dp, dict_row_stride,
+                         static_cast<int>(dict_n0), static_cast<int>(dict_off1), static_cast<int>(n_dict),
+                         static_cast<int>(dim), tiles_per_part, partial, parts, sc, scores_row_stride);
+    else
+      hipLaunchKernelGGL((sim_topk_ring_kernel<4>), grid, dim3(256), 0, s, sp, src_row_stride, src_capacity,
+                         src_rows, n_src_device, static_cast<int>(n_src), dp, dict_row_stride,
+                         static_cast<int>(dict_n0), static_cast<int>(dict_off1), static_cast<int>(n_dict),
+                         static_cast<int>(dim), tiles_per_part, partial, parts, sc, scores_row_stride);
+  } else if (topk == 1) {
     hipLaunchKernelGGL((sim_topk_kernel<1>), grid, dim3(256), 0, s, sp, src_row_stride, src_capacity, src_rows,
                        n_src_device, static_cast<int>(n_src), dp, dict_row_stride,
                        static_cast<int>(dict_n0), static_cast<int>(dict_off1),
                        static_cast<int>(n_dict), static_cast<int>(dim), tiles_per_part, partial,
                        parts, sc, scores_row_stride);
-    hipLaunchKernelGGL((topk_finalize_kernel<1>), dim3(blocks2), dim3(256), 0, s, partial,
-                       static_cast<int>(n_src), n_src_device, parts, static_cast<int>(dict_n0),
-                       static_cast<int>(dict_off1), values, index64, index32, index_map);
   } else {
     hipLaunchKernelGGL((sim_topk_kernel<4>), grid, dim3(256), 0, s, sp, src_row_stride, src_capacity, src_rows,
                        n_src_device, static_cast<int>(n_src), dp, dict_row_stride,
                        static_cast<int>(dict_n0), static_cast<int>(dict_off1),
                        static_cast<int>(n_dict), static_cast<int>(dim), tiles_per_part, partial,
                        parts, sc, scores_row_stride);
+  }
+  if (topk == 1)
+    hipLaunchKernelGGL((topk_finalize_kernel<1>), dim3(blocks2), dim3(256), 0, s, partial,
+                       static_cast<int>(n_src), n_src_device, parts, static_cast<int>(dict_n0),
+                       static_cast<int>(dict_off1), values, index64, index32, index_map);
+  else
     hipLaunchKernelGGL((topk_finalize_kernel<4>), dim3(blocks2), dim3(256), 0, s, partial,
                        static_cast<int>(n_src), n_src_device, parts, static_cast<int>(dict_n0),
                        static_cast<int>(dict_off1), values, index64, index32, index_map);
-  }
   return check_launch("similarity_topk");
 }

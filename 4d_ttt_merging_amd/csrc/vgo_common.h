@@ -66,4 +66,38 @@ __device__ __forceinline__ int xcd_remap(int pid, int total) {
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
+// ------------------------------------------------------------ LDS DMA ----
+// global_load_lds_dword{,x4}: lane i of the wave writes 4 (16) bytes at LDS
+// byte address M0 + 4i (16i).  Issued from inline asm so the compiler does not
+// track these loads (its tracking would wait for all of them before any LDS
+// read); kernels wait for them with wait_vmem.  Because vmcnt is in order, any
+// wait the compiler inserts for its own memory operations (a spill reload)
+// also waits for every DMA in flight, so loops that issue DMAs must not spill.
+// No kernel of this library otherwise uses M0.  An SALU write of M0 needs one
+// wait state before an LDS-DMA instruction reads it (the s_nop).
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  typedef const __attribute__((address_space(3))) char* lds_ptr;
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr)(p)));
+}
+// Global address = base (wave-uniform, SGPRs) + 32-bit byte offset (per lane).
+__device__ __forceinline__ void lds_dma16(const void* base, uint32_t offset, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :: "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(offset), "s"(base) : "memory");
+}
+__device__ __forceinline__ void lds_dma4(const void* base, uint32_t offset, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2"
+               :: "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(offset), "s"(base) : "memory");
+}
+// Per-lane 64-bit global address.
+__device__ __forceinline__ void lds_dma16_addr(const void* addr, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :: "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(addr) : "memory");
+}
+// Wait until at most N vector-memory operations of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
 }  // namespace vgo

@@ -71,7 +71,7 @@ def test_normalize_rows(kern, device, dim, eps):
 
 # ------------------------------------------------------------- matching ----
 @pytest.mark.parametrize("topk", [1, 4])
-@pytest.mark.parametrize("ns,nd,dim", [(37, 11, 64), (300, 777, 1024), (1000, 130, 128)])
+@pytest.mark.parametrize("ns,nd,dim", [(37, 11, 64), (300, 777, 1024), (1000, 130, 128), (260, 300, 72)])
 def test_similarity_selection_is_exact_on_kernel_scores(kern, device, topk, ns, nd, dim):
     print(f"[similarity] topk={topk} ns={ns} nd={nd} dim={dim}", flush=True)
     g = torch.Generator().manual_seed(ns + nd + topk)
@@ -113,6 +113,30 @@ def test_similarity_ranges_rows_and_device_count(kern, device):
     assert torch.equal(values[:211].cpu(), ref_v)
     assert torch.equal(index[:211].cpu(), index_map[positions[ref_i]])
     assert torch.isnan(scores[211:].float()).all()  # rows past the device count are untouched
+
+
+@pytest.mark.parametrize("dim", [256, 72])
+def test_similarity_invalid_source_ids_score_zero(kern, device, dim):
+    # Row ids outside the source buffer read as zero rows: every score is 0 and
+    # the lowest dictionary indices win (both kernels: dim 256 and dim 72).
+    g = torch.Generator().manual_seed(6)
+    src = F.normalize(torch.randn(200, dim, generator=g), dim=-1).bfloat16()
+    dst = F.normalize(torch.randn(300, dim, generator=g), dim=-1).bfloat16()
+    rows = torch.arange(200)
+    rows[[0, 77, 150]] = torch.tensor([200, 10 ** 6, -1])
+    for topk in (1, 4):
+        values, index = kern.similarity_topk(src.to(device), dst.to(device), topk, src_rows=rows.to(device),
+                                             n_src=200)
+        v, i = values.cpu(), index.cpu()
+        for r in (0, 77, 150):
+            assert torch.equal(v[r].reshape(-1), torch.zeros(topk))
+            assert torch.equal(i[r].reshape(-1), torch.arange(topk))
+        good = torch.ones(200, dtype=torch.bool)
+        good[[0, 77, 150]] = False
+        exact = om.bf16_scores(src[rows[good]], dst)
+        ref_v, ref_i = om.topk_lowest_index(exact, topk)
+        ok = (v[good].reshape(ref_v.shape) == ref_v).all(-1)
+        assert ok.float().mean() > 0.99  # exact-dot ties aside (see the selection test)
 
 
 def test_streaming_top4_api(vgo, device):
