@@ -20,6 +20,8 @@
 // (orderable bf16 score << 32 | ~j).  Work-groups split the dictionary into
 // `parts`; a second kernel merges the per-part lists.  Keys make the result
 // independent of evaluation order, so it is deterministic.
+#include <algorithm>
+
 #include "vgo_common.h"
 
 namespace vgo {
@@ -314,23 +316,27 @@ __global__ __launch_bounds__(256, 2) void sim_topk_kernel(
 }
 
 // ------------------------------------------------------ LDS-DMA ring ----
-// The same 128 x 128 work-group tile, per-wave 64 x 64 MFMA blocks and
-// epilogue, with operands brought in by LDS DMA (global_load_lds_dwordx4) in
-// 32-wide K chunks through a 4-stage ring, three chunks ahead: a dictionary
-// or source row that comes from MALL or HBM takes longer than one chunk's
-// MFMAs, which is all the register staging above can hide.  LDS rows are 64 B;
-// their four 16-byte chunks are XOR-permuted by sw4(row) = (row >> 2) & 3, so
-// the operand reads (16 rows at one logical chunk per quarter-wave) are
-// conflict-free.  Requires dim % 32 == 0.  Invalid source row ids read row 0
-// through the DMA and score 0 in the epilogue, as in the staged kernel.
+// Work-group tile 256 dictionary x 256 source rows, 8 waves of 128 x 64
+// (four 32-row dictionary blocks by two 32-column source blocks, accumulators
+// transposed as in the staged kernel), one work-group per CU.  A tile pair
+// moves 1 MB for 134 MFLOP -- twice the 128 x 128 tile's arithmetic per byte,
+// the fabric (L2 / MALL) being what bounds this kernel.  Operands arrive by
+// LDS DMA (global_load_lds_dwordx4) in 32-wide K chunks through a 4-stage
+// ring, three chunks ahead.  LDS rows are 64 B; their four 16-byte chunks are
+// XOR-permuted by sw4(row) = (row >> 2) & 3, so the operand reads (16 rows at
+// one logical chunk per quarter-wave) are conflict-free.  Requires
+// dim % 32 == 0.  Invalid source row ids read row 0 through the DMA and score
+// 0 in the epilogue, as in the staged kernel.
+constexpr int kRTile = 256;
+constexpr int kRWaves = 8;
 constexpr int kRKc = 32;
 constexpr int kRStages = 4;
-constexpr int kRTileElems = kTile * kRKc;
+constexpr int kRTileElems = kRTile * kRKc;
 constexpr int kRDmaPerStep = 4;  // per wave: two 16-row blocks of each operand
 __device__ __forceinline__ int sw4(int row) { return (row >> 2) & 3; }
 
 template <int K>
-__global__ __launch_bounds__(256, 2) void sim_topk_ring_kernel(
+__global__ __launch_bounds__(kRWaves * 64, 1) void sim_topk_ring_kernel(
     const bf16_t* __restrict__ src, int64_t src_stride, int64_t src_capacity,
     const int64_t* __restrict__ src_rows, const int* __restrict__ n_src_dev, int n_src,
     const bf16_t* __restrict__ dict,
@@ -343,17 +349,17 @@ __global__ __launch_bounds__(256, 2) void sim_topk_ring_kernel(
   int ns = n_src;
   if (n_src_dev) ns = min(ns, *n_src_dev);
   const int task = xcd_remap(blockIdx.x, gridDim.x);
-  const int s0 = (task / parts) * kTile;
+  const int s0 = (task / parts) * kRTile;
   if (s0 >= ns) return;
   const int part = task % parts;
-  const int d_begin = part * tiles_per_part * kTile;
-  const int d_end = min(n_dict, d_begin + tiles_per_part * kTile);
+  const int d_begin = part * tiles_per_part * kRTile;
+  const int d_end = min(n_dict, d_begin + tiles_per_part * kRTile);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wd = wave & 1;
-  const int ws = wave >> 1;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wd = wave & 1;   // dictionary half (128 rows)
+  const int ws = wave >> 1;  // source quarter (64 rows)
   const int l32 = lane & 31;
   const int hh = lane >> 5;
 
@@ -382,7 +388,7 @@ __global__ __launch_bounds__(256, 2) void sim_topk_ring_kernel(
   const bool all_src_ok = __ballot(!(src_ok[0] & src_ok[1])) == 0;
 
   const int n_chunks = dim / kRKc;
-  const int n_dtiles = d_end > d_begin ? (d_end - d_begin + kTile - 1) / kTile : 0;
+  const int n_dtiles = d_end > d_begin ? (d_end - d_begin + kRTile - 1) / kRTile : 0;
   const int n_steps = n_dtiles * n_chunks;
 
   const bf16_t* dict_p[2] = {dict, dict};
@@ -391,7 +397,7 @@ __global__ __launch_bounds__(256, 2) void sim_topk_ring_kernel(
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int r = 32 * wave + 16 * j + dr;
-      const int jj = min(d_begin + dt * kTile + r, d_end - 1);  // rows past the end repeat a valid row
+      const int jj = min(d_begin + dt * kRTile + r, d_end - 1);  // rows past the end repeat a valid row
       const int row = jj < n0 ? jj : off1 + (jj - n0);
       dict_p[j] = dict + static_cast<int64_t>(row) * dict_stride + 8 * (dpc ^ sw4(r));
     }
@@ -413,7 +419,7 @@ __global__ __launch_bounds__(256, 2) void sim_topk_ring_kernel(
     }
   };
   // Operand read offsets (elements) within a 32-row block: logical chunk 2t+hh
-  // of row l32; sw4 of rows x*32 + l32 + 64*half depends on l32 only.
+  // of row l32; sw4 of rows 32*x + l32 + base depends on l32 only.
   int off[2];
 #pragma unroll
   for (int t = 0; t < 2; ++t) off[t] = l32 * kRKc + (((2 * t + hh) ^ sw4(l32)) << 3);
@@ -423,9 +429,9 @@ __global__ __launch_bounds__(256, 2) void sim_topk_ring_kernel(
   best[1].init();
   float top_v[2] = {-__builtin_inff(), -__builtin_inff()};
   int top_j[2] = {-1, -1};
-  f32x16 acc[2][2];
+  f32x16 acc[4][2];
 #pragma unroll
-  for (int x = 0; x < 2; ++x)
+  for (int x = 0; x < 4; ++x)
 #pragma unroll
     for (int y = 0; y < 2; ++y) acc[x][y] = f32x16{};
 
@@ -444,20 +450,20 @@ __global__ __launch_bounds__(256, 2) void sim_topk_ring_kernel(
   for (int step = 0; step < n_steps; ++step) {
     issue(step + 3);
     const int stage = step & (kRStages - 1);
-    const bf16_t* al = a_lds + stage * kRTileElems + wd * 64 * kRKc;
+    const bf16_t* al = a_lds + stage * kRTileElems + wd * 128 * kRKc;
     const bf16_t* bl = b_lds + stage * kRTileElems + ws * 64 * kRKc;
-    bf16x8 a[2][2], b[2][2];
+    bf16x8 a[2][4], b[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int x = 0; x < 4; ++x) a[t][x] = *reinterpret_cast<const bf16x8*>(al + x * 32 * kRKc + off[t]);
+#pragma unroll
+      for (int y = 0; y < 2; ++y) b[t][y] = *reinterpret_cast<const bf16x8*>(bl + y * 32 * kRKc + off[t]);
+    }
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int x = 0; x < 2; ++x) {
-        a[t][x] = *reinterpret_cast<const bf16x8*>(al + x * 32 * kRKc + off[t]);
-        b[t][x] = *reinterpret_cast<const bf16x8*>(bl + x * 32 * kRKc + off[t]);
-      }
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int x = 0; x < 2; ++x)
+      for (int x = 0; x < 4; ++x)
 #pragma unroll
         for (int y = 0; y < 2; ++y)
           acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[t][x], b[t][y], acc[x][y], 0, 0, 0);
@@ -466,31 +472,34 @@ __global__ __launch_bounds__(256, 2) void sim_topk_ring_kernel(
 #pragma unroll
         for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
-          for (int db = 0; db < 2; ++db)
+          for (int db = 0; db < 4; ++db)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[db][sb][r] = src_ok[sb] ? acc[db][sb][r] : 0.0f;
       }
-      const int d0 = d_begin + dt * kTile;
+      const int d0 = d_begin + dt * kRTile;
       if (scores) {
 #pragma unroll
         for (int sb = 0; sb < 2; ++sb) {
           const int i = s0 + 64 * ws + 32 * sb + l32;
 #pragma unroll
-          for (int db = 0; db < 2; ++db)
+          for (int db = 0; db < 4; ++db)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-              const int jj = d0 + 64 * wd + 32 * db + 8 * (r >> 2) + 4 * hh + (r & 3);
+              const int jj = d0 + 128 * wd + 32 * db + 8 * (r >> 2) + 4 * hh + (r & 3);
               if (jj < d_end && i < ns)
                 scores[static_cast<int64_t>(i) * scores_stride + jj] = static_cast<bf16_t>(acc[db][sb][r]);
             }
         }
       }
-      const int jl = d0 + 64 * wd + 4 * hh;
+      const int jl = d0 + 128 * wd + 4 * hh;  // this lane's first dictionary row
       if (K == 1) {
+        // Running top-1 on the bf16-rounded score: a later (higher) j wins only
+        // when strictly greater, which is the lower-index rule for ties; a NaN
+        // wins over numbers and the first NaN is kept (ranking of the keys).
 #pragma unroll
         for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
-          for (int db = 0; db < 2; ++db)
+          for (int db = 0; db < 4; ++db)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
               const int jj = jl + 32 * db + 8 * (r >> 2) + (r & 3);
@@ -503,7 +512,7 @@ __global__ __launch_bounds__(256, 2) void sim_topk_ring_kernel(
 #pragma unroll
         for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
-          for (int db = 0; db < 2; ++db)
+          for (int db = 0; db < 4; ++db)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
               const int jj = jl + 32 * db + 8 * (r >> 2) + (r & 3);
@@ -513,7 +522,7 @@ __global__ __launch_bounds__(256, 2) void sim_topk_ring_kernel(
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
-        for (int db = 0; db < 2; ++db) acc[db][sb] = f32x16{};
+        for (int db = 0; db < 4; ++db) acc[db][sb] = f32x16{};
       kcs = 0;
       ++dt;
     } else {
@@ -535,7 +544,8 @@ __global__ __launch_bounds__(256, 2) void sim_topk_ring_kernel(
     for (int sb = 0; sb < 2; ++sb)
       if (top_j[sb] >= 0) best[sb].k[0] = make_key(top_v[sb], top_j[sb]);
   }
-  uint64_t* m_lds = reinterpret_cast<uint64_t*>(a_lds);  // [128 sources][4 lists][K]
+  // Merge the four lists of every source row (two dictionary halves x two lane halves).
+  uint64_t* m_lds = reinterpret_cast<uint64_t*>(a_lds);  // [256 sources][4 lists][K]
 #pragma unroll
   for (int sb = 0; sb < 2; ++sb) {
     const int local = 64 * ws + 32 * sb + l32;
@@ -543,7 +553,7 @@ __global__ __launch_bounds__(256, 2) void sim_topk_ring_kernel(
     for (int t = 0; t < K; ++t) m_lds[(local * 4 + wd * 2 + hh) * K + t] = best[sb].k[t];
   }
   __syncthreads();
-  if (tid < kTile) {
+  if (tid < kRTile) {
     const int i = s0 + tid;
     if (i < ns) {
       TopK<K> m;
@@ -592,37 +602,38 @@ __global__ __launch_bounds__(256) void topk_finalize_kernel(
   }
 }
 
-// The ring kernel runs when the dimension is a whole number of its K chunks.
-inline bool use_ring(int64_t dim) { return dim % kRKc == 0; }
 
 // Resident work-groups of the similarity kernel on the current device, cached.
 template <int K>
 int64_t resident_groups(bool ring) {
   static int cache[2][64] = {};
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return ring ? 256 : 512;
   if (cache[ring][dev] == 0) {
     int cus = 0, per_cu = 0;
     const hipError_t occ =
-        ring ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, sim_topk_ring_kernel<K>, 256, 0)
+        ring ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, sim_topk_ring_kernel<K>, kRWaves * 64, 0)
              : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, sim_topk_kernel<K>, 256, 0);
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         occ != hipSuccess)
-      return 512;
+      return ring ? 256 : 512;
     cache[ring][dev] = cus * (per_cu > 0 ? per_cu : 1);
   }
   return cache[ring][dev];
 }
 
-// Dictionary split: the number of parts that minimises (rounds of resident
-// work-groups) x (dictionary tiles per work-group + a half-tile fixed cost).
-// Both kernels hold 64 KB of LDS and run two work-groups per CU, so the split
-// does not depend on which one runs.
-int choose_parts(int64_t n_src, int64_t n_dict, int topk) {
-  const int64_t src_tiles = (n_src + kTile - 1) / kTile;
-  const int64_t dict_tiles = (n_dict + kTile - 1) / kTile;
+// The ring kernel runs when the dimension is a whole number of its K chunks.
+inline bool use_ring(int64_t dim) { return dim % kRKc == 0; }
+
+// Dictionary split for a kernel with `tile` x `tile` steps: the number of parts
+// that minimises (rounds of resident work-groups) x (dictionary tiles per
+// work-group + a half-tile fixed cost).
+int choose_parts(int64_t n_src, int64_t n_dict, int topk, bool ring) {
+  const int64_t tile = ring ? kRTile : kTile;
+  const int64_t src_tiles = (n_src + tile - 1) / tile;
+  const int64_t dict_tiles = (n_dict + tile - 1) / tile;
   if (src_tiles <= 0 || dict_tiles <= 0) return 1;
-  const int64_t slots = topk == 1 ? resident_groups<1>(true) : resident_groups<4>(true);
+  const int64_t slots = topk == 1 ? resident_groups<1>(ring) : resident_groups<4>(ring);
   int best = 1;
   double best_cost = 1e300;
   for (int64_t p = 1; p <= dict_tiles && p <= 4096; ++p) {
@@ -645,7 +656,8 @@ extern "C" int vgo_similarity_topk_workspace(int64_t n_src, int64_t n_dict, int 
   using namespace vgo;
   VGO_REQUIRE(topk == 1 || topk == 4, "similarity_topk: topk must be 1 or 4");
   VGO_REQUIRE(n_src >= 0 && n_dict >= 0, "similarity_topk: negative size");
-  const int p = choose_parts(n_src, n_dict, topk);
+  // Sized for whichever kernel the dimension selects.
+  const int p = std::max(choose_parts(n_src, n_dict, topk, true), choose_parts(n_src, n_dict, topk, false));
   if (parts) *parts = p;
   if (bytes) *bytes = static_cast<size_t>(n_src) * p * topk * sizeof(uint64_t);
   return VGO_OK;
@@ -673,15 +685,16 @@ extern "C" int vgo_similarity_topk(const void* src, int64_t src_row_stride, int6
                   dict_off1 + (n_dict - dict_n0) <= dict_capacity,
               "similarity_topk: dictionary ranges exceed the dictionary");
   VGO_REQUIRE(src_rows || n_src <= src_capacity, "similarity_topk: more sources than rows");
-  int parts = 0;
-  size_t need = 0;
-  vgo_similarity_topk_workspace(n_src, n_dict, topk, &parts, &need);
+  const bool ring = use_ring(dim);
+  const int parts = choose_parts(n_src, n_dict, topk, ring);
+  const size_t need = static_cast<size_t>(n_src) * parts * topk * sizeof(uint64_t);
   VGO_REQUIRE(workspace && workspace_bytes >= need, "similarity_topk: workspace too small");
   VGO_REQUIRE(aligned(workspace, 8), "similarity_topk: workspace must be 8-byte aligned");
-  const int64_t dict_tiles = (n_dict + kTile - 1) / kTile;
+  const int64_t tile = ring ? kRTile : kTile;
+  const int64_t dict_tiles = (n_dict + tile - 1) / tile;
   const int tiles_per_part = static_cast<int>((dict_tiles + parts - 1) / parts);
   hipStream_t s = as_stream(stream);
-  const int64_t src_tiles = (n_src + kTile - 1) / kTile;
+  const int64_t src_tiles = (n_src + tile - 1) / tile;
   VGO_REQUIRE(src_tiles * parts < (1LL << 31), "similarity_topk: grid too large");
   dim3 grid(static_cast<unsigned>(src_tiles * parts));
   uint64_t* partial = static_cast<uint64_t*>(workspace);
@@ -689,17 +702,16 @@ extern "C" int vgo_similarity_topk(const void* src, int64_t src_row_stride, int6
   const bf16_t* dp = static_cast<const bf16_t*>(dict);
   bf16_t* sc = static_cast<bf16_t*>(scores);
   const int blocks2 = static_cast<int>((n_src + 255) / 256);
-  const bool ring = use_ring(dim);
   if (ring) {
     // 64-bit row addresses per lane; the DMA reads stay inside the buffers
     // (rows are clamped, dim is a multiple of the chunk).
     if (topk == 1)
-      hipLaunchKernelGGL((sim_topk_ring_kernel<1>), grid, dim3(256), 0, s, sp, src_row_stride, src_capacity,
+      hipLaunchKernelGGL((sim_topk_ring_kernel<1>), grid, dim3(kRWaves * 64), 0, s, sp, src_row_stride, src_capacity,
                          src_rows, n_src_device, static_cast<int>(n_src), dp, dict_row_stride,
                          static_cast<int>(dict_n0), static_cast<int>(dict_off1), static_cast<int>(n_dict),
                          static_cast<int>(dim), tiles_per_part, partial, parts, sc, scores_row_stride);
     else
-      hipLaunchKernelGGL((sim_topk_ring_kernel<4>), grid, dim3(256), 0, s, sp, src_row_stride, src_capacity,
+      hipLaunchKernelGGL((sim_topk_ring_kernel<4>), grid, dim3(kRWaves * 64), 0, s, sp, src_row_stride, src_capacity,
                          src_rows, n_src_device, static_cast<int>(n_src), dp, dict_row_stride,
                          static_cast<int>(dict_n0), static_cast<int>(dict_off1), static_cast<int>(n_dict),
                          static_cast<int>(dim), tiles_per_part, partial, parts, sc, scores_row_stride);
