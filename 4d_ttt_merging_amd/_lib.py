@@ -31,6 +31,18 @@ _c_f32 = ctypes.c_float
 _c_size = ctypes.c_size_t
 _i64x3 = ctypes.c_int64 * 3
 
+
+class AttnProblem(ctypes.Structure):
+    """`vgo_attn_problem` of include/vgo.h."""
+
+    _fields_ = [
+        ("q", _c_p), ("k", _c_p), ("v", _c_p), ("log_mass", _c_p), ("out", _c_p),
+        ("batch", _c_i64), ("heads", _c_i64), ("n_query", _c_i64), ("n_key", _c_i64),
+        ("head_dim", _c_i64),
+        ("q_stride", _i64x3), ("k_stride", _i64x3), ("v_stride", _i64x3), ("o_stride", _i64x3),
+    ]
+
+
 # name -> (restype, argtypes); every symbol declared in include/vgo.h.
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "vgo_last_error": (ctypes.c_char_p, []),
@@ -45,6 +57,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "vgo_mass_bias_attn_fwd_ws": (_c_int, [
         _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
         _i64x3, _i64x3, _i64x3, _i64x3, _c_int, _c_p, _c_size, _c_p,
+    ]),
+    "vgo_mass_bias_attn_pair_workspace": (_c_int, [
+        ctypes.POINTER(AttnProblem), _c_int, _c_int, ctypes.POINTER(_c_size),
+    ]),
+    "vgo_mass_bias_attn_pair_fwd_ws": (_c_int, [
+        ctypes.POINTER(AttnProblem), _c_int, _c_int, _c_p, _c_size, _c_p,
     ]),
     "vgo_top4_project": (_c_int, [
         _c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_p,

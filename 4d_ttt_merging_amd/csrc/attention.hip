@@ -114,14 +114,7 @@ struct AttnArgs {
   const T* v;
   const T* bias;
   T* out;
-  float* partial;  // stream-K partial states, 2 per work-group (may be null)
   int heads, nq, nk, n_qblocks, ntiles;
-  // Schedule: `groups` work-groups; work-group w first runs the whole tasks
-  // w, w + groups, ... (`full_rounds` of them), then its share of the
-  // (task, key tile) units of the remaining tasks tail_task0.. (`units` in
-  // all, split evenly over the first `tail_groups` work-groups: stream-K on
-  // the last round only).
-  int64_t units, groups, full_rounds, tail_task0, tail_groups;
   int64_t qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn, osb, osh, osn;
   float c;  // log2(e) / 8, folded into Q
   // LDS-DMA kernel only: V^T packed per (batch*head) as [64][npad] in the MFMA
@@ -130,6 +123,24 @@ struct AttnArgs {
   const T* vt;
   const T* bias2;
   int npad;
+};
+
+// Schedule of one attn_pp_kernel launch over one or two problems (the second:
+// the dense special-query pass, run in the merged attention's launch).  With
+// `groups` work-groups, work-group w first runs problem 0's whole tasks w,
+// w + groups, ... (`full_rounds` of them), then its share of the (task, key
+// tile) units of problem 0's remaining tasks tail_task0.. (units [0, units0),
+// `tail_tasks0` tasks) followed by every task of problem 1 (units [units0,
+// units)), split evenly over the first `tail_groups` work-groups: stream-K on
+// the last round only.
+struct PPSchedule {
+  float* partial;  // stream-K partial states, 2 per work-group (may be null)
+  int64_t groups, full_rounds, tail_task0, tail_tasks0, units0, units, tail_groups;
+};
+template <typename T>
+struct PPLaunch {
+  AttnArgs<T> p[2];
+  PPSchedule s;
 };
 
 // First unit of work-group w under the static stream-K partition.
@@ -745,61 +756,84 @@ __device__ __forceinline__ void attn_pp_segment(const AttnArgs<T>& a, T* k_lds, 
 }
 
 // One work-group walks the units [sk_begin(w), sk_begin(w+1)) of the flattened
-// (task, key tile) space; a task is a (batch*head, 512-query block) pair.  A
-// segment that covers a whole task writes the output; a segment that covers a
-// part writes its partial state (slot 0: the work-group's first segment, slot
-// 1: its last), which attn_merge_kernel combines.
+// (task, key tile) space; a task is a (batch*head, 512-query block) pair of
+// one problem.  A segment that covers a whole task writes the output; a
+// segment that covers a part writes its partial state (slot 0: the
+// work-group's first segment, slot 1: its last), which attn_merge_kernel
+// combines.  Only a range's first and last segments can be partial: the
+// units of a task are contiguous and problem 1's start at a task boundary.
 template <typename T>
-__global__ __launch_bounds__(kPPWaves * 64, 1) void attn_pp_kernel(AttnArgs<T> a) {
+__global__ __launch_bounds__(kPPWaves * 64, 1) void attn_pp_kernel(PPLaunch<T> L) {
   __shared__ __attribute__((aligned(16))) T k_lds[kPPStages * kTileElems];
   __shared__ __attribute__((aligned(16))) T vt_lds[kPPStages * kTileElems];
   __shared__ __attribute__((aligned(16))) T b_lds[kPPStages * kBiasSlot];
+  const PPSchedule& sc = L.s;
   const int64_t w = xcd_remap(blockIdx.x, gridDim.x);
-  // Whole tasks: consecutive work-groups (one XCD's, after the remap) take
-  // consecutive tasks of a round, so they stream one head's K/V in step and
-  // share it in that XCD's L2.
-  for (int64_t r = 0; r < a.full_rounds; ++r) {
-    const int64_t task = w + r * a.groups;
-    const int bh = static_cast<int>(task / a.n_qblocks);
-    const int qblk = static_cast<int>(task - static_cast<int64_t>(bh) * a.n_qblocks);
-    attn_pp_segment<T>(a, k_lds, vt_lds, b_lds, bh, qblk, 0, a.ntiles, nullptr);
+  // Whole tasks first: consecutive work-groups (one XCD's, after the remap)
+  // take consecutive tasks of a round, so they stream one head's K/V in step
+  // and share it in that XCD's L2.  Then the stream-K range.  One call site
+  // for both keeps a single copy of the segment code.
+  int64_t r = 0;
+  int64_t u = 0, u_end = 0;
+  if (w < sc.tail_groups) {
+    u = sk_begin(w, sc.units, sc.tail_groups);
+    u_end = sk_begin(w + 1, sc.units, sc.tail_groups);
   }
-  if (w >= a.tail_groups) return;
-  int64_t u = sk_begin(w, a.units, a.tail_groups);
-  const int64_t u_end = sk_begin(w + 1, a.units, a.tail_groups);
   bool first = true;
-  while (u < u_end) {
-    const int64_t tt = u / a.ntiles;  // tail task
-    const int tile0 = static_cast<int>(u - tt * a.ntiles);
-    const int64_t seg_end = min(u_end, (tt + 1) * a.ntiles);
-    const int tile1 = static_cast<int>(seg_end - tt * a.ntiles);
-    const int64_t task = a.tail_task0 + tt;
-    const int bh = static_cast<int>(task / a.n_qblocks);
-    const int qblk = static_cast<int>(task - static_cast<int64_t>(bh) * a.n_qblocks);
+  for (;;) {
+    int second, bh, qblk, tile0, tile1;
     float* partial = nullptr;
-    if (tile0 != 0 || tile1 != a.ntiles)
-      partial = a.partial + (2 * w + (first ? 0 : 1)) * static_cast<int64_t>(kPartialFloats);
-    attn_pp_segment<T>(a, k_lds, vt_lds, b_lds, bh, qblk, tile0, tile1, partial);
-    u = seg_end;
-    first = false;
+    if (r < sc.full_rounds) {
+      const int64_t task = w + r * sc.groups;
+      ++r;
+      second = 0;
+      bh = static_cast<int>(task / L.p[0].n_qblocks);
+      qblk = static_cast<int>(task - static_cast<int64_t>(bh) * L.p[0].n_qblocks);
+      tile0 = 0;
+      tile1 = L.p[0].ntiles;
+    } else if (u < u_end) {
+      second = u >= sc.units0 ? 1 : 0;
+      const int ntiles = L.p[second].ntiles;
+      const int64_t base = second ? sc.units0 : 0;
+      const int64_t tt = (u - base) / ntiles;  // tail task of the problem
+      tile0 = static_cast<int>(u - base - tt * ntiles);
+      const int64_t seg_end = min(u_end, base + (tt + 1) * ntiles);
+      tile1 = static_cast<int>(seg_end - base - tt * ntiles);
+      const int64_t task = (second ? 0 : sc.tail_task0) + tt;
+      const int n_qblocks = L.p[second].n_qblocks;
+      bh = static_cast<int>(task / n_qblocks);
+      qblk = static_cast<int>(task - static_cast<int64_t>(bh) * n_qblocks);
+      if (tile0 != 0 || tile1 != ntiles)
+        partial = sc.partial + (2 * w + (first ? 0 : 1)) * static_cast<int64_t>(kPartialFloats);
+      u = seg_end;
+      first = false;
+    } else {
+      break;
+    }
+    attn_pp_segment<T>(L.p[second], k_lds, vt_lds, b_lds, bh, qblk, tile0, tile1, partial);
   }
 }
 
 // Combines the partial states of every tail task split across work-groups.
-// Block b handles tail task b / kMergeSplit, queries (b % kMergeSplit) *
-// kPPQBlock / kMergeSplit onwards; 16 threads per query, 4 dims each.  Partial
-// states are read eight at a time so their loads overlap.
+// Block b handles tail task b / kMergeSplit (problem 0's tail tasks, then
+// problem 1's tasks), queries (b % kMergeSplit) * kPPQBlock / kMergeSplit
+// onwards; 16 threads per query, 4 dims each.  Partial states are read eight
+// at a time so their loads overlap.
 constexpr int kMergeSplit = 8;
 template <typename T>
-__global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs<T> a) {
-  const int64_t tt = blockIdx.x / kMergeSplit;
+__global__ __launch_bounds__(256) void attn_merge_kernel(PPLaunch<T> L) {
+  const PPSchedule& sc = L.s;
+  const int64_t tt_all = blockIdx.x / kMergeSplit;
   const int qpart = blockIdx.x % kMergeSplit;
-  const int64_t t0 = tt * a.ntiles;
-  const int64_t w0 = sk_owner(t0, a.units, a.tail_groups);
-  const int64_t w1 = sk_owner(t0 + a.ntiles - 1, a.units, a.tail_groups);
+  const int second = tt_all >= sc.tail_tasks0 ? 1 : 0;
+  const AttnArgs<T>& a = L.p[second];
+  const int64_t tt = second ? tt_all - sc.tail_tasks0 : tt_all;
+  const int64_t t0 = (second ? sc.units0 : 0) + tt * a.ntiles;
+  const int64_t w0 = sk_owner(t0, sc.units, sc.tail_groups);
+  const int64_t w1 = sk_owner(t0 + a.ntiles - 1, sc.units, sc.tail_groups);
   if (w1 == w0) return;  // whole inside one work-group: already written
-  const int first_slot = sk_begin(w0, a.units, a.tail_groups) < t0 ? 1 : 0;
-  const int64_t task = a.tail_task0 + tt;
+  const int first_slot = sk_begin(w0, sc.units, sc.tail_groups) < t0 ? 1 : 0;
+  const int64_t task = (second ? 0 : sc.tail_task0) + tt;
   const int bh = static_cast<int>(task / a.n_qblocks);
   const int qblk = static_cast<int>(task - static_cast<int64_t>(bh) * a.n_qblocks);
   const int b = bh / a.heads;
@@ -808,7 +842,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs<T> a) {
   const int d0 = (threadIdx.x & 15) * 4;
   auto slot_ptr = [&](int64_t w) {
     const int slot = w == w0 ? first_slot : 0;
-    return a.partial + (2 * w + slot) * static_cast<int64_t>(kPartialFloats);
+    return sc.partial + (2 * w + slot) * static_cast<int64_t>(kPartialFloats);
   };
   for (int ql = qpart * (kPPQBlock / kMergeSplit) + (threadIdx.x >> 4);
        ql < (qpart + 1) * (kPPQBlock / kMergeSplit); ql += 16) {
@@ -1001,106 +1035,159 @@ int64_t resident_groups() {
 
 constexpr int64_t kMinUnitsPerGroup = 8;  // key tiles per work-group, at least
 
-// Work-group count of the stream-K schedule (0: plain schedule, one task per group).
+// A split tail task is cut into at most about this many pieces, which bounds
+// the partial states attn_merge_kernel reads per query.
+constexpr int64_t kMaxPieces = 32;
+
+// One attention problem of a call, as the C ABI describes it.
+struct Problem {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* bias;
+  void* out;
+  int64_t batch, heads, nq, nk;
+  const int64_t* qs;
+  const int64_t* ks;
+  const int64_t* vs;
+  const int64_t* os;
+};
+
+// The stream-K schedule of an attn_pp_kernel launch over `count` problems;
+// the workspace query and the launch compute the same one on one device.
+struct PPPlan {
+  int count;
+  int64_t tasks[2], ntiles[2];
+  PPSchedule s;
+};
+
 template <typename T>
-int64_t stream_groups(int64_t tasks, int64_t units) {
+PPPlan pp_plan(const Problem* pr, int count) {
+  PPPlan plan{};
+  plan.count = count;
+  int64_t units_all = 0, max_tiles = 1;
+  for (int i = 0; i < count; ++i) {
+    plan.tasks[i] = (pr[i].nq + kPPQBlock - 1) / kPPQBlock * pr[i].batch * pr[i].heads;
+    plan.ntiles[i] = (pr[i].nk + kBN - 1) / kBN;
+    units_all += plan.tasks[i] * plan.ntiles[i];
+    max_tiles = std::max(max_tiles, plan.ntiles[i]);
+  }
   const int64_t slots = resident_groups<T>();
-  if (slots <= 0) return 0;
-  int64_t groups = std::min<int64_t>(slots, (units + kMinUnitsPerGroup - 1) / kMinUnitsPerGroup);
-  if (groups <= 0 || groups == tasks) return 0;
-  return groups;
+  int64_t groups = std::min<int64_t>(slots, (units_all + kMinUnitsPerGroup - 1) / kMinUnitsPerGroup);
+  if (groups <= 0) groups = plan.tasks[0] + (count > 1 ? plan.tasks[1] : 0);  // one task per group
+  PPSchedule& sc = plan.s;
+  sc.partial = nullptr;
+  sc.groups = groups;
+  sc.full_rounds = plan.tasks[0] / groups;
+  sc.tail_task0 = sc.full_rounds * groups;
+  sc.tail_tasks0 = plan.tasks[0] - sc.tail_task0;
+  sc.units0 = sc.tail_tasks0 * plan.ntiles[0];
+  sc.units = sc.units0 + (count > 1 ? plan.tasks[1] * plan.ntiles[1] : 0);
+  const int64_t min_units = std::max<int64_t>(kMinUnitsPerGroup, (max_tiles + kMaxPieces - 1) / kMaxPieces);
+  sc.tail_groups = sc.units > 0 ? std::min<int64_t>(groups, std::max<int64_t>(1, sc.units / min_units)) : 0;
+  return plan;
 }
 
-// Workspace of the DMA path: V^T, bias pairs, then the partial states (each
-// part 256-byte aligned).
+// Workspace of the DMA path: per problem V^T and the bias pairs, then the
+// partial states (each part 256-byte aligned).
 struct AttnWorkspace {
-  size_t vt, bias2, partial, total;
+  size_t vt[2], bias2[2], partial, total;
 };
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
-inline AttnWorkspace attn_workspace(int64_t bh, int64_t ntiles, int64_t groups, size_t elem) {
-  AttnWorkspace w;
-  const int64_t npad = ntiles * kBN;
-  w.vt = 0;
-  w.bias2 = align256(static_cast<size_t>(bh) * kD * npad * elem);
-  w.partial = w.bias2 + align256(static_cast<size_t>(2 * npad) * elem);
-  w.total = w.partial + static_cast<size_t>(groups) * 2 * kPartialFloats * sizeof(float);
+inline AttnWorkspace attn_workspace(const PPPlan& plan, const Problem* pr, size_t elem) {
+  AttnWorkspace w{};
+  size_t at = 0;
+  for (int i = 0; i < plan.count; ++i) {
+    const int64_t npad = plan.ntiles[i] * kBN;
+    w.vt[i] = at;
+    at += align256(static_cast<size_t>(pr[i].batch * pr[i].heads) * kD * npad * elem);
+    w.bias2[i] = at;
+    at += align256(static_cast<size_t>(2 * npad) * elem);
+  }
+  w.partial = at;
+  w.total = at + (plan.s.units > 0 ? static_cast<size_t>(plan.s.groups) * 2 * kPartialFloats * sizeof(float) : 0);
   return w;
 }
 
 template <typename T>
-int launch_mfma(const void* q, const void* k, const void* v, const void* bias, void* out,
-                int64_t batch, int64_t heads, int64_t nq, int64_t nk, const int64_t* qs,
-                const int64_t* ks, const int64_t* vs, const int64_t* os, void* workspace,
-                size_t workspace_bytes, bool split, hipStream_t stream) {
-  const int64_t qblock = split ? kPPQBlock : kQBlock;
-  const int64_t n_qblocks = (nq + qblock - 1) / qblock;
-  const int64_t ntiles = (nk + kBN - 1) / kBN;
-  const int64_t tasks = n_qblocks * batch * heads;
-  VGO_REQUIRE(tasks <= 0x7fffffff && batch * heads <= 0xffff && ntiles < 0x7fffffff / kBN,
-              "mass_bias_attention: grid too large");
+AttnArgs<T> make_args(const Problem& pr, int64_t qblock) {
   AttnArgs<T> a;
-  a.q = static_cast<const T*>(q);
-  a.k = static_cast<const T*>(k);
-  a.v = static_cast<const T*>(v);
-  a.bias = static_cast<const T*>(bias);
-  a.out = static_cast<T*>(out);
-  a.partial = nullptr;
-  a.heads = static_cast<int>(heads);
-  a.nq = static_cast<int>(nq);
-  a.nk = static_cast<int>(nk);
-  a.n_qblocks = static_cast<int>(n_qblocks);
-  a.ntiles = static_cast<int>(ntiles);
-  a.groups = tasks;
-  a.full_rounds = 1;
-  a.tail_task0 = tasks;
-  a.units = 0;
-  a.tail_groups = 0;
-  a.qsb = qs[0], a.qsh = qs[1], a.qsn = qs[2];
-  a.ksb = ks[0], a.ksh = ks[1], a.ksn = ks[2];
-  a.vsb = vs[0], a.vsh = vs[1], a.vsn = vs[2];
-  a.osb = os[0], a.osh = os[1], a.osn = os[2];
+  a.q = static_cast<const T*>(pr.q);
+  a.k = static_cast<const T*>(pr.k);
+  a.v = static_cast<const T*>(pr.v);
+  a.bias = static_cast<const T*>(pr.bias);
+  a.out = static_cast<T*>(pr.out);
+  a.heads = static_cast<int>(pr.heads);
+  a.nq = static_cast<int>(pr.nq);
+  a.nk = static_cast<int>(pr.nk);
+  a.n_qblocks = static_cast<int>((pr.nq + qblock - 1) / qblock);
+  a.ntiles = static_cast<int>((pr.nk + kBN - 1) / kBN);
+  a.qsb = pr.qs[0], a.qsh = pr.qs[1], a.qsn = pr.qs[2];
+  a.ksb = pr.ks[0], a.ksh = pr.ks[1], a.ksn = pr.ks[2];
+  a.vsb = pr.vs[0], a.vsh = pr.vs[1], a.vsn = pr.vs[2];
+  a.osb = pr.os[0], a.osh = pr.os[1], a.osn = pr.os[2];
   a.c = kLog2e / 8.0f;
   a.vt = nullptr;
   a.bias2 = nullptr;
-  a.npad = static_cast<int>(ntiles * kBN);
-  if (!split) {
-    hipLaunchKernelGGL((attn_reg_kernel<T>), dim3(static_cast<unsigned>(a.groups)), dim3(kWaves * 64),
-                       0, stream, a);
-    return check_launch("mass_bias_attention");
+  a.npad = a.ntiles * kBN;
+  return a;
+}
+
+// No workspace: one 256-query task per work-group of attn_reg_kernel.
+template <typename T>
+int launch_reg(const Problem& pr, hipStream_t stream) {
+  const int64_t tasks = (pr.nq + kQBlock - 1) / kQBlock * pr.batch * pr.heads;
+  const int64_t ntiles = (pr.nk + kBN - 1) / kBN;
+  VGO_REQUIRE(tasks <= 0x7fffffff && pr.batch * pr.heads <= 0xffff && ntiles < 0x7fffffff / kBN,
+              "mass_bias_attention: grid too large");
+  const AttnArgs<T> a = make_args<T>(pr, kQBlock);
+  hipLaunchKernelGGL((attn_reg_kernel<T>), dim3(static_cast<unsigned>(tasks)), dim3(kWaves * 64), 0,
+                     stream, a);
+  return check_launch("mass_bias_attention");
+}
+
+// Workspace path over one or two problems: pack V^T and the bias of each,
+// then the ping-pong LDS-DMA kernel, then the merge of split tasks.
+template <typename T>
+int launch_pp(const Problem* pr, int count, void* workspace, size_t workspace_bytes,
+              hipStream_t stream) {
+  for (int i = 0; i < count; ++i) {
+    const int64_t tasks = (pr[i].nq + kPPQBlock - 1) / kPPQBlock * pr[i].batch * pr[i].heads;
+    const int64_t ntiles = (pr[i].nk + kBN - 1) / kBN;
+    VGO_REQUIRE(tasks <= 0x7fffffff && pr[i].batch * pr[i].heads <= 0xffff &&
+                    ntiles < 0x7fffffff / kBN,
+                "mass_bias_attention: grid too large");
   }
-  // Workspace path: pack V^T and the bias, then the ping-pong LDS-DMA kernel.
-  const int64_t groups = stream_groups<T>(tasks, tasks * ntiles);
-  const AttnWorkspace ws = attn_workspace(batch * heads, ntiles, groups, sizeof(T));
+  PPPlan plan = pp_plan<T>(pr, count);
+  VGO_REQUIRE(plan.s.groups <= 0x7fffffff, "mass_bias_attention: grid too large");
+  const AttnWorkspace ws = attn_workspace(plan, pr, sizeof(T));
   if (workspace == nullptr || workspace_bytes < ws.total)
     return fail(VGO_EWORKSPACE, "mass_bias_attention: workspace too small");
   VGO_REQUIRE(aligned(workspace, 256), "mass_bias_attention: workspace must be 256-byte aligned");
   char* base = static_cast<char*>(workspace);
-  T* vt = reinterpret_cast<T*>(base + ws.vt);
-  T* bias2 = reinterpret_cast<T*>(base + ws.bias2);
-  a.vt = vt;
-  a.bias2 = bias2;
-  if (groups > 0) {
-    a.groups = groups;
-    a.full_rounds = tasks / groups;
-    a.tail_task0 = a.full_rounds * groups;
-    a.units = (tasks - a.tail_task0) * ntiles;
-    // At most ~8 pieces per tail task: a work-group takes >= ntiles/8 key tiles.
-    const int64_t min_units = std::max<int64_t>(kMinUnitsPerGroup, (ntiles + 7) / 8);
-    a.tail_groups = std::min<int64_t>(groups, std::max<int64_t>(1, a.units / min_units));
-    a.partial = reinterpret_cast<float*>(base + ws.partial);
+  PPLaunch<T> L{};
+  for (int i = 0; i < count; ++i) {
+    AttnArgs<T>& a = L.p[i];
+    a = make_args<T>(pr[i], kPPQBlock);
+    a.vt = reinterpret_cast<T*>(base + ws.vt[i]);
+    a.bias2 = reinterpret_cast<T*>(base + ws.bias2[i]);
+    hipLaunchKernelGGL((vt_pack_kernel<T>),
+                       dim3(static_cast<unsigned>(a.ntiles), static_cast<unsigned>(pr[i].batch * pr[i].heads)),
+                       dim3(256), 0, stream, a.v, a.heads, a.nk, a.ntiles, a.npad, a.vsb, a.vsh, a.vsn,
+                       a.bias, const_cast<T*>(a.vt), const_cast<T*>(a.bias2));
+    const int status = check_launch("mass_bias_attention(pack)");
+    if (status != VGO_OK) return status;
   }
-  hipLaunchKernelGGL((vt_pack_kernel<T>), dim3(static_cast<unsigned>(ntiles), static_cast<unsigned>(batch * heads)),
-                     dim3(256), 0, stream, a.v, a.heads, a.nk, a.ntiles, a.npad, a.vsb, a.vsh, a.vsn,
-                     a.bias, vt, bias2);
-  int status = check_launch("mass_bias_attention(pack)");
-  if (status != VGO_OK) return status;
-  hipLaunchKernelGGL((attn_pp_kernel<T>), dim3(static_cast<unsigned>(a.groups)), dim3(kPPWaves * 64),
-                     0, stream, a);
-  status = check_launch("mass_bias_attention");
-  if (status != VGO_OK || a.partial == nullptr || a.units == 0) return status;
-  const int64_t tail_tasks = a.units / ntiles;
+  if (count == 1) L.p[1] = L.p[0];  // never selected: problem 1 has no units
+  L.s = plan.s;
+  if (plan.s.units > 0) L.s.partial = reinterpret_cast<float*>(base + ws.partial);
+  hipLaunchKernelGGL((attn_pp_kernel<T>), dim3(static_cast<unsigned>(plan.s.groups)),
+                     dim3(kPPWaves * 64), 0, stream, L);
+  int status = check_launch("mass_bias_attention");
+  if (status != VGO_OK || plan.s.units == 0) return status;
+  const int64_t tail_tasks = plan.s.tail_tasks0 + (count > 1 ? plan.tasks[1] : 0);
   hipLaunchKernelGGL((attn_merge_kernel<T>), dim3(static_cast<unsigned>(tail_tasks * kMergeSplit)),
-                     dim3(256), 0, stream, a);
+                     dim3(256), 0, stream, L);
   return check_launch("mass_bias_attention(merge)");
 }
 
@@ -1125,44 +1212,102 @@ int launch_f32(const void* q, const void* k, const void* v, const void* bias, vo
 
 namespace {
 
-int attn_entry(const void* q, const void* k, const void* v, const void* log_mass, void* out,
-               int64_t batch, int64_t heads, int64_t n_query, int64_t n_key, int64_t head_dim,
-               const int64_t* q_stride, const int64_t* k_stride, const int64_t* v_stride,
-               const int64_t* o_stride, int dtype, void* workspace, size_t workspace_bytes,
-               bool split, void* stream) {
+using vgo::Problem;
+
+// Checks one problem; sets *empty when it has no output rows.
+int check_problem(const Problem& p, int64_t head_dim, int dtype, bool* empty) {
   using namespace vgo;
   VGO_REQUIRE(head_dim == 64, "mass_bias_attention: only head_dim=64 is supported");
-  VGO_REQUIRE(batch >= 0 && heads >= 0 && n_query >= 0 && n_key >= 0,
+  VGO_REQUIRE(p.batch >= 0 && p.heads >= 0 && p.nq >= 0 && p.nk >= 0,
               "mass_bias_attention: negative size");
-  if (batch == 0 || heads == 0 || n_query == 0) return VGO_OK;
-  VGO_REQUIRE(n_key > 0, "mass_bias_attention: no keys");
-  VGO_REQUIRE(q && k && v && out, "mass_bias_attention: null pointer");
-  VGO_REQUIRE(q_stride && k_stride && v_stride && o_stride, "mass_bias_attention: null strides");
-  VGO_REQUIRE(n_query <= 0x7fffffff && n_key <= 0x7fffffff, "mass_bias_attention: too many tokens");
-  hipStream_t s = as_stream(stream);
+  *empty = p.batch == 0 || p.heads == 0 || p.nq == 0;
+  if (*empty) return VGO_OK;
+  VGO_REQUIRE(p.nk > 0, "mass_bias_attention: no keys");
+  VGO_REQUIRE(p.q && p.k && p.v && p.out, "mass_bias_attention: null pointer");
+  VGO_REQUIRE(p.qs && p.ks && p.vs && p.os, "mass_bias_attention: null strides");
+  VGO_REQUIRE(p.nq <= 0x7fffffff && p.nk <= 0x7fffffff, "mass_bias_attention: too many tokens");
   if (dtype == VGO_BF16 || dtype == VGO_F16) {
     for (int i = 0; i < 3; ++i) {
-      VGO_REQUIRE(q_stride[i] % 8 == 0 && k_stride[i] % 8 == 0 && v_stride[i] % 8 == 0 &&
-                      o_stride[i] % 4 == 0,
+      VGO_REQUIRE(p.qs[i] % 8 == 0 && p.ks[i] % 8 == 0 && p.vs[i] % 8 == 0 && p.os[i] % 4 == 0,
                   "mass_bias_attention: token/head/batch strides must be multiples of 8 elements");
     }
-    VGO_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(out, 8),
+    VGO_REQUIRE(aligned(p.q, 16) && aligned(p.k, 16) && aligned(p.v, 16) && aligned(p.out, 8),
                 "mass_bias_attention: q/k/v must be 16-byte aligned");
     // Token offsets inside one (batch, head) plane are 32-bit in the kernel.
     const int64_t lim = int64_t(1) << 31;
-    if (n_key * std::max<int64_t>(k_stride[2], v_stride[2]) >= lim ||
-        n_query * std::max<int64_t>(q_stride[2], o_stride[2]) >= lim)
+    if (p.nk * std::max<int64_t>(p.ks[2], p.vs[2]) >= lim || p.nq * std::max<int64_t>(p.qs[2], p.os[2]) >= lim)
       return fail(VGO_EUNSUPPORTED, "mass_bias_attention: token stride x tokens exceeds 2^31 elements");
-    if (dtype == VGO_BF16)
-      return launch_mfma<bf16_t>(q, k, v, log_mass, out, batch, heads, n_query, n_key, q_stride,
-                                 k_stride, v_stride, o_stride, workspace, workspace_bytes, split, s);
-    return launch_mfma<f16_t>(q, k, v, log_mass, out, batch, heads, n_query, n_key, q_stride,
-                              k_stride, v_stride, o_stride, workspace, workspace_bytes, split, s);
+    return VGO_OK;
   }
-  if (dtype == VGO_F32)
-    return launch_f32(q, k, v, log_mass, out, batch, heads, n_query, n_key, q_stride, k_stride,
-                      v_stride, o_stride, s);
+  if (dtype == VGO_F32) return VGO_OK;
   return fail(VGO_EINVAL, "mass_bias_attention: unsupported dtype");
+}
+
+// Runs the non-empty problems of `problems` (count 1 or 2) in one launch of
+// the workspace kernel (split) or one launch each of the kernel without one.
+int attn_run(const Problem* problems, const int64_t* head_dims, int count, int dtype,
+             void* workspace, size_t workspace_bytes, bool split, void* stream) {
+  using namespace vgo;
+  Problem live[2];
+  int n = 0;
+  for (int i = 0; i < count; ++i) {
+    bool empty = false;
+    const int status = check_problem(problems[i], head_dims[i], dtype, &empty);
+    if (status != VGO_OK) return status;
+    if (!empty) live[n++] = problems[i];
+  }
+  if (n == 0) return VGO_OK;
+  hipStream_t s = as_stream(stream);
+  if (dtype == VGO_F32) {
+    for (int i = 0; i < n; ++i) {
+      const Problem& p = live[i];
+      const int status = launch_f32(p.q, p.k, p.v, p.bias, p.out, p.batch, p.heads, p.nq, p.nk, p.qs,
+                                    p.ks, p.vs, p.os, s);
+      if (status != VGO_OK) return status;
+    }
+    return VGO_OK;
+  }
+  if (split)
+    return dtype == VGO_BF16 ? launch_pp<bf16_t>(live, n, workspace, workspace_bytes, s)
+                             : launch_pp<f16_t>(live, n, workspace, workspace_bytes, s);
+  for (int i = 0; i < n; ++i) {
+    const int status = dtype == VGO_BF16 ? launch_reg<bf16_t>(live[i], s) : launch_reg<f16_t>(live[i], s);
+    if (status != VGO_OK) return status;
+  }
+  return VGO_OK;
+}
+
+// Workspace bytes of the split path (0 for fp32 or when every problem is empty).
+int attn_workspace_bytes(const Problem* problems, int count, int dtype, size_t* bytes) {
+  using namespace vgo;
+  VGO_REQUIRE(bytes, "mass_bias_attention: null size pointer");
+  *bytes = 0;
+  Problem live[2];
+  int n = 0;
+  for (int i = 0; i < count; ++i) {
+    const Problem& p = problems[i];
+    VGO_REQUIRE(p.batch >= 0 && p.heads >= 0 && p.nq >= 0 && p.nk >= 0,
+                "mass_bias_attention: negative size");
+    if (p.batch == 0 || p.heads == 0 || p.nq == 0 || p.nk == 0) continue;
+    live[n++] = p;
+  }
+  if (n == 0 || dtype == VGO_F32) return VGO_OK;
+  VGO_REQUIRE(dtype == VGO_BF16 || dtype == VGO_F16, "mass_bias_attention: unsupported dtype");
+  const PPPlan plan = dtype == VGO_BF16 ? pp_plan<bf16_t>(live, n) : pp_plan<f16_t>(live, n);
+  *bytes = attn_workspace(plan, live, 2).total;
+  return VGO_OK;
+}
+
+Problem single_problem(const void* q, const void* k, const void* v, const void* log_mass, void* out,
+                       int64_t batch, int64_t heads, int64_t n_query, int64_t n_key,
+                       const int64_t* q_stride, const int64_t* k_stride, const int64_t* v_stride,
+                       const int64_t* o_stride) {
+  return Problem{q, k, v, log_mass, out, batch, heads, n_query, n_key, q_stride, k_stride, v_stride, o_stride};
+}
+
+Problem from_c(const vgo_attn_problem& p) {
+  return Problem{p.q, p.k, p.v, p.log_mass, p.out, p.batch, p.heads, p.n_query, p.n_key,
+                 p.q_stride, p.k_stride, p.v_stride, p.o_stride};
 }
 
 }  // namespace
@@ -1173,25 +1318,16 @@ extern "C" int vgo_mass_bias_attn_fwd(const void* q, const void* k, const void* 
                                       int64_t head_dim, const int64_t q_stride[3],
                                       const int64_t k_stride[3], const int64_t v_stride[3],
                                       const int64_t o_stride[3], int dtype, void* stream) {
-  return attn_entry(q, k, v, log_mass, out, batch, heads, n_query, n_key, head_dim, q_stride,
-                    k_stride, v_stride, o_stride, dtype, nullptr, 0, false, stream);
+  const Problem p = single_problem(q, k, v, log_mass, out, batch, heads, n_query, n_key, q_stride,
+                                   k_stride, v_stride, o_stride);
+  return attn_run(&p, &head_dim, 1, dtype, nullptr, 0, false, stream);
 }
 
 extern "C" int vgo_mass_bias_attn_workspace(int64_t batch, int64_t heads, int64_t n_query,
                                             int64_t n_key, int dtype, size_t* bytes) {
-  using namespace vgo;
-  VGO_REQUIRE(bytes, "mass_bias_attention: null size pointer");
-  VGO_REQUIRE(batch >= 0 && heads >= 0 && n_query >= 0 && n_key >= 0,
-              "mass_bias_attention: negative size");
-  *bytes = 0;
-  if (batch == 0 || heads == 0 || n_query == 0 || n_key == 0 || dtype == VGO_F32) return VGO_OK;
-  VGO_REQUIRE(dtype == VGO_BF16 || dtype == VGO_F16, "mass_bias_attention: unsupported dtype");
-  const int64_t tasks = (n_query + kPPQBlock - 1) / kPPQBlock * batch * heads;
-  const int64_t ntiles = (n_key + kBN - 1) / kBN;
-  const int64_t groups = dtype == VGO_BF16 ? stream_groups<bf16_t>(tasks, tasks * ntiles)
-                                           : stream_groups<f16_t>(tasks, tasks * ntiles);
-  *bytes = attn_workspace(batch * heads, ntiles, groups, 2).total;
-  return VGO_OK;
+  const Problem p = single_problem(nullptr, nullptr, nullptr, nullptr, nullptr, batch, heads, n_query,
+                                   n_key, nullptr, nullptr, nullptr, nullptr);
+  return attn_workspace_bytes(&p, 1, dtype, bytes);
 }
 
 extern "C" int vgo_mass_bias_attn_fwd_ws(const void* q, const void* k, const void* v,
@@ -1201,6 +1337,29 @@ extern "C" int vgo_mass_bias_attn_fwd_ws(const void* q, const void* k, const voi
                                          const int64_t k_stride[3], const int64_t v_stride[3],
                                          const int64_t o_stride[3], int dtype, void* workspace,
                                          size_t workspace_bytes, void* stream) {
-  return attn_entry(q, k, v, log_mass, out, batch, heads, n_query, n_key, head_dim, q_stride,
-                    k_stride, v_stride, o_stride, dtype, workspace, workspace_bytes, true, stream);
+  const Problem p = single_problem(q, k, v, log_mass, out, batch, heads, n_query, n_key, q_stride,
+                                   k_stride, v_stride, o_stride);
+  return attn_run(&p, &head_dim, 1, dtype, workspace, workspace_bytes, true, stream);
+}
+
+extern "C" int vgo_mass_bias_attn_pair_workspace(const vgo_attn_problem* problems, int count,
+                                                 int dtype, size_t* bytes) {
+  using namespace vgo;
+  VGO_REQUIRE(problems && (count == 1 || count == 2), "mass_bias_attention: 1 or 2 problems");
+  Problem p[2];
+  for (int i = 0; i < count; ++i) p[i] = from_c(problems[i]);
+  return attn_workspace_bytes(p, count, dtype, bytes);
+}
+
+extern "C" int vgo_mass_bias_attn_pair_fwd_ws(const vgo_attn_problem* problems, int count, int dtype,
+                                              void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace vgo;
+  VGO_REQUIRE(problems && (count == 1 || count == 2), "mass_bias_attention: 1 or 2 problems");
+  Problem p[2];
+  int64_t head_dims[2];
+  for (int i = 0; i < count; ++i) {
+    p[i] = from_c(problems[i]);
+    head_dims[i] = problems[i].head_dim;
+  }
+  return attn_run(p, head_dims, count, dtype, workspace, workspace_bytes, true, stream);
 }

@@ -7,16 +7,20 @@ unchanged.  With a token plan, `SelfAttention` runs the merged path on the HIP
 library:
 
   qkv = Linear(x)                         (torch GEMM, hipBLASLt)
-  q, k = LayerNorm64(q), LayerNorm64(k)   (torch)
-  Q/K/V compaction through the plan       vgo_compact, straight between
-                                          head-major [H, N, 64] views
-  mass-bias attention                     vgo_mass_bias_attn_fwd, written
+  Q/K/V compaction through the plan,      vgo_compact: q/k LayerNorm64 of every
+  written head-major [H, N, 64]           gathered row before pooling
+  preserved / special queries             vgo_qkv_epilogue (LayerNorm64, split)
+  mass-bias attention                     vgo_mass_bias_attn_fwd_ws, written
                                           directly in [B, N, H, 64] order
-  dense special queries                   vgo_mass_bias_attn_fwd without bias
+  dense special queries                   the same launch
+                                          (vgo_mass_bias_attn_pair_fwd_ws), then
+                                          their rows copied over the result
   out = Linear(x)                         (torch GEMM)
   restore                                 vgo_top4_project
 
-Frame blocks (RoPE, no plan) use torch's SDPA exactly as the reference does.
+Frame and register blocks (no plan) in bf16/f16 run the same attention kernel
+behind vgo_qkv_epilogue (LayerNorm64 + RoPE); other dtypes and layouts take
+the reference's torch op sequence.
 The reference's experimental hooks that import the absent module
 `sampled_update_operator` (attention.py:267-299) and the source-query
 correction branch (attention.py:304-312, 376-385) are not part of this path
@@ -32,7 +36,7 @@ import torch.nn.functional as F
 from torch import Tensor, nn
 
 from . import _kernels, profiling
-from .mass_bias_attention import _attention_into
+from .mass_bias_attention import _attention_into, _attention_pair_into
 
 
 class _null:
@@ -266,15 +270,9 @@ class SelfAttention(nn.Module):
                 raise ValueError("log_key_mass length does not match key tokens")
         out = torch.empty((B, n_query, H, 64), device=device, dtype=dtype)
         x = out.permute(0, 2, 1, 3)  # [B, H, Nq, 64] view written in [B, Nq, H, 64] order
-        with profiling.span("global.main_attention"):
-            _attention_into(q_c, k_c, v_c, bias, x)
+        special = output_indices = None
         if getattr(plan, "dense_special_queries", False):
-            original = plan.special_query_original
-            output_indices = original if preserve_queries else plan.special_query_compact
-            if original is None or output_indices is None:
-                raise RuntimeError("dense-special attention plan has no special-token mapping")
-            if B != 1:
-                raise RuntimeError("dense special queries need the batch-1 plans they are built for")
+            original, output_indices = self._special_mapping(plan, preserve_queries, B)
             with profiling.span("global.special_attention"):
                 rows = qkv.reshape(N, 3 * C)
                 _, dense_k, dense_v = _kernels.qkv_epilogue(
@@ -284,9 +282,8 @@ class SelfAttention(nn.Module):
                     rows, H, tokens_in=N, tokens_out=original.numel(), rows=original,
                     q_norm=None if qn is None else qn[:2], eps=qn[2] if qn is not None else 1e-5,
                     want=(True, False, False), out_dtype=dtype)[0]
-                exact = torch.empty_like(special_q)
-                _attention_into(special_q, dense_k, dense_v, None, exact)
-                x.index_copy_(2, output_indices, exact)
+                special = (special_q, dense_k, dense_v, None, torch.empty_like(special_q))
+        self._attend(q_c, k_c, v_c, bias, x, special, output_indices)
         return out.view(B, n_query, C)
 
     def _merged_attention(self, q, k, v, plan, B, N, C, H, D) -> Tensor:
@@ -335,19 +332,41 @@ class SelfAttention(nn.Module):
                 raise ValueError("log_key_mass length does not match key tokens")
         out = torch.empty((B, n_query, H, D), device=q.device, dtype=dtype)
         x = out.permute(0, 2, 1, 3)
-        with profiling.span("global.main_attention"):
-            _attention_into(qa, ka, va, bias, x)
+        special = output_indices = None
         if getattr(plan, "dense_special_queries", False):
-            original = plan.special_query_original
-            output_indices = original if preserve_queries else plan.special_query_compact
-            if original is None or output_indices is None:
-                raise RuntimeError("dense-special attention plan has no special-token mapping")
+            original, output_indices = self._special_mapping(plan, preserve_queries, B)
             with profiling.span("global.special_attention"):
                 special_q = q.index_select(2, original).to(dtype)
                 exact = torch.empty((B, H, original.numel(), D), device=q.device, dtype=dtype)
-                _attention_into(special_q, k.to(dtype), v.to(dtype), None, exact)
-                x.index_copy_(2, output_indices, exact)
+                special = (special_q, k.to(dtype), v.to(dtype), None, exact)
+        self._attend(qa, ka, va, bias, x, special, output_indices)
         return out.view(B, n_query, C)
+
+    @staticmethod
+    def _special_mapping(plan, preserve_queries: bool, B: int) -> tuple[Tensor, Tensor]:
+        """Special-token query rows and the output rows they replace (attention.py:406-414)."""
+        original = plan.special_query_original
+        output_indices = original if preserve_queries else plan.special_query_compact
+        if original is None or output_indices is None:
+            raise RuntimeError("dense-special attention plan has no special-token mapping")
+        if B != 1:
+            raise RuntimeError("dense special queries need the batch-1 plans they are built for")
+        return original, output_indices
+
+    @staticmethod
+    def _attend(q: Tensor, k: Tensor, v: Tensor, bias, x: Tensor, special, output_indices) -> None:
+        """Merged attention into x; with a dense special-query pass, both in one launch.
+
+        The special rows then replace the merged result's rows, as the
+        reference's `x.index_copy_` does (attention.py:420)."""
+        with profiling.span("global.main_attention"):
+            if special is None:
+                _attention_into(q, k, v, bias, x)
+            else:
+                _attention_pair_into((q, k, v, bias, x), special)
+        if special is not None:
+            with profiling.span("global.special_attention"):
+                x.index_copy_(2, output_indices, special[4])
 
 
 class SelfAttentionBlock(nn.Module):

@@ -15,18 +15,12 @@ import torch
 from . import _lib
 
 
-def _attention_into(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                    bias: torch.Tensor | None, out: torch.Tensor, *,
-                    split: bool = True) -> torch.Tensor:
-    """Run the kernel on [B,H,N,64] views (any batch/head/token strides) into `out`.
+def _problem(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, bias: torch.Tensor | None,
+             out: torch.Tensor) -> tuple[_lib.AttnProblem, tuple[torch.Tensor, ...]]:
+    """Checks one attention problem and describes it for the C ABI.
 
-    split=True takes the workspace entry: V^T packed per head, 512-query
-    blocks on the 8-wave kernel, (query block, key tile) work balanced over
-    the resident work-groups (stream-K, partial states merged by a third
-    kernel); split=False takes the entry without a workspace (one
-    work-group per 256-query block).
-    """
-    lib = _lib.load()
+    Returns the `vgo_attn_problem` and the tensors it points into (kept alive
+    by the caller until the launch is queued)."""
     _lib.require_gpu(q, k, v, bias, out)
     if not (q.dtype == k.dtype == v.dtype == out.dtype):
         raise ValueError("q, k, v and the output must share one dtype")
@@ -43,14 +37,32 @@ def _attention_into(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if out.stride(-1) != 1:
         raise ValueError("output channel stride must be 1")
     batch, heads, n_query, head_dim = q.shape
-    n_key = k.shape[-2]
+    problem = _lib.AttnProblem(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.ptr(bias), out.data_ptr(),
+        batch, heads, n_query, k.shape[-2], head_dim,
+        _lib.strides3(q), _lib.strides3(k), _lib.strides3(v), _lib.strides3(out))
+    return problem, (q, k, v, bias, out)
+
+
+def _attention_into(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                    bias: torch.Tensor | None, out: torch.Tensor, *,
+                    split: bool = True) -> torch.Tensor:
+    """Run the kernel on [B,H,N,64] views (any batch/head/token strides) into `out`.
+
+    split=True takes the workspace entry: V^T packed per head, 512-query
+    blocks on the 8-wave kernel, (query block, key tile) work balanced over
+    the resident work-groups (stream-K, partial states merged by a third
+    kernel); split=False takes the entry without a workspace (one
+    work-group per 256-query block).
+    """
+    lib = _lib.load()
+    p, keep = _problem(q, k, v, bias, out)
     dtype = _lib.dtype_code(q.dtype)
-    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.ptr(bias), out.data_ptr(),
-            batch, heads, n_query, n_key, head_dim,
-            _lib.strides3(q), _lib.strides3(k), _lib.strides3(v), _lib.strides3(out), dtype)
+    args = (p.q, p.k, p.v, p.log_mass, p.out, p.batch, p.heads, p.n_query, p.n_key, p.head_dim,
+            p.q_stride, p.k_stride, p.v_stride, p.o_stride, dtype)
     need = ctypes.c_size_t(0)
     if split:
-        _lib.check(lib.vgo_mass_bias_attn_workspace(batch, heads, n_query, n_key, dtype,
+        _lib.check(lib.vgo_mass_bias_attn_workspace(p.batch, p.heads, p.n_query, p.n_key, dtype,
                                                     ctypes.byref(need)))
     if need.value == 0:
         status = lib.vgo_mass_bias_attn_fwd(*args, _lib.stream_of(q))
@@ -59,7 +71,31 @@ def _attention_into(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         status = lib.vgo_mass_bias_attn_fwd_ws(*args, workspace.data_ptr(), need.value,
                                                _lib.stream_of(q))
     _lib.check(status)
+    del keep
     return out
+
+
+def _attention_pair_into(main: tuple, special: tuple) -> None:
+    """Merged attention and the dense special-query pass in one launch.
+
+    `main` and `special` are (q, k, v, bias, out) as for `_attention_into`;
+    each output receives its problem's result (vgo_mass_bias_attn_pair_fwd_ws).
+    """
+    lib = _lib.load()
+    if main[0].dtype != special[0].dtype or main[0].device != special[0].device:
+        raise ValueError("both attention problems must share one dtype and device")
+    p0, keep0 = _problem(*main)
+    p1, keep1 = _problem(*special)
+    problems = (_lib.AttnProblem * 2)(p0, p1)
+    dtype = _lib.dtype_code(main[0].dtype)
+    need = ctypes.c_size_t(0)
+    _lib.check(lib.vgo_mass_bias_attn_pair_workspace(problems, 2, dtype, ctypes.byref(need)))
+    workspace = None
+    if need.value:
+        workspace = torch.empty(need.value // 4, device=main[0].device, dtype=torch.float32)
+    _lib.check(lib.vgo_mass_bias_attn_pair_fwd_ws(
+        problems, 2, dtype, _lib.ptr(workspace), need.value, _lib.stream_of(main[0])))
+    del keep0, keep1
 
 
 def mass_bias_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,

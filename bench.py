@@ -206,6 +206,39 @@ def c3_attention(vgo, device, steps):
             "frac": flops / sec / 1e12 / PEAK_BF16_TFLOPS, "torch_sdpa_ms": sdpa * 1e3}
 
 
+def special_pass(device, steps):
+    """Merged attention plus the dense special-query pass at C4 sizes.
+
+    16,464 merged tokens with log-mass bias, and the 160 special queries
+    (32 frames x 5) over all 32,928 keys without bias: two launches against
+    one pair launch (vgo_mass_bias_attn_pair_fwd_ws)."""
+    mba = importlib.import_module("4d_ttt_merging_amd.mass_bias_attention")
+    nq, ns, nd = FRAMES * (SPECIALS + 1024) // 2, FRAMES * SPECIALS, FRAMES * (SPECIALS + 1024)
+    g = torch.Generator(device=device).manual_seed(8)
+
+    def rand(*shape, std=0.125):
+        return (torch.randn(*shape, device=device, generator=g) * std).bfloat16()
+
+    q, k, v = rand(1, HEADS, nq, 64), rand(1, HEADS, nq, 64), rand(1, HEADS, nq, 64, std=1.0)
+    bias = torch.randint(1, 9, (nq,), device=device, generator=g).float().log().bfloat16()
+    sq, sk, sv = rand(1, HEADS, ns, 64), rand(1, HEADS, nd, 64), rand(1, HEADS, nd, 64, std=1.0)
+    o0, o1 = torch.empty_like(q), torch.empty_like(sq)
+
+    def two():
+        mba._attention_into(q, k, v, bias, o0)
+        mba._attention_into(sq, sk, sv, None, o1)
+
+    def pair():
+        mba._attention_pair_into((q, k, v, bias, o0), (sq, sk, sv, None, o1))
+
+    sec_two = event_time(two, steps, 3)
+    sec_pair = event_time(pair, steps, 3)
+    flops = 4 * HEADS * 64 * (nq * nq + ns * nd)
+    return {"merged_queries": nq, "special_queries": ns, "dense_keys": nd,
+            "two_launches_ms": sec_two * 1e3, "pair_ms": sec_pair * 1e3,
+            "pair_tflops": flops / sec_pair / 1e12}
+
+
 def c2_projection(vgo, device, steps):
     """top-4 projection, N=1,048,576 rows from a 65,536-row table."""
     n, m, d = 1 << 20, 65536, 1024
@@ -460,6 +493,8 @@ def main() -> int:
     torch.cuda.synchronize()
     log("C3 attention microbench")
     result["c3_attention"] = c3_attention(vgo, device, 20)
+    log("special-query pass microbench")
+    result["special_pass"] = special_pass(device, 20)
     log("C2 projection microbench")
     result["c2_projection"] = c2_projection(vgo, device, 10)
     log("simplex solvers microbench")

@@ -85,6 +85,39 @@ int vgo_mass_bias_attn_fwd_ws(const void* q, const void* k, const void* v, const
                               size_t workspace_bytes, void* stream);
 
 /*
+ * One attention problem of vgo_mass_bias_attn_pair_fwd_ws, with the meaning of
+ * vgo_mass_bias_attn_fwd's arguments of the same names (log_mass NULL: no bias).
+ */
+typedef struct vgo_attn_problem {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* log_mass;
+  void* out;
+  int64_t batch, heads, n_query, n_key, head_dim;
+  int64_t q_stride[3], k_stride[3], v_stride[3], o_stride[3];
+} vgo_attn_problem;
+
+/*
+ * Merged global attention and its dense special-query pass in one launch.
+ * problems[0] is the mass-bias attention over merged keys; problems[1]
+ * (count == 2) is the exact pass of the special-token queries over every
+ * original key, without bias.  Together they replace the two calls of
+ * vggt_omega/models/layers/attention.py:386-405 (mass_bias_attention) and
+ * :406-422 (the special queries' dense SDPA), which run one after the other.
+ * The two problems' (512-query block, 64-key tile) units share one stream-K
+ * schedule, so the short special pass fills the merged attention's last round
+ * instead of running alone on a few work-groups.  Each problem writes its own
+ * `out`; the reference then copies the special rows over the merged result
+ * (attention.py:420), which the caller still does.  Same dtypes, checks and
+ * workspace rules as vgo_mass_bias_attn_fwd_ws; count == 1 equals that call.
+ */
+int vgo_mass_bias_attn_pair_workspace(const vgo_attn_problem* problems, int count, int dtype,
+                                      size_t* bytes);
+int vgo_mass_bias_attn_pair_fwd_ws(const vgo_attn_problem* problems, int count, int dtype,
+                                   void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Top-4 convex projection (unmerge): out[i,:] = sum_c w[i,c] * table[index[i,c],:].
  *
  * Replaces the restore of WeightedBilinearTokenPlan / TokenPlan

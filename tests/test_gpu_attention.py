@@ -144,3 +144,85 @@ def test_full_c4_size_rows_match_oracle(vgo, device):
     assert_close(plain[:, :, rows.to(device)], ref, torch.bfloat16, what="C4 plain rows")
     # Same math on every row: the two schedules differ only in summation order.
     assert_close(split, plain.float(), torch.bfloat16, what="C4 stream-K vs plain")
+
+
+def _pair(vgo, main, special):
+    from importlib import import_module
+    mba = import_module(vgo.__name__ + ".mass_bias_attention")
+    outs = (torch.empty_like(main[0]), torch.empty_like(special[0]))
+    mba._attention_pair_into((*main, outs[0]), (*special, None, outs[1]))
+    return outs
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("shapes", [
+    ((1, 16, 1044, 522), (1, 16, 20, 1044)),     # C1: merged pass + 4 frames x 5 specials
+    ((1, 2, 100, 20000), (1, 2, 7, 3000)),       # both problems cut over many work-groups
+    ((2, 3, 700, 1333), (1, 3, 513, 2100)),      # different batch; special tasks > 512 queries
+    ((1, 1, 1, 1), (1, 1, 1, 65)),               # single rows
+])
+def test_pair_launch_matches_oracle(vgo, device, dtype, shapes):
+    """Merged attention and the dense special-query pass in one launch."""
+    (b0, h0, nq0, nk0), (b1, h1, nq1, nk1) = shapes
+    if dtype == torch.float32:
+        # Over 20,000 unit-variance values the outputs average to ~1e-2, and the
+        # RMS floor of the relative error then meets fp32 summation error
+        # (1.3e-5 measured); the fp32 path keeps its 1e-5 bar at 4,096 keys.
+        nk0 = min(nk0, 4096)
+    print(f"[attn pair] dtype={dtype} shapes={shapes} nk0={nk0}", flush=True)
+    std = 1.0 if dtype == torch.float32 else 0.125
+    q, k, v, mass = _inputs(7 + nq0 + nk1, b0, h0, nq0, nk0, dtype, std=std)
+    sq, sk, sv, _ = _inputs(9 + nq1, b1, h1, nq1, nk1, dtype, std=std)
+    bias = mass.log().to(dtype)
+    main = (q.to(device), k.to(device), v.to(device), bias.to(device))
+    special = (sq.to(device), sk.to(device), sv.to(device))
+    out0, out1 = _pair(vgo, main, special)
+    torch.cuda.synchronize()
+    assert_close(out0, oracle.mass_bias_attention(q, k, v, bias.float()), dtype, what=f"pair main {shapes}")
+    ref1 = oracle.mass_bias_attention(sq, sk, sv, torch.zeros(nk1))
+    assert_close(out1, ref1, dtype, what=f"pair special {shapes}")
+
+
+def test_pair_launch_c4_special_pass(vgo, device):
+    """C4 sizes: 16,464 merged tokens with bias + 160 special queries over 32,928 keys."""
+    print("[attn pair c4]", flush=True)
+    q, k, v, mass = _inputs(61, 1, 16, 16464, 16464, torch.bfloat16)
+    sq, sk, sv, _ = _inputs(62, 1, 16, 160, 32928, torch.bfloat16)
+    bias = mass.log().bfloat16()
+    out0, out1 = _pair(vgo, (q.to(device), k.to(device), v.to(device), bias.to(device)),
+                       (sq.to(device), sk.to(device), sv.to(device)))
+    single = _attention_split(vgo, q.to(device), k.to(device), v.to(device), bias.to(device), True)
+    torch.cuda.synchronize()
+    g = torch.Generator().manual_seed(63)
+    rows = torch.cat([torch.randperm(16464, generator=g)[:61], torch.tensor([0, 16463])]).unique()
+    assert_close(out0[:, :, rows.to(device)], oracle.mass_bias_attention(q[:, :, rows], k, v, bias.float()),
+                 torch.bfloat16, what="C4 pair main rows")
+    assert_close(out0, single.float(), torch.bfloat16, what="C4 pair main vs single launch")
+    assert_close(out1, oracle.mass_bias_attention(sq, sk, sv, torch.zeros(32928)), torch.bfloat16,
+                 what="C4 special pass")
+
+
+def test_pair_launch_empty_problems_and_errors(vgo, device):
+    from importlib import import_module
+    mba = import_module(vgo.__name__ + ".mass_bias_attention")
+    q, k, v, mass = _inputs(3, 1, 2, 300, 200, torch.bfloat16)
+    args = (q.to(device), k.to(device), v.to(device), mass.log().bfloat16().to(device))
+    empty_q = torch.empty(1, 2, 0, 64, device=device, dtype=torch.bfloat16)
+    out0, out1 = _pair(vgo, args, (empty_q, args[1], args[2]))
+    assert out1.shape == (1, 2, 0, 64)
+    assert_close(out0, oracle.mass_bias_attention(q, k, v, mass.log().bfloat16().float()), torch.bfloat16,
+                 what="pair with empty special pass")
+    out0, out1 = _pair(vgo, (empty_q, args[1], args[2], args[3]), args[:3])
+    assert_close(out1, oracle.mass_bias_attention(q, k, v, torch.zeros(200)), torch.bfloat16,
+                 what="pair with empty main pass")
+    with pytest.raises(ValueError, match="one dtype"):
+        _pair(vgo, args, (args[0].half(), args[1].half(), args[2].half()))
+    with pytest.raises(ValueError, match="head_dim=64"):
+        _pair(vgo, args, (args[0][..., :32], args[1][..., :32], args[2][..., :32]))
+    with pytest.raises(RuntimeError, match="workspace too small"):
+        problems = (mba._lib.AttnProblem * 2)(mba._problem(*args, torch.empty_like(args[0]))[0],
+                                             mba._problem(*args[:3], None, torch.empty_like(args[0]))[0])
+        lib = mba._lib.load()
+        mba._lib.check(lib.vgo_mass_bias_attn_pair_fwd_ws(problems, 2, 1, None, 0, None))
+    with pytest.raises(ValueError, match="1 or 2 problems"):
+        mba._lib.check(mba._lib.load().vgo_mass_bias_attn_pair_fwd_ws(problems, 3, 1, None, 0, None))
