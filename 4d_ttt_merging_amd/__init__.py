@@ -11,13 +11,15 @@ reference package `vggt_omega` for the merged global-attention path:
 * `streaming_top4`                       vggt_omega/models/sparse_convex_kernels.py
 * `SelfAttention`, `SelfAttentionBlock`  vggt_omega/models/layers/{attention,block}.py
 * `top4_project`                         the restore gather of the plans
+* `plan_io` (`save_plan`, `load_plan`, `load_ttt_trace`, ...)  plan files and
+  replay of the TTT planner's trace records (sparse_convex.py:77-80, 1907-1976)
 
 Every GPU computation of the path runs in the hand-written gfx950 HIP library
 `libvgo.so` (built by `_build.build()`); there is no CPU fallback.
 """
 from __future__ import annotations
 
-from . import _lib
+from . import _lib, plan_io
 from .layers import LinearKMaskedBias, SelfAttention, SelfAttentionBlock
 from .mass_bias_attention import dense_attention, mass_bias_attention
 from .projection import top4_project
@@ -42,6 +44,7 @@ __all__ = [
     "dense_attention",
     "deterministic_weighted_normalizer",
     "mass_bias_attention",
+    "plan_io",
     "streaming_top4",
     "top4_project",
 ]

@@ -14,9 +14,15 @@ register_token) and merge setters (`set_fastvggt`, `set_sparse_convex`,
   patch tokens installed with `set_input_patch_tokens_cache` (the reference's
   own bypass, aggregator.py:233-241, 735-743);
 * the other planners (k-means, hash, TTT, temporal, reference-anchor, affine)
-  are out of scope and rejected by the setters.
+  are out of scope and rejected by the setters; plans they built can still
+  run here through `set_sparse_convex_plans` (e.g. TTT trace records rebuilt
+  by `plan_io.load_ttt_trace`), and `set_sparse_convex(reuse_plan=True)`
+  reuses one plan across a forward's global blocks as the reference's reuse
+  planners do.
 """
 from __future__ import annotations
+
+import dataclasses
 
 import torch
 import torch.nn as nn
@@ -70,6 +76,10 @@ class Aggregator(nn.Module):
         self.sparse_convex_physical_key_layers: frozenset[int] = frozenset()
         self.sparse_convex_dense_global_layers: frozenset[int] = frozenset()
         self.sparse_convex_last_plan_stats: list[dict[str, float | int]] = []
+        self.sparse_convex_reuse_plan = False
+        self.sparse_convex_refit_ordinal = -1
+        self._sparse_convex_reuse_plan = None
+        self._sparse_convex_replay: list | None = None
         self._input_patch_tokens_cache: torch.Tensor | None = None
         self.init_weights()
 
@@ -90,8 +100,17 @@ class Aggregator(nn.Module):
                           qkv_global_layers: tuple[int, ...] | None = _DEFAULT_SPARSE_CONVEX_QKV_LAYERS,
                           physical_key_layers: tuple[int, ...] = (),
                           planner: str = "fixed_topology",
-                          dense_global_layers: tuple[int, ...] = ()) -> None:
-        """Sparse-convex merging (aggregator.py:243-289), fixed-topology planner."""
+                          dense_global_layers: tuple[int, ...] = (), reuse_plan: bool = False,
+                          refit_ordinal: int = -1) -> None:
+        """Sparse-convex merging (aggregator.py:243-289), fixed-topology planner.
+
+        `reuse_plan` builds the plan at the first merged global block of a
+        forward and reuses it in the later ones, with the per-layer
+        preserve_queries / preserve_destination_keys of each (the reuse of
+        aggregator.py:980-1006, which the reference switches on with the
+        kmeans_convex_reuse planner or VGGT_TTT_REUSE_PLAN=1); `refit_ordinal`
+        (VGGT_TTT_REFIT_ORDINAL there) rebuilds the cached plan at that global
+        ordinal."""
         if not -1.0 <= threshold <= 1.000001:
             raise ValueError("sparse-convex threshold must lie in [-1,1]")
         global_count = sum(kind == "global" for kind in self.inter_frame_attention_types)
@@ -114,6 +133,18 @@ class Aggregator(nn.Module):
             None if qkv_global_layers is None else frozenset(int(x) for x in qkv_global_layers))
         self.sparse_convex_physical_key_layers = frozenset(int(x) for x in physical_key_layers)
         self.sparse_convex_dense_global_layers = frozenset(int(x) for x in dense_global_layers)
+        self.sparse_convex_reuse_plan = bool(reuse_plan)
+        self.sparse_convex_refit_ordinal = int(refit_ordinal)
+
+    def set_sparse_convex_plans(self, plans) -> None:
+        """Replay given plans (e.g. `plan_io.load_ttt_trace` or `plan_io.load_plan` output)
+        instead of building them: the k-th plan a forward would build is plans[k].
+
+        The reference's TTT planner writes one trace record per plan it builds
+        (sparse_convex.py:1907-1931), in this order.  Each plan takes the
+        per-layer preserve flags as a reused plan does (aggregator.py:993-1001).
+        None restores planning."""
+        self._sparse_convex_replay = None if plans is None else list(plans)
 
     def set_input_patch_tokens_cache(self, tokens: torch.Tensor | None) -> None:
         """Install or clear the patch tokens consumed by forward() (aggregator.py:233-241)."""
@@ -157,6 +188,8 @@ class Aggregator(nn.Module):
         rope = (sin, cos)
         self.fastvggt_last_plan_stats = []
         self.sparse_convex_last_plan_stats = []
+        self._sparse_convex_reuse_plan = None
+        self._sparse_convex_replayed = 0
         outputs: list[torch.Tensor | None] = []
         for block_idx in range(self.depth):
             tokens = tokens.view(batch_size * num_frames, num_tokens, embed_dim)
@@ -202,16 +235,35 @@ class Aggregator(nn.Module):
                         compact_queries = global_ordinal < self.sparse_convex_qkv_global_blocks
                     preserve_queries = not compact_queries
                     preserve_keys = preserve_queries or global_ordinal in self.sparse_convex_physical_key_layers
-                    plan = build_sparse_convex_plan(
-                        normalized, threshold=self.sparse_convex_threshold,
-                        preserve_queries=preserve_queries, preserve_destination_keys=preserve_keys,
-                        **layout)
+                    reuse_plan = self.sparse_convex_reuse_plan
+                    force_refit = reuse_plan and global_ordinal == self.sparse_convex_refit_ordinal >= 0
+                    if reuse_plan and self._sparse_convex_reuse_plan is not None and not force_refit:
+                        plan = _with_preserve_flags(self._sparse_convex_reuse_plan, preserve_queries,
+                                                    preserve_keys)
+                    else:
+                        if self._sparse_convex_replay is not None:
+                            if self._sparse_convex_replayed >= len(self._sparse_convex_replay):
+                                raise RuntimeError("the replayed sparse-convex plans ran out at "
+                                                   f"global ordinal {global_ordinal}")
+                            plan = _with_preserve_flags(
+                                self._sparse_convex_replay[self._sparse_convex_replayed],
+                                preserve_queries, preserve_keys)
+                            self._sparse_convex_replayed += 1
+                        else:
+                            plan = build_sparse_convex_plan(
+                                normalized, threshold=self.sparse_convex_threshold,
+                                preserve_queries=preserve_queries,
+                                preserve_destination_keys=preserve_keys, **layout)
+                        if reuse_plan:
+                            self._sparse_convex_reuse_plan = plan
                     self.sparse_convex_last_plan_stats.append({
                         "block_index": block_idx, "global_ordinal": global_ordinal,
                         "original_tokens": plan.original_tokens, "kept_tokens": plan.kept_tokens,
                         "merged_tokens": plan.original_tokens - plan.kept_tokens,
                         "merge_ratio": 1.0 - plan.keep_ratio,
                         "compact_queries": bool(compact_queries), "physical_keys": bool(preserve_keys),
+                        "reused_plan": bool(reuse_plan and global_ordinal > 0 and not force_refit),
+                        "refit_plan": bool(force_refit),
                         "attention_query_tokens": int(plan.kept_tokens if compact_queries
                                                       else plan.original_tokens),
                         **plan.metadata})
@@ -233,3 +285,12 @@ def _slice_expand_and_flatten(token_tensor: torch.Tensor, batch_size: int, num_f
     others = token_tensor[:, 1:].expand(batch_size, num_frames - 1, *token_tensor.shape[2:])
     tokens = torch.cat([first, others], dim=1)
     return tokens.view(batch_size * num_frames, *tokens.shape[2:])
+
+
+def _with_preserve_flags(plan, preserve_queries: bool, preserve_keys: bool):
+    """The plan with this layer's preserve flags (aggregator.py:993-1001)."""
+    if (plan.preserve_queries == preserve_queries
+            and plan.preserve_destination_keys == preserve_keys):
+        return plan
+    return dataclasses.replace(plan, preserve_queries=preserve_queries,
+                               preserve_destination_keys=preserve_keys)

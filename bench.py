@@ -239,6 +239,36 @@ def special_pass(device, steps):
             "pair_tflops": flops / sec_pair / 1e12}
 
 
+def plan_replay(vgo, device, steps):
+    """Sparse-convex plan at C4 size: built from tokens, rebuilt from its TTT trace
+    record, and written to / read from a plan file.
+
+    Tokens: 32 frames of 1,029 tokens whose patches are noisy copies of one
+    frame (so most candidates merge).  `replay_ms` includes the record's
+    host-to-device copy and the two small device-to-host reads that size the
+    plan and check its parents."""
+    import tempfile
+    pio = importlib.import_module("4d_ttt_merging_amd.plan_io")
+    tpf = SPECIALS + GRID[0] * GRID[1]
+    layout = dict(frames=FRAMES, tokens_per_frame=tpf, patch_token_start=SPECIALS, patch_hw=GRID)
+    g = torch.Generator(device=device).manual_seed(12)
+    base = torch.randn(1, 1, tpf, DIM, device=device, generator=g)
+    tokens = (base + 0.15 * torch.randn(1, FRAMES, tpf, DIM, device=device, generator=g))
+    tokens = tokens.reshape(1, FRAMES * tpf, DIM).bfloat16()
+    plan = vgo.build_sparse_convex_plan(tokens, threshold=0.9, **layout)
+    build = timed(lambda: vgo.build_sparse_convex_plan(tokens, threshold=0.9, **layout), steps, 1)
+    record = pio.ttt_record_from_plan(plan, frames=FRAMES, tokens_per_frame=tpf, patch_token_start=SPECIALS)
+    replay = timed(lambda: pio.plan_from_ttt_record(record, tokens_per_frame=tpf,
+                                                    patch_token_start=SPECIALS, device=device), steps, 1)
+    with tempfile.TemporaryDirectory() as tmp:
+        path = f"{tmp}/plan.safetensors"
+        save = timed(lambda: pio.save_plan(plan, path), steps, 1)
+        load = timed(lambda: pio.load_plan(path, device=device), steps, 1)
+    return {"tokens": FRAMES * tpf, "sources": plan.source_original.shape[1], "kept": plan.kept_tokens,
+            "build_ms": build * 1e3, "replay_ms": replay * 1e3, "save_ms": save * 1e3,
+            "load_ms": load * 1e3}
+
+
 def c2_projection(vgo, device, steps):
     """top-4 projection, N=1,048,576 rows from a 65,536-row table."""
     n, m, d = 1 << 20, 65536, 1024
@@ -495,6 +525,8 @@ def main() -> int:
     result["c3_attention"] = c3_attention(vgo, device, 20)
     log("special-query pass microbench")
     result["special_pass"] = special_pass(device, 20)
+    log("plan replay microbench")
+    result["plan_replay"] = plan_replay(vgo, device, 10)
     log("C2 projection microbench")
     result["c2_projection"] = c2_projection(vgo, device, 10)
     log("simplex solvers microbench")
