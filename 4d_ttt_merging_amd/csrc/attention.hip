@@ -392,6 +392,11 @@ struct WaveAttn {
     VOps vops;
     load_v(vl, vops);
     __builtin_amdgcn_sched_barrier(0);
+    pv_scores(vops, p, kl, bl, s);
+  }
+  // The same with the V^T operands already requested (vops).
+  __device__ __forceinline__ void pv_scores(const VOps& vops, const op8 (&p)[kQB][4], const T* kl,
+                                            const T* bl, f32x16 (&s)[kQB][2]) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -620,6 +625,18 @@ __device__ __forceinline__ void ring_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// The same barrier without waiting for this wave's LDS reads: V^T operands
+// requested at the end of a softmax phase for the next MFMA phase stay in
+// flight across it.  They read a stage that the DMA overwrites only two
+// barriers later, and the compiler waits for them before their first use.
+template <int N>
+__device__ __forceinline__ void ring_barrier_reads_in_flight() {
+  asm volatile("" ::: "memory");
+  if constexpr (N >= 0) wait_vmem<N>();
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 template <typename T>
 __device__ __forceinline__ void attn_pp_segment(const AttnArgs<T>& a, T* k_lds, T* vt_lds, T* b_lds,
                                                 int bh, int qblk, int tile0, int tile1, float* partial) {
@@ -714,10 +731,13 @@ __device__ __forceinline__ void attn_pp_segment(const AttnArgs<T>& a, T* k_lds, 
       issue(tile + 2);  // A_j
       w.softmax(s, kl(tile), bl(tile), p);
       pin_probs();
-      ring_barrier<kPPDmaPerTile>();  // tile + 1 has landed
+      __builtin_amdgcn_sched_barrier(0);
+      typename WaveAttn<T>::VOps vops;
+      w.load_v(vl(tile), vops);  // B_j's first operands, in flight across the barrier
+      ring_barrier_reads_in_flight<kPPDmaPerTile>();  // tile + 1 has landed
       renew_probs();
       // B_j.  After the last tile the scores of the look-ahead tile go unused.
-      w.pv_scores(vl(tile), p, kl(tile + 1), bl(tile + 1), s);
+      w.pv_scores(vops, p, kl(tile + 1), bl(tile + 1), s);
       pin_scores();
       ring_barrier<2 * kPPDmaPerTile>();
       renew_scores();
@@ -732,19 +752,24 @@ __device__ __forceinline__ void attn_pp_segment(const AttnArgs<T>& a, T* k_lds, 
     renew_scores();
     w.softmax(s, kl(tile0), bl(tile0), p);  // B_0
     pin_probs();
-    ring_barrier<-1>();
+    __builtin_amdgcn_sched_barrier(0);
+    typename WaveAttn<T>::VOps vops;
+    w.load_v(vl(tile0), vops);
+    ring_barrier_reads_in_flight<-1>();
     for (int tile = tile0 + 1; tile < tile1; ++tile) {
       renew_probs();
-      w.pv_scores(vl(tile - 1), p, kl(tile), bl(tile), s);  // A_j
+      w.pv_scores(vops, p, kl(tile), bl(tile), s);  // A_j
       pin_scores();
       ring_barrier<-1>();
       renew_scores();
       w.softmax(s, kl(tile), bl(tile), p);  // B_j
       pin_probs();
-      ring_barrier<-1>();
+      __builtin_amdgcn_sched_barrier(0);
+      w.load_v(vl(tile), vops);
+      ring_barrier_reads_in_flight<-1>();
     }
     renew_probs();
-    w.pv(vl(tile1 - 1), p);  // H_n
+    w.pv(vops, p);  // H_n
     pin_scores();
     ring_barrier<-1>();
   }
