@@ -319,10 +319,13 @@ __global__ __launch_bounds__(256, 2) void sim_topk_kernel(
 // Work-group tile 256 dictionary x 256 source rows, 8 waves of 128 x 64
 // (four 32-row dictionary blocks by two 32-column source blocks, accumulators
 // transposed as in the staged kernel), one work-group per CU.  A tile pair
-// moves 1 MB for 134 MFLOP -- twice the 128 x 128 tile's arithmetic per byte,
-// the fabric (L2 / MALL) being what bounds this kernel.  Operands arrive by
-// LDS DMA (global_load_lds_dwordx4) in 32-wide K chunks through a 4-stage
-// ring, three chunks ahead.  LDS rows are 64 B; their four 16-byte chunks are
+// moves 1 MB for 134 MFLOP, twice the 128 x 128 tile's arithmetic per byte.
+// Operands arrive by LDS DMA (global_load_lds_dwordx4) in 32-wide K chunks
+// through a 5-stage ring (all 160 KB of the CU's LDS), up to four chunks
+// ahead.  A step's first k-step operands are read from LDS during the
+// previous step, its second k-step's during its first k-step's MFMAs, so the
+// LDS reads (96 KB per step and CU, near the LDS bandwidth) overlap the
+// MFMAs instead of preceding them.  LDS rows are 64 B; their four 16-byte chunks are
 // XOR-permuted by sw4(row) = (row >> 2) & 3, so the operand reads (16 rows at
 // one logical chunk per quarter-wave) are conflict-free.  Requires
 // dim % 32 == 0.  Invalid source row ids read row 0 through the DMA and score
@@ -330,7 +333,8 @@ __global__ __launch_bounds__(256, 2) void sim_topk_kernel(
 constexpr int kRTile = 256;
 constexpr int kRWaves = 8;
 constexpr int kRKc = 32;
-constexpr int kRStages = 4;
+constexpr int kRStages = 5;                 // 5 x 32 KB: all of the CU's LDS
+constexpr int kRAhead = kRStages - 1;       // steps in flight ahead of the one computed
 constexpr int kRTileElems = kRTile * kRKc;
 constexpr int kRDmaPerStep = 4;  // per wave: two 16-row blocks of each operand
 __device__ __forceinline__ int sw4(int row) { return (row >> 2) & 3; }
@@ -403,19 +407,24 @@ __global__ __launch_bounds__(kRWaves * 64, 1) void sim_topk_ring_kernel(
     }
     cur_dt = dt;
   };
-  // Issues step `st` (clamped to the last step: the look-ahead past the end
-  // re-reads valid rows into a stage nobody reads again) into stage st & 3.
-  auto issue = [&](int st) {
-    const int sc = min(st, n_steps - 1);
-    const int dt = sc / n_chunks;
-    const int kc = (sc - dt * n_chunks) * kRKc;
-    if (dt != cur_dt) set_dtile(dt);
-    const int stage = st & (kRStages - 1);
+  // Issues the next step in order (iss_dt, iss_kc) into stage `stage`; steps
+  // past the last one are not issued (the waits below then end sooner).
+  int iss_step = 0, iss_dt = 0, iss_kc = 0, iss_stage = 0;
+  auto issue_next = [&]() {
+    if (iss_step >= n_steps) return;
+    if (iss_dt != cur_dt) set_dtile(iss_dt);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int blk = (32 * wave + 16 * j) * kRKc;
-      lds_dma16_addr(dict_p[j] + kc, lds_offset(a_lds + stage * kRTileElems + blk));
-      lds_dma16_addr(src_p[j] + kc, lds_offset(b_lds + stage * kRTileElems + blk));
+      lds_dma16_addr(dict_p[j] + iss_kc, lds_offset(a_lds + iss_stage * kRTileElems + blk));
+      lds_dma16_addr(src_p[j] + iss_kc, lds_offset(b_lds + iss_stage * kRTileElems + blk));
+    }
+    ++iss_step;
+    iss_stage = iss_stage == kRStages - 1 ? 0 : iss_stage + 1;
+    iss_kc += kRKc;
+    if (iss_kc == dim) {
+      iss_kc = 0;
+      ++iss_dt;
     }
   };
   // Operand read offsets (elements) within a 32-row block: logical chunk 2t+hh
@@ -435,38 +444,58 @@ __global__ __launch_bounds__(kRWaves * 64, 1) void sim_topk_ring_kernel(
 #pragma unroll
     for (int y = 0; y < 2; ++y) acc[x][y] = f32x16{};
 
+  // Operands of one 16-wide k-step t of the step in stage `stg`: this wave's
+  // 128 dictionary rows (4 blocks) and 64 source rows (2 blocks).
+  auto read_half = [&](int stg, int t, bf16x8 (&a)[4], bf16x8 (&b)[2]) {
+    const bf16_t* al = a_lds + stg * kRTileElems + wd * 128 * kRKc;
+    const bf16_t* bl = b_lds + stg * kRTileElems + ws * 64 * kRKc;
+#pragma unroll
+    for (int x = 0; x < 4; ++x) a[x] = *reinterpret_cast<const bf16x8*>(al + x * 32 * kRKc + off[t]);
+#pragma unroll
+    for (int y = 0; y < 2; ++y) b[y] = *reinterpret_cast<const bf16x8*>(bl + y * 32 * kRKc + off[t]);
+  };
+  auto mma_half = [&](const bf16x8 (&a)[4], const bf16x8 (&b)[2]) {
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+      for (int y = 0; y < 2; ++y)
+        acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[x], b[y], acc[x][y], 0, 0, 0);
+  };
+  // k-step 0 operands of the current step (read a step ahead) and k-step 1
+  // operands (read at the step's start, under k-step 0's MFMAs).
+  bf16x8 a0[4], b0[2], a1[4], b1[2];
   if (n_steps > 0) {
     // The index loads above complete here, so no compiler-inserted wait for
     // them (which would count the untracked DMAs too) lands in the ring.
     wait_vmem<0>();
-    issue(0);
-    issue(1);
-    issue(2);
-    wait_vmem<2 * kRDmaPerStep>();  // step 0 has landed
+#pragma unroll
+    for (int st = 0; st < kRAhead; ++st) issue_next();
+    wait_vmem<(kRAhead - 1) * kRDmaPerStep>();  // step 0 has landed
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    read_half(0, 0, a0, b0);
   }
-  int dt = 0, kcs = 0;
+  int dt = 0, kcs = 0, stage = 0;
   for (int step = 0; step < n_steps; ++step) {
-    issue(step + 3);
-    const int stage = step & (kRStages - 1);
-    const bf16_t* al = a_lds + stage * kRTileElems + wd * 128 * kRKc;
-    const bf16_t* bl = b_lds + stage * kRTileElems + ws * 64 * kRKc;
-    bf16x8 a[2][4], b[2][2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-#pragma unroll
-      for (int x = 0; x < 4; ++x) a[t][x] = *reinterpret_cast<const bf16x8*>(al + x * 32 * kRKc + off[t]);
-#pragma unroll
-      for (int y = 0; y < 2; ++y) b[t][y] = *reinterpret_cast<const bf16x8*>(bl + y * 32 * kRKc + off[t]);
-    }
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int x = 0; x < 4; ++x)
-#pragma unroll
-        for (int y = 0; y < 2; ++y)
-          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[t][x], b[t][y], acc[x][y], 0, 0, 0);
+    // After this barrier step + 1 has landed for every wave and every wave
+    // has finished step - 1, whose stage the next DMA refills.  A wave's
+    // reads of a stage are consumed by its MFMAs before its next barrier, so
+    // the barrier need not wait for LDS reads in flight.
+    wait_vmem<(kRAhead - 2) * kRDmaPerStep>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    issue_next();
+    const int next = stage == kRStages - 1 ? 0 : stage + 1;
+    read_half(stage, 1, a1, b1);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_half(a0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    // Unconditional: after the last step this reads a stage nobody uses,
+    // and a branch here would make the wait below cover these reads too.
+    read_half(next, 0, a0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_half(a1, b1);
+    stage = next;
     if (kcs == n_chunks - 1) {
       if (!all_src_ok) {
 #pragma unroll
@@ -496,18 +525,27 @@ __global__ __launch_bounds__(kRWaves * 64, 1) void sim_topk_ring_kernel(
         // Running top-1 on the bf16-rounded score: a later (higher) j wins only
         // when strictly greater, which is the lower-index rule for ties; a NaN
         // wins over numbers and the first NaN is kept (ranking of the keys).
+        // A lane's rows jl + pos rise with pos, a compile-time constant per
+        // element, so the tile's winner is tracked by pos and jl added once.
+        // Rows past d_end exist only in a part's last, partial tile.
+        const int lim = d0 + kRTile <= d_end ? kRTile : d_end - jl;
 #pragma unroll
-        for (int sb = 0; sb < 2; ++sb)
+        for (int sb = 0; sb < 2; ++sb) {
+          float tv = top_v[sb];
+          int tp = -1;
 #pragma unroll
           for (int db = 0; db < 4; ++db)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-              const int jj = jl + 32 * db + 8 * (r >> 2) + (r & 3);
+              const int pos = 32 * db + 8 * (r >> 2) + (r & 3);
               const float v = bf16_round(acc[db][sb][r]);
-              const bool take = (jj < d_end) & ((v > top_v[sb]) | ((v != v) & (top_v[sb] == top_v[sb])));
-              top_v[sb] = take ? v : top_v[sb];
-              top_j[sb] = take ? jj : top_j[sb];
+              const bool take = (pos < lim) & ((v > tv) | ((v != v) & (tv == tv)));
+              tv = take ? v : tv;
+              tp = take ? pos : tp;
             }
+          top_j[sb] = tp >= 0 ? jl + tp : top_j[sb];
+          top_v[sb] = tv;
+        }
       } else {
 #pragma unroll
         for (int sb = 0; sb < 2; ++sb)
@@ -528,12 +566,6 @@ __global__ __launch_bounds__(kRWaves * 64, 1) void sim_topk_ring_kernel(
     } else {
       ++kcs;
     }
-    // This wave's reads of the stage are complete and its DMAs of step + 1
-    // have landed; after the barrier every wave's have.
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    wait_vmem<2 * kRDmaPerStep>();
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
   }
   // The look-ahead DMAs land before the ring's LDS is reused for the merge.
   wait_vmem<0>();
