@@ -43,12 +43,14 @@ def similarity_topk(src: torch.Tensor, dictionary: torch.Tensor, topk: int, *,
                     dict_ranges: tuple[int, int, int] | None = None,
                     index_map: torch.Tensor | None = None, want_values: bool = True,
                     index_dtype: torch.dtype = torch.int64,
-                    scores: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+                    scores: torch.Tensor | None = None,
+                    out: tuple[torch.Tensor, torch.Tensor] | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """Top-K bf16 cosine matches of every source row against a dictionary.
 
     dict_ranges = (n0, off1, n_dict): dictionary position j reads row j for
     j < n0 and row off1 + j - n0 otherwise (default: all rows).  Returns
-    (values [n, K] fp32, indices [n, K]) with ties going to the lower position.
+    (values [n, K] fp32, indices [n, K]) with ties going to the lower position,
+    written into `out` = (values, indices) when given (contiguous, those shapes).
     """
     lib = _lib.load()
     _lib.require_gpu(src, dictionary, src_rows, n_src_device, index_map, scores)
@@ -70,8 +72,15 @@ def similarity_topk(src: torch.Tensor, dictionary: torch.Tensor, topk: int, *,
     _lib.check(lib.vgo_similarity_topk_workspace(n_src, n_dict, topk, ctypes.byref(parts),
                                                  ctypes.byref(need)))
     workspace = torch.empty(max(1, need.value // 8), device=src.device, dtype=torch.int64)
-    values = torch.empty((n_src, topk), device=src.device, dtype=torch.float32) if want_values else None
-    index = torch.empty((n_src, topk), device=src.device, dtype=index_dtype)
+    if out is not None:
+        values, index = out
+        _lib.require_gpu(values, index)
+        if (values.shape != (n_src, topk) or index.shape != (n_src, topk) or not values.is_contiguous()
+                or not index.is_contiguous() or values.dtype != torch.float32 or index.dtype != index_dtype):
+            raise ValueError("similarity_topk: `out` must be contiguous [n, K] fp32 values and indices")
+    else:
+        values = torch.empty((n_src, topk), device=src.device, dtype=torch.float32) if want_values else None
+        index = torch.empty((n_src, topk), device=src.device, dtype=index_dtype)
     idx64 = index if index_dtype == torch.int64 else None
     idx32 = index if index_dtype == torch.int32 else None
     if index_map is not None:

@@ -80,6 +80,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "vgo_fastvggt_assemble": (_c_int, [
         _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p,
     ]),
+    "vgo_fastvggt_assemble_workspace": (_c_int, [_c_i64, _c_i64, _c_i64, ctypes.POINTER(_c_size)]),
+    "vgo_fastvggt_assemble_ws": (_c_int, [
+        _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_size,
+        _c_p,
+    ]),
     "vgo_sparse_convex_assemble": (_c_int, [
         _c_p, _c_p, _c_p, _c_p, _c_p, _c_f32, _c_p, _c_i64, _c_i64, _c_f32, _c_p, _c_p, _c_p,
         _c_p, _c_p, _c_p, _c_p,

@@ -409,6 +409,304 @@ __global__ __launch_bounds__(kThreads) void sparse_convex_assemble_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Multi-work-group FastVGGT assembly (the workspace entry).  The same rule as
+// fastvggt_assemble_kernel, spread over the chip as a chain of short kernels:
+//   init     inverse = 0, workspace histograms cleared
+//   hist p   (p = 0..3) histogram of digit p of the keys matching the prefix
+//            chosen from digits 0..p-1 (each work-group re-derives that
+//            prefix from the previous histogram; work-group 0 records it)
+//   mark     threshold; keys above it are removed; ties counted per group
+//   ties     the first need_ties ties in source order are removed
+//   kcount   kept tokens per 2048-token group
+//   compact  compact ids (ascending) and the keep list
+//   inverse  removed sources take their target's compact id
+// Every step is integer work; the result is bit-identical to the one-group
+// kernel.
+constexpr int kAThreads = 256;
+constexpr int kAPer = 8;                     // elements per thread, contiguous
+constexpr int kAChunk = kAThreads * kAPer;  // elements per work-group
+constexpr int kASel = 4 * 256;               // sel[5][4] follows hist[4][256]
+constexpr int kAGroupsAt = kASel + 20;       // per-group counts follow
+
+__host__ __device__ inline int64_t fv_ws_ints(int s_groups, int t_groups) {
+  return kAGroupsAt + s_groups + t_groups;
+}
+
+// Exclusive prefix over the 256 threads; *total receives the sum.
+__device__ int scan256(int v, int* lds4, int* total) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) lds4[wave] = x;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wave; ++w) base += lds4[w];
+  const int t = lds4[0] + lds4[1] + lds4[2] + lds4[3];
+  __syncthreads();
+  *total = t;
+  return base + x - v;
+}
+
+// Wave 0: from a 256-bin digit histogram of the keys matching `prefix`, with
+// `above` keys known to lie above them, the digit of the `removed`-th largest
+// key; writes the extended prefix and count above it to *out_prefix/*out_above.
+__device__ void fv_select(const int* hist, uint32_t prefix, int above, int removed, int shift,
+                          uint32_t* out_prefix, int* out_above) {
+  const int lane = threadIdx.x & 63;
+  const int need = removed - above;
+  int h[4], local = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    h[q] = hist[4 * lane + q];
+    local += h[q];
+  }
+  int suffix = local;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_down(suffix, off);
+    if (lane + off < 64) suffix += y;
+  }
+  int c = suffix - local;
+  int found = -1, more = 0;
+#pragma unroll
+  for (int q = 3; q >= 0; --q) {
+    if (found < 0 && c + h[q] >= need) {
+      found = 4 * lane + q;
+      more = c;
+    }
+    c += h[q];
+  }
+  const uint64_t hit = __ballot(found >= 0);
+  const int top = 63 - __clzll(hit);
+  if (lane == top) {
+    *out_above = above + more;
+    *out_prefix = prefix | (static_cast<uint32_t>(found) << shift);
+  }
+}
+
+__global__ __launch_bounds__(kAThreads) void fva_init_kernel(int total, int64_t* __restrict__ inverse,
+                                                            int* __restrict__ ws, int64_t ws_ints) {
+  const int b = blockIdx.y;
+  int64_t* inv = inverse + static_cast<int64_t>(b) * total;
+  const int t0 = blockIdx.x * kAChunk + threadIdx.x * kAPer;
+#pragma unroll
+  for (int k = 0; k < kAPer; ++k)
+    if (t0 + k < total) inv[t0 + k] = 0;
+  if (blockIdx.x == 0) {
+    int* w = ws + b * ws_ints;
+    for (int i = threadIdx.x; i < kAGroupsAt; i += kAThreads) w[i] = 0;
+  }
+}
+
+__global__ __launch_bounds__(kAThreads) void fva_hist_kernel(const float* __restrict__ best, int ns,
+                                                            int removed, int pass, int* __restrict__ ws,
+                                                            int64_t ws_ints) {
+  __shared__ int lh[256];
+  __shared__ uint32_t s_prefix;
+  __shared__ int s_above;
+  const int b = blockIdx.y;
+  int* w = ws + b * ws_ints;
+  const int tid = threadIdx.x;
+  if (pass == 0) {
+    if (tid == 0) {
+      s_prefix = 0;
+      s_above = 0;
+    }
+  } else if (tid < 64) {
+    fv_select(w + (pass - 1) * 256, static_cast<uint32_t>(w[kASel + 4 * (pass - 1)]),
+              w[kASel + 4 * (pass - 1) + 1], removed, 32 - 8 * pass, &s_prefix, &s_above);
+  }
+  lh[tid] = 0;
+  __syncthreads();
+  if (blockIdx.x == 0 && tid == 0) {
+    w[kASel + 4 * pass] = static_cast<int>(s_prefix);
+    w[kASel + 4 * pass + 1] = s_above;
+  }
+  const uint32_t prefix = s_prefix;
+  const uint32_t pmask = pass == 0 ? 0u : (0xFFFFFFFFu << (32 - 8 * pass));
+  const int shift = 24 - 8 * pass;
+  const float* bb = best + static_cast<int64_t>(b) * ns;
+  const int i0 = blockIdx.x * kAChunk + tid * kAPer;
+#pragma unroll
+  for (int k = 0; k < kAPer; ++k) {
+    const int i = i0 + k;
+    const uint32_t key = i < ns ? ord32(bb[i]) : 0u;
+    hist_add(lh, i < ns && (key & pmask) == prefix, (key >> shift) & 0xFF);
+  }
+  __syncthreads();
+  if (lh[tid]) atomicAdd(&w[pass * 256 + tid], lh[tid]);
+}
+
+__global__ __launch_bounds__(kAThreads) void fva_mark_kernel(const float* __restrict__ best,
+                                                            const int64_t* __restrict__ source_ids,
+                                                            int ns, int total, int removed,
+                                                            int64_t* __restrict__ inverse,
+                                                            uint8_t* __restrict__ removed_flag,
+                                                            int* __restrict__ ws, int64_t ws_ints) {
+  __shared__ uint32_t s_prefix;
+  __shared__ int s_above;
+  __shared__ int lds4[4];
+  const int b = blockIdx.y;
+  int* w = ws + b * ws_ints;
+  const int tid = threadIdx.x;
+  if (tid < 64)
+    fv_select(w + 3 * 256, static_cast<uint32_t>(w[kASel + 12]), w[kASel + 13], removed, 0, &s_prefix,
+              &s_above);
+  __syncthreads();
+  const uint32_t thresh = s_prefix;
+  if (blockIdx.x == 0 && tid == 0) {
+    w[kASel + 16] = static_cast<int>(thresh);
+    w[kASel + 17] = removed - s_above;  // ties to remove, lowest position first
+  }
+  const float* bb = best + static_cast<int64_t>(b) * ns;
+  int64_t* inv = inverse + static_cast<int64_t>(b) * total;
+  uint8_t* flag = removed_flag + static_cast<int64_t>(b) * ns;
+  const int i0 = blockIdx.x * kAChunk + tid * kAPer;
+  int ties = 0;
+#pragma unroll
+  for (int k = 0; k < kAPer; ++k) {
+    const int i = i0 + k;
+    if (i < ns) {
+      const uint32_t key = ord32(bb[i]);
+      const bool rm = key > thresh;
+      flag[i] = rm ? 1 : 0;
+      ties += key == thresh;
+      if (rm) {
+        const int64_t sid = source_ids[i];
+        if (sid >= 0 && sid < total) inv[sid] = -1;
+      }
+    }
+  }
+  int n = 0;
+  scan256(ties, lds4, &n);
+  if (tid == 0) w[kAGroupsAt + blockIdx.x] = n;
+}
+
+__global__ __launch_bounds__(kAThreads) void fva_ties_kernel(const float* __restrict__ best,
+                                                            const int64_t* __restrict__ source_ids,
+                                                            int ns, int total,
+                                                            int64_t* __restrict__ inverse,
+                                                            uint8_t* __restrict__ removed_flag,
+                                                            const int* __restrict__ ws, int64_t ws_ints) {
+  __shared__ int lds4[4];
+  const int b = blockIdx.y;
+  const int* w = ws + b * ws_ints;
+  const int tid = threadIdx.x;
+  const uint32_t thresh = static_cast<uint32_t>(w[kASel + 16]);
+  const int need = w[kASel + 17];
+  int before = 0;  // ties in earlier groups
+  for (int g = tid; g < static_cast<int>(blockIdx.x); g += kAThreads) before += w[kAGroupsAt + g];
+  int sum = 0;
+  scan256(before, lds4, &sum);
+  before = sum;
+  if (before >= need) return;  // uniform
+  const float* bb = best + static_cast<int64_t>(b) * ns;
+  int64_t* inv = inverse + static_cast<int64_t>(b) * total;
+  uint8_t* flag = removed_flag + static_cast<int64_t>(b) * ns;
+  const int i0 = blockIdx.x * kAChunk + tid * kAPer;
+  uint32_t tie_bits = 0;
+#pragma unroll
+  for (int k = 0; k < kAPer; ++k) {
+    const int i = i0 + k;
+    tie_bits |= (i < ns && ord32(bb[i]) == thresh ? 1u : 0u) << k;
+  }
+  int n = 0;
+  int rank = before + scan256(__popc(tie_bits), lds4, &n);
+#pragma unroll
+  for (int k = 0; k < kAPer; ++k) {
+    if ((tie_bits >> k) & 1u) {
+      if (rank < need) {
+        const int i = i0 + k;
+        flag[i] = 1;
+        const int64_t sid = source_ids[i];
+        if (sid >= 0 && sid < total) inv[sid] = -1;
+      }
+      ++rank;
+    }
+  }
+}
+
+__global__ __launch_bounds__(kAThreads) void fva_kcount_kernel(int total, const int64_t* __restrict__ inverse,
+                                                              int* __restrict__ ws, int64_t ws_ints,
+                                                              int s_groups) {
+  __shared__ int lds4[4];
+  const int b = blockIdx.y;
+  const int64_t* inv = inverse + static_cast<int64_t>(b) * total;
+  const int t0 = blockIdx.x * kAChunk + threadIdx.x * kAPer;
+  int kept = 0;
+#pragma unroll
+  for (int k = 0; k < kAPer; ++k) kept += (t0 + k < total && inv[t0 + k] == 0) ? 1 : 0;
+  int n = 0;
+  scan256(kept, lds4, &n);
+  if (threadIdx.x == 0) ws[b * ws_ints + kAGroupsAt + s_groups + blockIdx.x] = n;
+}
+
+__global__ __launch_bounds__(kAThreads) void fva_compact_kernel(int total, int removed,
+                                                               int64_t* __restrict__ inverse,
+                                                               int64_t* __restrict__ keep,
+                                                               const int* __restrict__ ws, int64_t ws_ints,
+                                                               int s_groups) {
+  __shared__ int lds4[4];
+  const int b = blockIdx.y;
+  const int* w = ws + b * ws_ints + kAGroupsAt + s_groups;
+  const int tid = threadIdx.x;
+  int before = 0;
+  for (int g = tid; g < static_cast<int>(blockIdx.x); g += kAThreads) before += w[g];
+  int sum = 0;
+  scan256(before, lds4, &sum);
+  int64_t* inv = inverse + static_cast<int64_t>(b) * total;
+  int64_t* kp = keep + static_cast<int64_t>(b) * (total - removed);
+  const int t0 = blockIdx.x * kAChunk + tid * kAPer;
+  uint32_t kept_bits = 0;
+#pragma unroll
+  for (int k = 0; k < kAPer; ++k) kept_bits |= (t0 + k < total && inv[t0 + k] == 0 ? 1u : 0u) << k;
+  int n = 0;
+  int rank = sum + scan256(__popc(kept_bits), lds4, &n);
+  const int n_keep = total - removed;
+#pragma unroll
+  for (int k = 0; k < kAPer; ++k) {
+    if ((kept_bits >> k) & 1u) {
+      inv[t0 + k] = rank;
+      if (rank < n_keep) kp[rank] = t0 + k;  // always true for a valid (disjoint) source list
+      ++rank;
+    }
+  }
+}
+
+__global__ __launch_bounds__(kAThreads) void fva_inverse_kernel(const int32_t* __restrict__ target,
+                                                               const int64_t* __restrict__ source_ids,
+                                                               const int64_t* __restrict__ dest_ids,
+                                                               int ns, int nd, int total,
+                                                               int64_t* __restrict__ inverse,
+                                                               const uint8_t* __restrict__ removed_flag) {
+  const int b = blockIdx.y;
+  const int32_t* tb = target + static_cast<int64_t>(b) * ns;
+  int64_t* inv = inverse + static_cast<int64_t>(b) * total;
+  const uint8_t* flag = removed_flag + static_cast<int64_t>(b) * ns;
+  const int i0 = blockIdx.x * kAChunk + threadIdx.x * kAPer;
+  int64_t sid[kAPer], dst[kAPer];
+#pragma unroll
+  for (int k = 0; k < kAPer; ++k) {
+    const int i = i0 + k;
+    sid[k] = -1;
+    dst[k] = -1;
+    if (i < ns && flag[i]) {
+      sid[k] = source_ids[i];
+      const int32_t d = tb[i];
+      dst[k] = (d >= 0 && d < nd) ? dest_ids[d] : -1;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kAPer; ++k)
+    if (sid[k] >= 0 && sid[k] < total) inv[sid[k]] = (dst[k] >= 0 && dst[k] < total) ? inv[dst[k]] : -1;
+}
+
 }  // namespace
 }  // namespace vgo
 
@@ -451,4 +749,60 @@ extern "C" int vgo_sparse_convex_assemble(const float* fit, const float* alpha, 
                      static_cast<int>(n_candidates), static_cast<int>(total_tokens), threshold, keep,
                      original_to_compact, source, parent, weight, stats);
   return check_launch("sparse_convex_assemble");
+}
+
+extern "C" int vgo_fastvggt_assemble_workspace(int64_t batch, int64_t n_sources, int64_t total_tokens,
+                                               size_t* bytes) {
+  using namespace vgo;
+  VGO_REQUIRE(bytes, "fastvggt_assemble: null size pointer");
+  VGO_REQUIRE(batch >= 0 && n_sources >= 0 && total_tokens >= 0 && total_tokens < (1LL << 30),
+              "fastvggt_assemble: bad size");
+  const int s_groups = static_cast<int>((n_sources + kAChunk - 1) / kAChunk);
+  const int t_groups = static_cast<int>((total_tokens + kAChunk - 1) / kAChunk);
+  *bytes = static_cast<size_t>(batch) * fv_ws_ints(s_groups, t_groups) * sizeof(int);
+  return VGO_OK;
+}
+
+extern "C" int vgo_fastvggt_assemble_ws(const float* best, const int32_t* target,
+                                        const int64_t* source_ids, const int64_t* dest_ids,
+                                        int64_t batch, int64_t n_sources, int64_t n_dest,
+                                        int64_t total_tokens, int64_t removed, int64_t* keep,
+                                        int64_t* inverse, uint8_t* removed_flag, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+  using namespace vgo;
+  VGO_REQUIRE(batch >= 0 && n_sources >= 0 && n_dest >= 0 && total_tokens >= 0,
+              "fastvggt_assemble: negative size");
+  VGO_REQUIRE(removed >= 1 && removed <= n_sources, "fastvggt_assemble: removed must lie in [1, sources]");
+  VGO_REQUIRE(n_sources + n_dest <= total_tokens && total_tokens < (1LL << 30),
+              "fastvggt_assemble: inconsistent token counts");
+  VGO_REQUIRE(batch <= 0xffff, "fastvggt_assemble: batch too large");
+  if (batch == 0) return VGO_OK;
+  VGO_REQUIRE(best && target && source_ids && dest_ids && keep && inverse && removed_flag,
+              "fastvggt_assemble: null pointer");
+  const int ns = static_cast<int>(n_sources), total = static_cast<int>(total_tokens);
+  const int s_groups = (ns + kAChunk - 1) / kAChunk;
+  const int t_groups = (total + kAChunk - 1) / kAChunk;
+  const int64_t ws_ints = fv_ws_ints(s_groups, t_groups);
+  if (workspace == nullptr ||
+      workspace_bytes < static_cast<size_t>(batch) * ws_ints * sizeof(int))
+    return fail(VGO_EWORKSPACE, "fastvggt_assemble: workspace too small");
+  VGO_REQUIRE(aligned(workspace, 4), "fastvggt_assemble: workspace must be 4-byte aligned");
+  int* ws = static_cast<int*>(workspace);
+  hipStream_t s = as_stream(stream);
+  const unsigned nb = static_cast<unsigned>(batch);
+  hipLaunchKernelGGL(fva_init_kernel, dim3(t_groups, nb), dim3(kAThreads), 0, s, total, inverse, ws, ws_ints);
+  for (int pass = 0; pass < 4; ++pass)
+    hipLaunchKernelGGL(fva_hist_kernel, dim3(s_groups, nb), dim3(kAThreads), 0, s, best, ns,
+                       static_cast<int>(removed), pass, ws, ws_ints);
+  hipLaunchKernelGGL(fva_mark_kernel, dim3(s_groups, nb), dim3(kAThreads), 0, s, best, source_ids, ns, total,
+                     static_cast<int>(removed), inverse, removed_flag, ws, ws_ints);
+  hipLaunchKernelGGL(fva_ties_kernel, dim3(s_groups, nb), dim3(kAThreads), 0, s, best, source_ids, ns, total,
+                     inverse, removed_flag, ws, ws_ints);
+  hipLaunchKernelGGL(fva_kcount_kernel, dim3(t_groups, nb), dim3(kAThreads), 0, s, total, inverse, ws,
+                     ws_ints, s_groups);
+  hipLaunchKernelGGL(fva_compact_kernel, dim3(t_groups, nb), dim3(kAThreads), 0, s, total,
+                     static_cast<int>(removed), inverse, keep, ws, ws_ints, s_groups);
+  hipLaunchKernelGGL(fva_inverse_kernel, dim3(s_groups, nb), dim3(kAThreads), 0, s, target, source_ids,
+                     dest_ids, ns, static_cast<int>(n_dest), total, inverse, removed_flag);
+  return check_launch("fastvggt_assemble");
 }

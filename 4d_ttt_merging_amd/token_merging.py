@@ -14,11 +14,13 @@ Every reduction, gather and selection runs in the HIP library: compaction is
 `vgo_compact` over a stable CSR of plan members (`vgo_csr_build`), restore is
 `vgo_top4_project` over a dense [N,4] map, masses are `vgo_segment_mass`, and
 the FastVGGT match/rank is `vgo_normalize_rows` -> `vgo_similarity_topk` ->
-`vgo_fastvggt_assemble`.  Only the layout-dependent index lists (which tokens
+`vgo_fastvggt_assemble_ws`.  Only the layout-dependent index lists (which tokens
 are destinations, protected or sources) are computed on the host, once per
 layout, with torch's CPU generator exactly as the reference draws them.
 """
 from __future__ import annotations
+
+import ctypes
 
 import functools
 import math
@@ -477,17 +479,20 @@ def build_fastvggt_plan(
         x = _as_rows(tokens[b])
         src = _kernels.normalize_rows(x, sources, 1e-12)
         dst = _kernels.normalize_rows(x, destinations, 1e-12)
-        values, index = _kernels.similarity_topk(src, dst, 1, index_dtype=torch.int32)
-        best[b] = values[:, 0]
-        target[b] = index[:, 0]
+        _kernels.similarity_topk(src, dst, 1, index_dtype=torch.int32,
+                                 out=(best[b].view(-1, 1), target[b].view(-1, 1)))
     keep = torch.empty((batch, total - removed), device=device, dtype=torch.int64)
     inverse = torch.empty((batch, total), device=device, dtype=torch.int64)
     flags = torch.empty((batch, sources.numel()), device=device, dtype=torch.uint8)
     lib = _kernels._lib.load()
-    status = lib.vgo_fastvggt_assemble(
+    need = ctypes.c_size_t(0)
+    _kernels._lib.check(lib.vgo_fastvggt_assemble_workspace(batch, sources.numel(), total,
+                                                            ctypes.byref(need)))
+    workspace = torch.empty(max(need.value // 4, 1), device=device, dtype=torch.int32)
+    status = lib.vgo_fastvggt_assemble_ws(
         best.data_ptr(), target.data_ptr(), sources.data_ptr(), destinations.data_ptr(), batch,
         sources.numel(), destinations.numel(), total, removed, keep.data_ptr(), inverse.data_ptr(),
-        flags.data_ptr(), _kernels._lib.stream_of(tokens))
+        flags.data_ptr(), workspace.data_ptr(), need.value, _kernels._lib.stream_of(tokens))
     _kernels._lib.check(status)
     plan = TokenPlan(keep, inverse, total)
     # Match results stay on the device for diagnostics and tests.

@@ -189,6 +189,22 @@ int vgo_fastvggt_assemble(const float* best, const int32_t* target, const int64_
                           int64_t* inverse, uint8_t* removed_flag, void* stream);
 
 /*
+ * Workspace variant of vgo_fastvggt_assemble, same arguments and result (bit
+ * for bit).  The selection, marking, compaction and inverse steps run as a
+ * chain of short kernels over many work-groups instead of one; `workspace`
+ * (size from vgo_fastvggt_assemble_workspace, 4-byte aligned, any contents)
+ * holds the digit histograms and per-group counts.  Replaces the same
+ * reference lines (vggt_omega/models/token_merging.py:1112-1121).
+ */
+int vgo_fastvggt_assemble_workspace(int64_t batch, int64_t n_sources, int64_t total_tokens,
+                                    size_t* bytes);
+int vgo_fastvggt_assemble_ws(const float* best, const int32_t* target, const int64_t* source_ids,
+                             const int64_t* dest_ids, int64_t batch, int64_t n_sources,
+                             int64_t n_dest, int64_t total_tokens, int64_t removed, int64_t* keep,
+                             int64_t* inverse, uint8_t* removed_flag, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
+/*
  * Sparse-convex plan assembly (vggt_omega/models/sparse_convex.py:2435-2455):
  * sources = candidates with fit >= threshold (ascending), keep = the rest,
  * original_to_compact, parent = original_to_compact[support], weight = alpha.

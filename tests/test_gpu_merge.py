@@ -153,18 +153,29 @@ def test_streaming_top4_api(vgo, device):
 
 
 # ------------------------------------------------------ rank and select ----
-@pytest.mark.parametrize("batch,ns,nd,removed", [(1, 50, 20, 1), (2, 3000, 900, 1700),
-                                                 (1, 5000, 100, 5000), (1, 20000, 7000, 12345),
-                                                 (1, 70000, 3000, 40000)])
-def test_fastvggt_assemble_exact(vgo, kern, device, batch, ns, nd, removed):
-    print(f"[assemble] batch={batch} ns={ns} removed={removed}", flush=True)
+@pytest.mark.parametrize("batch,ns,nd,removed,keys", [
+    (1, 50, 20, 1, "bf16"), (2, 3000, 900, 1700, "bf16"), (1, 5000, 100, 5000, "bf16"),
+    (1, 20000, 7000, 12345, "bf16"), (1, 70000, 3000, 40000, "bf16"),
+    (2, 23808, 8960, 16464, "fp32"),   # C4 sizes; full 32-bit keys with repeated values
+    (1, 4097, 10, 2049, "fp32"),       # group boundaries of the multi-group path
+])
+@pytest.mark.parametrize("entry", ["one_group", "workspace"])
+def test_fastvggt_assemble_exact(vgo, kern, device, batch, ns, nd, removed, keys, entry):
+    print(f"[assemble] {entry} batch={batch} ns={ns} removed={removed} keys={keys}", flush=True)
     g = torch.Generator().manual_seed(ns + removed)
     total = ns + nd + 37
     perm = torch.randperm(total, generator=g)
     sources = perm[:ns].sort().values
     dests = perm[ns:ns + nd].sort().values
-    # bf16-valued scores with heavy ties
-    best = (torch.randint(0, 40, (batch, ns), generator=g).float() / 64).to(torch.bfloat16).float()
+    if keys == "bf16":
+        # bf16-valued scores with heavy ties
+        best = (torch.randint(0, 40, (batch, ns), generator=g).float() / 64).to(torch.bfloat16).float()
+    else:
+        # fp32 scores: every bit of the key matters; a few values repeat, one is negative zero
+        best = torch.rand(batch, ns, generator=g) * 2 - 1
+        best[:, ::97] = best[:, 5:6]
+        best[:, 3] = -0.0
+        best[:, 4] = 0.0
     target = torch.randint(0, nd, (batch, ns), generator=g, dtype=torch.int32)
     keep = torch.empty((batch, total - removed), dtype=torch.int64, device=device)
     inverse = torch.empty((batch, total), dtype=torch.int64, device=device)
@@ -172,16 +183,26 @@ def test_fastvggt_assemble_exact(vgo, kern, device, batch, ns, nd, removed):
     best_d, target_d = best.to(device), target.to(device)
     sources_d, dests_d = sources.to(device), dests.to(device)
     lib = import_package("_lib")
-    status = lib.load().vgo_fastvggt_assemble(
-        best_d.data_ptr(), target_d.data_ptr(), sources_d.data_ptr(), dests_d.data_ptr(), batch,
-        ns, nd, total, removed, keep.data_ptr(), inverse.data_ptr(), flags.data_ptr(),
-        torch.cuda.current_stream().cuda_stream)
+    args = (best_d.data_ptr(), target_d.data_ptr(), sources_d.data_ptr(), dests_d.data_ptr(), batch,
+            ns, nd, total, removed, keep.data_ptr(), inverse.data_ptr(), flags.data_ptr())
+    stream = torch.cuda.current_stream().cuda_stream
+    if entry == "one_group":
+        status = lib.load().vgo_fastvggt_assemble(*args, stream)
+    else:
+        import ctypes
+        need = ctypes.c_size_t(0)
+        lib.check(lib.load().vgo_fastvggt_assemble_workspace(batch, ns, total, ctypes.byref(need)))
+        ws = torch.full((need.value // 4,), 7, dtype=torch.int32, device=device)  # not zeroed on purpose
+        status = lib.load().vgo_fastvggt_assemble_ws(*args, ws.data_ptr(), need.value, stream)
     lib.check(status)
     torch.cuda.synchronize()
     for b in range(batch):
         rk, ri = om.fastvggt_select(best[b], target[b].long(), sources, dests, total, removed)
         assert torch.equal(keep[b].cpu(), rk)
         assert torch.equal(inverse[b].cpu(), ri)
+        removed_ids = torch.ones(total, dtype=torch.bool)
+        removed_ids[rk] = False
+        assert torch.equal(flags[b].cpu().bool(), removed_ids[sources])
 
 
 # --------------------------------------------------------- FastVGGT plan ----
