@@ -407,11 +407,13 @@ __global__ __launch_bounds__(kRWaves * 64, 1) void sim_topk_ring_kernel(
     }
     cur_dt = dt;
   };
-  // Issues the next step in order (iss_dt, iss_kc) into stage `stage`; steps
-  // past the last one are not issued (the waits below then end sooner).
+  // Issues the next step in order (iss_dt, iss_kc) into the next stage.  Past
+  // the last step it re-issues the last one (valid rows, into a stage nobody
+  // reads again): every call issues the same number of DMAs, which the
+  // vmcnt waits below count on -- with fewer in flight, "at most N
+  // outstanding" would no longer mean that the oldest step has landed.
   int iss_step = 0, iss_dt = 0, iss_kc = 0, iss_stage = 0;
   auto issue_next = [&]() {
-    if (iss_step >= n_steps) return;
     if (iss_dt != cur_dt) set_dtile(iss_dt);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -419,12 +421,13 @@ __global__ __launch_bounds__(kRWaves * 64, 1) void sim_topk_ring_kernel(
       lds_dma16_addr(dict_p[j] + iss_kc, lds_offset(a_lds + iss_stage * kRTileElems + blk));
       lds_dma16_addr(src_p[j] + iss_kc, lds_offset(b_lds + iss_stage * kRTileElems + blk));
     }
-    ++iss_step;
     iss_stage = iss_stage == kRStages - 1 ? 0 : iss_stage + 1;
-    iss_kc += kRKc;
-    if (iss_kc == dim) {
-      iss_kc = 0;
-      ++iss_dt;
+    if (++iss_step < n_steps) {
+      iss_kc += kRKc;
+      if (iss_kc == dim) {
+        iss_kc = 0;
+        ++iss_dt;
+      }
     }
   };
   // Operand read offsets (elements) within a 32-row block: logical chunk 2t+hh

@@ -71,7 +71,10 @@ def test_normalize_rows(kern, device, dim, eps):
 
 # ------------------------------------------------------------- matching ----
 @pytest.mark.parametrize("topk", [1, 4])
-@pytest.mark.parametrize("ns,nd,dim", [(37, 11, 64), (300, 777, 1024), (1000, 130, 128), (260, 300, 72)])
+@pytest.mark.parametrize("ns,nd,dim", [(37, 11, 64), (300, 777, 1024), (1000, 130, 128), (260, 300, 72),
+                                        # one or two 32-wide K chunks in all: fewer steps than the
+                                        # ring's look-ahead (regression: the DMA count must stay uniform)
+                                        (513, 40, 32), (700, 257, 32), (90, 600, 64)])
 def test_similarity_selection_is_exact_on_kernel_scores(kern, device, topk, ns, nd, dim):
     print(f"[similarity] topk={topk} ns={ns} nd={nd} dim={dim}", flush=True)
     g = torch.Generator().manual_seed(ns + nd + topk)
