@@ -584,8 +584,8 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attn_reg_kernel(AttnArgs<T> a)
 //   B_j:  group 0 P.V(j), S(j+1)      group 1 softmax(j)
 //   H_n:  group 0 --                  group 1 P.V(n-1)
 // K/V^T/bias tiles arrive by LDS DMA in a 4-stage ring (tile j in stage
-// j & 3), tile j + 2 issued by group 0 at the start of A_j; tile j is read
-// from B_{j-1} to A_{j+1}.  Only group 0 issues DMAs: the compiler does not
+// j & 3), tile j + 3 issued by group 0 at the start of B_j (under its
+// MFMAs); tile j is read from B_{j-1} to A_{j+1}.  Only group 0 issues DMAs: the compiler does not
 // see them, and a wait it inserts for its own memory operations (a register
 // reload, say) would also wait for every DMA in flight; group 0's loop has
 // none, group 1 then has no DMA to wait for.
@@ -722,21 +722,25 @@ __device__ __forceinline__ void attn_pp_segment(const AttnArgs<T>& a, T* k_lds, 
   if (group == 0) {
     issue(tile0);
     issue(tile0 + 1);
-    ring_barrier<kPPDmaPerTile>();  // tile0 has landed
+    issue(tile0 + 2);
+    ring_barrier<2 * kPPDmaPerTile>();  // tile0 has landed
     w.scores(kl(tile0), bl(tile0), s);  // H0
     pin_scores();
-    ring_barrier<kPPDmaPerTile>();
+    ring_barrier<2 * kPPDmaPerTile>();
     renew_scores();
     for (int tile = tile0; tile < tile1; ++tile) {
-      issue(tile + 2);  // A_j
-      w.softmax(s, kl(tile), bl(tile), p);
+      w.softmax(s, kl(tile), bl(tile), p);  // A_j
       pin_probs();
       __builtin_amdgcn_sched_barrier(0);
       typename WaveAttn<T>::VOps vops;
       w.load_v(vl(tile), vops);  // B_j's first operands, in flight across the barrier
       ring_barrier_reads_in_flight<kPPDmaPerTile>();  // tile + 1 has landed
       renew_probs();
-      // B_j.  After the last tile the scores of the look-ahead tile go unused.
+      // B_j.  Tile j + 3 refills the stage of tile j - 1, whose last reads
+      // (group 1's, in A_j) completed before the barrier just passed; the
+      // DMA issue runs under this phase's MFMAs rather than the softmax.
+      // After the last tile the scores of the look-ahead tile go unused.
+      issue(tile + 3);
       w.pv_scores(vops, p, kl(tile + 1), bl(tile + 1), s);
       pin_scores();
       ring_barrier<2 * kPPDmaPerTile>();
