@@ -228,3 +228,51 @@ def qkv_epilogue(qkv: torch.Tensor, heads: int, *, tokens_in: int, tokens_out: i
         _lib.stream_of(qkv))
     _lib.check(status)
     return tuple(outs)
+
+
+def residual_layer_norm(x: torch.Tensor, branch: torch.Tensor | None = None,
+                        gamma: torch.Tensor | None = None,
+                        norm: tuple[torch.Tensor | None, torch.Tensor | None, float] | None = None, *,
+                        write_sum: bool = True, norm_dtype: torch.dtype | None = torch.bfloat16,
+                        norm_f32: bool = False):
+    """One pass over fp32 rows [..., dim]: s = x + gamma * branch, n = LayerNorm(s).
+
+    `norm` = (weight, bias, eps) of the LayerNorm (affine tensors may be None).
+    Returns (s, n, n_f32): s when `write_sum` (and a branch is given), n in
+    `norm_dtype` and its fp32 copy when asked, else None in their places.
+    """
+    lib = _lib.load()
+    _lib.require_gpu(x, branch)
+    if x.dtype != torch.float32:
+        raise ValueError("residual_layer_norm: x must be float32")
+    dim = x.shape[-1]
+    rows = x.reshape(-1, dim)
+    b_rows = None
+    if branch is not None:
+        if branch.shape != x.shape:
+            raise ValueError(f"residual_layer_norm: branch {tuple(branch.shape)} != x {tuple(x.shape)}")
+        b_rows = branch.reshape(-1, dim)
+    n = rows.shape[0]
+    total = (torch.empty_like(x, memory_format=torch.contiguous_format)
+             if write_sum and branch is not None else None)
+    w = b = None
+    eps = 0.0
+    normed = normed32 = None
+    if norm is not None:
+        w, b, eps = norm
+        w = None if w is None else w.detach().to(torch.float32).contiguous()
+        b = None if b is None else b.detach().to(torch.float32).contiguous()
+        if norm_dtype is not None:
+            normed = torch.empty(x.shape, device=x.device, dtype=norm_dtype)
+        if norm_f32:
+            normed32 = torch.empty(x.shape, device=x.device, dtype=torch.float32)
+    if gamma is not None:
+        gamma = gamma.detach().to(torch.float32).contiguous()
+    status = lib.vgo_residual_layer_norm(
+        rows.data_ptr(), rows.stride(0), _c(b_rows), 0 if b_rows is None else b_rows.stride(0),
+        _lib.dtype_code(branch.dtype) if branch is not None else _lib.VGO_F32, _c(gamma), _c(w), _c(b),
+        float(eps), n, dim, _c(total), dim, _c(normed), dim,
+        _lib.dtype_code(normed.dtype) if normed is not None else _lib.VGO_BF16, _c(normed32), dim,
+        _lib.stream_of(x))
+    _lib.check(status)
+    return total, normed, normed32

@@ -112,6 +112,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "vgo_failed_rows": (_c_int, [_c_p, _c_p, _c_f32, _c_i64, _c_f32, _c_p, _c_p, _c_p]),
     "vgo_four_support_active_set": (_c_int, [_c_p, _c_p, _c_i64, _c_f32, _c_p, _c_p]),
     "vgo_four_support_projected_gradient": (_c_int, [_c_p, _c_p, _c_i64, _c_int, _c_p, _c_p]),
+    "vgo_residual_layer_norm": (_c_int, [
+        _c_p, _c_i64, _c_p, _c_i64, _c_int, _c_p, _c_p, _c_p, _c_f32, _c_i64, _c_i64, _c_p, _c_i64,
+        _c_p, _c_i64, _c_int, _c_p, _c_i64, _c_p,
+    ]),
 }
 
 _lock = threading.Lock()

@@ -226,7 +226,7 @@ class Aggregator(nn.Module):
                 return tokens.view(batch_size, num_frames, num_tokens, embed_dim)
             layout = dict(frames=num_frames, tokens_per_frame=num_tokens,
                           patch_token_start=self.patch_token_start, patch_hw=patch_hw)
-            normalized = block.norm1(tokens)
+            normalized, attn_input = block.norm1_for_plan(tokens)
             with profiling.span("global.plan_build"):
                 if self.sparse_convex_enabled:
                     if self.sparse_convex_qkv_global_layers is not None:
@@ -276,7 +276,7 @@ class Aggregator(nn.Module):
                         "kept_tokens": plan.kept_tokens,
                         "merged_tokens": plan.original_tokens - plan.kept_tokens,
                         "merge_ratio": 1.0 - plan.keep_ratio, **plan.metadata})
-            tokens = block.forward_compacted(tokens, plan, normalized=normalized)
+            tokens = block.forward_compacted(tokens, plan, normalized=attn_input)
         return tokens.view(batch_size, num_frames, num_tokens, embed_dim)
 
 

@@ -1,0 +1,247 @@
+// Residual-stream rows of a transformer block in one pass per row:
+//   s[r,:]  = x[r,:] + gamma * branch[r,:]          (LayerScale + residual add)
+//   n[r,:]  = (s[r,:] - mean) * rsqrt(var + eps) * w + b   (LayerNorm over dim)
+// The block is vggt_omega/models/layers/block.py:126-127 and :219-226,
+//   x_attn = x + ls1(attn(norm1(x)));  x_ffn = x_attn + ls2(mlp(norm2(x_attn))),
+// with LayerScale = `x * gamma` (layer_scale.py:38) and torch LayerNorm.  Under
+// bf16 autocast the reference runs each of these as its own pass over the fp32
+// stream (multiply, add, layer_norm, then the cast autocast puts in front of the
+// next Linear); here one wave reads a row once and writes the new stream row
+// and its normalised, already-cast copy.
+//
+// s is bit-identical to the reference's: the branch element is widened to fp32,
+// multiplied by gamma and added to x with separate IEEE roundings (no fused
+// multiply-add; the library is built with -ffp-contract=off), exactly the two
+// fp32 ops torch performs.  The LayerNorm uses two passes over the row held in
+// registers (mean, then the mean of squared deviations) and differs from torch's
+// Welford pass only by fp32 rounding.
+//
+// One wave per row, four rows per work-group; lane l owns elements 4(l + 64i) ..
+// 4(l + 64i) + 3, so each load or store instruction of a wave covers one
+// contiguous 1 KB (fp32) or 512 B (16-bit) span.  HBM-bound: per row it reads
+// 4*dim (x) + s_b*dim (branch) and writes 4*dim (s) + s_n*dim (n).
+#include "vgo_common.h"
+
+namespace vgo {
+namespace {
+
+// 4-element chunks per lane: dim <= 4 * 64 * kChunks.  Two instantiations,
+// kChunks = 4 (dim <= 1024) and 8 (dim <= 2048), keep the register budget of the
+// common case small.
+constexpr int kRowChunks = 8;
+
+template <typename T>
+struct Vec4;
+template <>
+struct Vec4<float> {
+  using type = f32x4;
+};
+template <>
+struct Vec4<bf16_t> {
+  using type = bf16x4;
+};
+template <>
+struct Vec4<f16_t> {
+  using type = f16x4;
+};
+
+template <typename T>
+__device__ __forceinline__ f32x4 load4(const T* p) {
+  const typename Vec4<T>::type v = *reinterpret_cast<const typename Vec4<T>::type*>(p);
+  return f32x4{to_f32(v[0]), to_f32(v[1]), to_f32(v[2]), to_f32(v[3])};
+}
+
+template <typename T>
+__device__ __forceinline__ void store4(T* p, f32x4 v) {
+  typename Vec4<T>::type o;
+  o[0] = from_f32<T>(v[0]);
+  o[1] = from_f32<T>(v[1]);
+  o[2] = from_f32<T>(v[2]);
+  o[3] = from_f32<T>(v[3]);
+  *reinterpret_cast<typename Vec4<T>::type*>(p) = o;
+}
+
+// Butterfly sum: every lane ends with the same value (each exchange adds the
+// same two operands in either order).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+struct RowArgs {
+  const float* x;
+  int64_t x_stride;
+  const void* branch;
+  int64_t branch_stride;
+  const float* gamma;
+  const float* ln_w;
+  const float* ln_b;
+  float eps;
+  int64_t rows;
+  int dim;
+  float* x_out;
+  int64_t x_out_stride;
+  void* norm;
+  int64_t norm_stride;
+  float* norm_f32;
+  int64_t norm_f32_stride;
+};
+
+template <int kChunks, bool kBranch, typename TB, typename TN>
+__global__ __launch_bounds__(256) void residual_ln_kernel(RowArgs a) {
+  const int lane = lane_id();
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (r >= a.rows) return;
+  const int chunks = a.dim >> 2;
+  // Every load is unconditional, so one wait covers them all: a lane's chunk
+  // offset is clamped into the row and chunks past its end are zeroed after
+  // loading; a NULL parameter vector reads x's first row in its place and the
+  // value is then replaced by the identity.
+  int off[kChunks];
+  bool live[kChunks];
+#pragma unroll
+  for (int i = 0; i < kChunks; ++i) {
+    const int c = i * 64 + lane;
+    live[i] = c < chunks;
+    off[i] = 4 * (live[i] ? c : chunks - 1);
+  }
+  const float* xr = a.x + r * a.x_stride;
+  const float* gp = a.gamma ? a.gamma : a.x;
+  const float* wp = a.ln_w ? a.ln_w : a.x;
+  const float* bp = a.ln_b ? a.ln_b : a.x;
+  f32x4 v[kChunks], w[kChunks], bias[kChunks];
+#pragma unroll
+  for (int i = 0; i < kChunks; ++i) v[i] = *reinterpret_cast<const f32x4*>(xr + off[i]);
+  if constexpr (kBranch) {
+    const TB* br = static_cast<const TB*>(a.branch) + r * a.branch_stride;
+    f32x4 b[kChunks], g[kChunks];
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+      b[i] = load4(br + off[i]);
+      g[i] = *reinterpret_cast<const f32x4*>(gp + off[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+      w[i] = *reinterpret_cast<const f32x4*>(wp + off[i]);
+      bias[i] = *reinterpret_cast<const f32x4*>(bp + off[i]);
+    }
+    // Empty asm reading the loaded registers: the loads that are only used
+    // under a NULL test cannot sink into that branch behind a wait of their own.
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) asm volatile("" : "+v"(b[i]), "+v"(g[i]), "+v"(w[i]), "+v"(bias[i]));
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+      if (a.gamma) b[i] = b[i] * g[i];
+      v[i] = v[i] + b[i];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+      w[i] = *reinterpret_cast<const f32x4*>(wp + off[i]);
+      bias[i] = *reinterpret_cast<const f32x4*>(bp + off[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) asm volatile("" : "+v"(w[i]), "+v"(bias[i]));
+  }
+  if (a.x_out) {
+    float* xo = a.x_out + r * a.x_out_stride;
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i)
+      if (live[i]) *reinterpret_cast<f32x4*>(xo + off[i]) = v[i];
+  }
+  if (!a.norm && !a.norm_f32) return;
+
+  const float inv_dim = 1.0f / static_cast<float>(a.dim);
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kChunks; ++i)
+    s += live[i] ? (v[i][0] + v[i][1]) + (v[i][2] + v[i][3]) : 0.0f;
+  const float mean = wave_sum(s) * inv_dim;
+  float q = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kChunks; ++i) {
+    const f32x4 d = v[i] - mean;
+    v[i] = d;
+    q += live[i] ? (d[0] * d[0] + d[1] * d[1]) + (d[2] * d[2] + d[3] * d[3]) : 0.0f;
+  }
+  const float rstd = 1.0f / sqrtf(wave_sum(q) * inv_dim + a.eps);
+  TN* no = a.norm ? static_cast<TN*>(a.norm) + r * a.norm_stride : nullptr;
+  float* nf = a.norm_f32 ? a.norm_f32 + r * a.norm_f32_stride : nullptr;
+#pragma unroll
+  for (int i = 0; i < kChunks; ++i) {
+    f32x4 n = v[i] * rstd;
+    if (a.ln_w) n = n * w[i];
+    if (a.ln_b) n = n + bias[i];
+    if (!live[i]) continue;
+    if (no) store4(no + off[i], n);
+    if (nf) *reinterpret_cast<f32x4*>(nf + off[i]) = n;
+  }
+}
+
+template <bool kBranch, typename TB, typename TN>
+int launch_rows(const RowArgs& a, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((a.rows + 3) / 4));
+  if (a.dim <= 4 * 64 * 4)
+    hipLaunchKernelGGL((residual_ln_kernel<4, kBranch, TB, TN>), grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((residual_ln_kernel<kRowChunks, kBranch, TB, TN>), grid, dim3(256), 0, s, a);
+  return check_launch("residual_layer_norm");
+}
+
+template <typename TN>
+int dispatch_branch(const RowArgs& a, int branch_dtype, hipStream_t s) {
+  if (!a.branch) return launch_rows<false, float, TN>(a, s);
+  switch (branch_dtype) {
+    case VGO_BF16: return launch_rows<true, bf16_t, TN>(a, s);
+    case VGO_F16: return launch_rows<true, f16_t, TN>(a, s);
+    case VGO_F32: return launch_rows<true, float, TN>(a, s);
+    default: return fail(VGO_EINVAL, "residual_layer_norm: unsupported branch dtype");
+  }
+}
+
+size_t dtype_bytes(int dtype) { return dtype == VGO_F32 ? 4 : 2; }
+
+}  // namespace
+}  // namespace vgo
+
+extern "C" int vgo_residual_layer_norm(const float* x, int64_t x_row_stride, const void* branch,
+                                       int64_t branch_row_stride, int branch_dtype,
+                                       const float* gamma, const float* ln_weight,
+                                       const float* ln_bias, float eps, int64_t rows, int64_t dim,
+                                       float* x_out, int64_t x_out_row_stride, void* norm_out,
+                                       int64_t norm_row_stride, int norm_dtype, float* norm_f32,
+                                       int64_t norm_f32_row_stride, void* stream) {
+  using namespace vgo;
+  VGO_REQUIRE(rows >= 0 && dim >= 0, "residual_layer_norm: negative size");
+  if (rows == 0 || dim == 0) return VGO_OK;
+  VGO_REQUIRE(x, "residual_layer_norm: null x");
+  VGO_REQUIRE(x_out || norm_out || norm_f32, "residual_layer_norm: no output");
+  VGO_REQUIRE(branch || !x_out || x_out == x,
+              "residual_layer_norm: x_out without a branch must be NULL or x itself");
+  VGO_REQUIRE(dim % 4 == 0 && dim <= 4 * 64 * kRowChunks,
+              "residual_layer_norm: dim must be a multiple of 4 and at most 2048");
+  VGO_REQUIRE(rows < (int64_t(1) << 33), "residual_layer_norm: too many rows");
+  VGO_REQUIRE(norm_dtype == VGO_BF16 || norm_dtype == VGO_F16 || !norm_out,
+              "residual_layer_norm: norm_out must be bf16 or f16");
+  VGO_REQUIRE(branch_dtype == VGO_BF16 || branch_dtype == VGO_F16 || branch_dtype == VGO_F32 || !branch,
+              "residual_layer_norm: unsupported branch dtype");
+  // Four-element vector accesses: every row start must be 4-element aligned.
+  auto vec_ok = [](const void* p, int64_t stride, size_t elem) {
+    return !p || (aligned(p, 4 * elem) && stride % 4 == 0);
+  };
+  VGO_REQUIRE(vec_ok(x, x_row_stride, 4) && vec_ok(x_out, x_out_row_stride, 4) &&
+                  vec_ok(norm_f32, norm_f32_row_stride, 4) &&
+                  vec_ok(branch, branch_row_stride, dtype_bytes(branch_dtype)) &&
+                  vec_ok(norm_out, norm_row_stride, 2) && vec_ok(gamma, 0, 4) &&
+                  vec_ok(ln_weight, 0, 4) && vec_ok(ln_bias, 0, 4),
+              "residual_layer_norm: pointers must be 4-element aligned and row strides multiples of 4");
+  VGO_REQUIRE(!x_out || x_out == x || x_out_row_stride != 0,
+              "residual_layer_norm: zero x_out row stride");
+  RowArgs a{x, x_row_stride, branch, branch_row_stride, gamma, ln_weight, ln_bias, eps, rows,
+            static_cast<int>(dim), x_out, x_out_row_stride, norm_out, norm_row_stride, norm_f32,
+            norm_f32_row_stride};
+  hipStream_t s = as_stream(stream);
+  if (norm_out && norm_dtype == VGO_F16) return dispatch_branch<f16_t>(a, branch_dtype, s);
+  return dispatch_branch<bf16_t>(a, branch_dtype, s);
+}

@@ -392,17 +392,83 @@ class SelfAttentionBlock(nn.Module):
 
     def forward(self, x: Tensor, rope=None) -> Tensor:
         """Inference forward of block.py:89-129 (no stochastic depth)."""
+        if self._fused_rows(x):
+            return self._fused_tail(x, self.attn(self._norm1_input(x), rope=rope))
         x_attn = x + self.ls1(self.attn(self.norm1(x), rope=rope))
         return x_attn + self.ls2(self.mlp(self.norm2(x_attn)))
 
     def forward_compacted(self, x: Tensor, token_plan, *, normalized: Tensor = None) -> Tensor:
-        """Inference-only compact-Q/K/V attention block (block.py:219-226)."""
+        """Inference-only compact-Q/K/V attention block (block.py:219-226).
+
+        `normalized` is norm1(x) as the attention input: fp32 as the reference
+        computes it, or already cast to the autocast dtype (`norm1_for_plan`)."""
         if self.training:
             raise RuntimeError("token compaction is inference-only")
         if normalized is None:
-            normalized = self.norm1(x)
+            normalized = self._norm1_input(x) if self._fused_rows(x) else self.norm1(x)
+        if self._fused_rows(x):
+            return self._fused_tail(x, self.attn(normalized, token_plan=token_plan))
         x_attn = x + self.ls1(self.attn(normalized, token_plan=token_plan))
         return x_attn + self.ls2(self.mlp(self.norm2(x_attn)))
+
+    def norm1_for_plan(self, x: Tensor) -> tuple[Tensor, Tensor]:
+        """(norm1(x) in fp32 for the planners, the same rows as the attention input).
+
+        With the fused row kernel both come from one pass, the second already in
+        the autocast dtype the qkv Linear would cast it to; otherwise both are
+        the reference's fp32 `norm1(x)` (aggregator.py:1002)."""
+        if self._fused_rows(x):
+            _, h, h32 = _kernels.residual_layer_norm(x, norm=_ln_args(self.norm1),
+                                                     norm_dtype=_autocast_dtype(), norm_f32=True)
+            return h32, h
+        n = self.norm1(x)
+        return n, n
+
+    # ------------------------------------------------ fused residual rows ----
+    def _fused_rows(self, x: Tensor) -> bool:
+        """The residual stream runs through vgo_residual_layer_norm: inference under
+        bf16/f16 autocast on an fp32 stream, torch LayerNorms over the last dim,
+        LayerScale (not in place) or Identity, rows the kernel can address."""
+        if torch.is_grad_enabled() or self.training or not x.is_cuda or x.dtype != torch.float32:
+            return False
+        if _autocast_dtype() is None:
+            return False
+        dim = x.shape[-1]
+        for norm in (self.norm1, self.norm2):
+            if type(norm) is not nn.LayerNorm or tuple(norm.normalized_shape) != (dim,):
+                return False
+        for ls in (self.ls1, self.ls2):
+            if not (type(ls) is nn.Identity or (type(ls) is LayerScale and not ls.inplace)):
+                return False
+        return (dim % 4 == 0 and dim <= 2048 and x.is_contiguous() and x.data_ptr() % 16 == 0)
+
+    def _norm1_input(self, x: Tensor) -> Tensor:
+        return _kernels.residual_layer_norm(x, norm=_ln_args(self.norm1), norm_dtype=_autocast_dtype())[1]
+
+    def _fused_tail(self, x: Tensor, y: Tensor) -> Tensor:
+        """x_attn = x + ls1(y); return x_attn + ls2(mlp(norm2(x_attn))) with two row passes."""
+        if y.shape != x.shape or y.stride(-1) != 1:
+            y = y.reshape(x.shape).contiguous()
+        x_attn, h, _ = _kernels.residual_layer_norm(x, y, _ls_gamma(self.ls1), _ln_args(self.norm2),
+                                                    norm_dtype=_autocast_dtype())
+        out, _, _ = _kernels.residual_layer_norm(x_attn, self.mlp(h).reshape(x.shape),
+                                                 _ls_gamma(self.ls2))
+        return out
+
+
+def _autocast_dtype() -> torch.dtype | None:
+    if torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") in (
+            torch.bfloat16, torch.float16):
+        return torch.get_autocast_dtype("cuda")
+    return None
+
+
+def _ln_args(norm: nn.LayerNorm):
+    return (norm.weight, norm.bias, norm.eps)
+
+
+def _ls_gamma(ls: nn.Module) -> Tensor | None:
+    return ls.gamma if isinstance(ls, LayerScale) else None
 
 
 def init_weights_vit(module: nn.Module, name: str = "") -> None:

@@ -174,6 +174,7 @@ def torch_reference_forward(model, ref_global, patches):
     # RoPE, SDPA) -- not on this build's fused kernels.
     for blk in list(model.frame_blocks) + list(model.inter_frame_blocks):
         blk.attn._fusable = lambda *a: False
+        blk._fused_rows = lambda x: False
     for i in range(model.depth):
         tokens = model.frame_blocks[i](tokens.view(B * S, T, D), (sin, cos))
         tokens = tokens.view(B, S, T, D)
@@ -186,6 +187,7 @@ def torch_reference_forward(model, ref_global, patches):
             tokens = ref_global.block(blk, tokens.reshape(B, S * T, D)).view(B, S, T, D)
     for blk in list(model.frame_blocks) + list(model.inter_frame_blocks):
         del blk.attn._fusable
+        del blk._fused_rows
     return tokens
 
 
@@ -204,6 +206,35 @@ def c3_attention(vgo, device, steps):
         q, k, v, attn_mask=mass.bfloat16().view(1, 1, 1, -1)), max(2, steps // 4), 1)
     return {"nq": nq, "nk": nk, "ms": sec * 1e3, "tflops": flops / sec / 1e12,
             "frac": flops / sec / 1e12 / PEAK_BF16_TFLOPS, "torch_sdpa_ms": sdpa * 1e3}
+
+
+def block_rows(device, steps):
+    """Residual stream of one block at C4 sizes (32,928 x 1,024 fp32 rows).
+
+    x_attn = x + ls(branch) and norm2(x_attn) cast to bf16: one
+    vgo_residual_layer_norm pass against torch's multiply, add, layer_norm and
+    cast.  Algorithmic bytes: read x (4) + branch (2), write x_attn (4) + the
+    bf16 norm (2) per element."""
+    kern = importlib.import_module("4d_ttt_merging_amd._kernels")
+    n = FRAMES * (SPECIALS + 1024)
+    g = torch.Generator(device=device).manual_seed(9)
+    x = torch.randn(n, DIM, device=device, generator=g)
+    branch = torch.randn(n, DIM, device=device, generator=g).bfloat16()
+    gamma = torch.rand(DIM, device=device, generator=g)
+    w, b = torch.ones(DIM, device=device), torch.zeros(DIM, device=device)
+
+    def fused():
+        kern.residual_layer_norm(x, branch, gamma, (w, b, 1e-6))
+
+    def reference():
+        x_attn = x + branch * gamma
+        F.layer_norm(x_attn, (DIM,), w, b, 1e-6).to(torch.bfloat16)
+
+    sec = event_time(fused, steps, 3)
+    sec_ref = event_time(reference, steps, 3)
+    nbytes = n * DIM * (4 + 2 + 4 + 2)
+    return {"rows": n, "dim": DIM, "fused_ms": sec * 1e3, "fused_gbs": nbytes / sec / 1e9,
+            "torch_ms": sec_ref * 1e3}
 
 
 def special_pass(device, steps):
@@ -523,6 +554,8 @@ def main() -> int:
     torch.cuda.synchronize()
     log("C3 attention microbench")
     result["c3_attention"] = c3_attention(vgo, device, 20)
+    log("block residual rows microbench")
+    result["block_rows"] = block_rows(device, 20)
     log("special-query pass microbench")
     result["special_pass"] = special_pass(device, 20)
     log("plan replay microbench")

@@ -335,6 +335,28 @@ int vgo_four_support_projected_gradient(const float* gram, const float* rhs, int
 int vgo_failed_rows(const float* fit, const float* top1, float easy_threshold, int64_t n,
                     float threshold, int32_t* list, int* count, void* stream);
 
+/*
+ * Residual-stream rows of a transformer block, one pass per row of dim fp32
+ * values (dim a multiple of 4, at most 2048):
+ *   s = x + gamma * branch   (branch == NULL: s = x; gamma == NULL: gamma = 1),
+ *   written to x_out (NULL: not written; may equal x),
+ *   LN(s) = (s - mean) / sqrt(var + eps) * ln_weight + ln_bias (either affine
+ *   pointer may be NULL), written to norm_out in norm_dtype (bf16 or f16) and/or
+ *   to norm_f32 (either may be NULL).
+ * s is bit-identical to torch's `x + branch * gamma` in fp32 (branch widened
+ * first, separate roundings).  Pointers are 4-element aligned and row strides
+ * are multiples of 4 elements.  Replaces the LayerScale multiply, residual add,
+ * LayerNorm and autocast cast of SelfAttentionBlock.forward /
+ * forward_compacted (vggt_omega/models/layers/block.py:126-127, 219-226;
+ * layer_scale.py:38).
+ */
+int vgo_residual_layer_norm(const float* x, int64_t x_row_stride, const void* branch,
+                            int64_t branch_row_stride, int branch_dtype, const float* gamma,
+                            const float* ln_weight, const float* ln_bias, float eps, int64_t rows,
+                            int64_t dim, float* x_out, int64_t x_out_row_stride, void* norm_out,
+                            int64_t norm_row_stride, int norm_dtype, float* norm_f32,
+                            int64_t norm_f32_row_stride, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

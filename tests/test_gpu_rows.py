@@ -1,0 +1,158 @@
+"""Residual-stream rows (vgo_residual_layer_norm) against torch's op sequence.
+
+* s = x + branch * gamma is compared bit for bit with torch's fp32 result on
+  the CPU (the kernel performs the same two IEEE operations).
+* LayerNorm(s) in fp32 is within the fp32 bar (1e-5) of `F.layer_norm` in
+  float64, and the 16-bit copy is within half an ulp of such a value (one
+  rounding of an fp32 result, as autocast's cast of torch's fp32 LayerNorm).
+* Shapes cover the 4- and 8-chunk instantiations, dims that are not a multiple
+  of 256, one row, rows not a multiple of the four rows per work-group, no
+  gamma / no affine / no branch, and the in-place form.
+* SelfAttentionBlock.forward and forward_compacted with the fused rows match
+  the reference op sequence (torch LayerNorm, LayerScale, add, autocast casts)
+  within the bf16 bar.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from tests._tol import assert_close
+from tests.conftest import import_package
+from tests.golden.inputs import structured_tokens
+
+pytestmark = pytest.mark.gpu
+
+KW = dict(frames=4, patch_hw=(16, 16), tokens_per_frame=261, patch_token_start=5)
+
+
+@pytest.fixture(scope="module")
+def kern():
+    return import_package("_kernels")
+
+
+def _inputs(rows, dim, branch_dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(rows, dim, generator=g) * 3 + 0.5
+    branch = (torch.randn(rows, dim, generator=g) * 2).to(branch_dtype)
+    gamma = torch.rand(dim, generator=g) * 0.7 + 0.05
+    w = 1 + 0.2 * torch.randn(dim, generator=g)
+    b = 0.1 * torch.randn(dim, generator=g)
+    return x, branch, gamma, w, b
+
+
+def _rounded_close(actual: torch.Tensor, ref64: torch.Tensor, dtype: torch.dtype, what: str):
+    """actual (16-bit) is a round-to-nearest of some value within the fp32 bar of ref64:
+    |actual - ref| <= ulp(actual) / 2 + 1e-5 * max(|ref|, rms(ref))."""
+    got = actual.double().cpu()
+    ref = ref64.double().cpu()
+    _, expo = torch.frexp(got)
+    half_ulp = torch.ldexp(torch.full_like(got, torch.finfo(dtype).eps / 2), expo - 1)
+    scale = torch.maximum(ref.abs(), ref.pow(2).mean().sqrt())
+    bad = (got - ref).abs() > half_ulp + 1e-5 * scale
+    assert not bad.any(), f"{what}: {int(bad.sum())} elements beyond half an ulp + the fp32 bar"
+
+
+@pytest.mark.parametrize("rows,dim,branch_dtype,norm_dtype", [
+    (1029, 1024, torch.bfloat16, torch.bfloat16),
+    (5, 1024, torch.float16, torch.float16),
+    (1, 256, torch.float32, torch.bfloat16),
+    (333, 1028, torch.bfloat16, torch.bfloat16),
+    (77, 2048, torch.bfloat16, torch.bfloat16),
+    (64, 1536, torch.float16, torch.bfloat16),
+    (9, 4, torch.bfloat16, torch.float16),
+])
+def test_residual_layer_norm_matches_torch(kern, device, rows, dim, branch_dtype, norm_dtype):
+    print(f"[rows] residual+LN rows={rows} dim={dim} {branch_dtype} -> {norm_dtype}", flush=True)
+    x, branch, gamma, w, b = _inputs(rows, dim, branch_dtype, rows * 7 + dim)
+    s, n, n32 = kern.residual_layer_norm(x.to(device), branch.to(device), gamma.to(device),
+                                         (w.to(device), b.to(device), 1e-5), norm_dtype=norm_dtype,
+                                         norm_f32=True)
+    ref_s = x + branch * gamma  # torch's fp32 mul then add (block.py:126)
+    assert s.dtype == torch.float32 and torch.equal(s.cpu(), ref_s)
+    ref64 = F.layer_norm(ref_s.double(), (dim,), w.double(), b.double(), 1e-5)
+    assert_close(n32.cpu(), ref64, torch.float32, what="fp32 LayerNorm")
+    _rounded_close(n, ref64, norm_dtype, "16-bit LayerNorm")
+
+
+def test_residual_layer_norm_variants(kern, device):
+    print("[rows] variants", flush=True)
+    x, branch, gamma, w, b = _inputs(130, 1024, torch.bfloat16, 3)
+    xd, bd = x.to(device), branch.to(device)
+    # No gamma (Identity LayerScale), no affine LayerNorm.
+    s, n, _ = kern.residual_layer_norm(xd, bd, None, (None, None, 1e-6), norm_dtype=torch.bfloat16)
+    ref_s = x + branch.float()
+    assert torch.equal(s.cpu(), ref_s)
+    _rounded_close(n, F.layer_norm(ref_s.double(), (1024,), eps=1e-6), torch.bfloat16, "no-affine LayerNorm")
+    # LayerNorm only (norm1 of a block): no branch, no sum written.
+    s, n, n32 = kern.residual_layer_norm(xd, norm=(w.to(device), b.to(device), 1e-5), norm_f32=True)
+    assert s is None
+    assert_close(n32.cpu(), F.layer_norm(x.double(), (1024,), w.double(), b.double(), 1e-5),
+                 torch.float32, what="LN-only fp32")
+    _rounded_close(n, F.layer_norm(x.double(), (1024,), w.double(), b.double(), 1e-5), torch.bfloat16,
+                   "LN-only bf16")
+    # Residual only, written in place over x.
+    lib_mod = import_package("_lib")
+    lib = lib_mod.load()
+    xi = xd.clone()
+    status = lib.vgo_residual_layer_norm(
+        xi.data_ptr(), 1024, bd.data_ptr(), 1024, lib_mod.VGO_BF16, gamma.to(device).data_ptr(),
+        None, None, 0.0, 130, 1024, xi.data_ptr(), 1024, None, 0, lib_mod.VGO_BF16, None, 0,
+        torch.cuda.current_stream().cuda_stream)
+    lib_mod.check(status)
+    assert torch.equal(xi.cpu(), x + branch * gamma)
+    # Zero rows is a no-op; bad sizes and misaligned rows are rejected on the host.
+    lib_mod.check(lib.vgo_residual_layer_norm(None, 0, None, 0, 0, None, None, None, 0.0, 0, 1024, None,
+                                              0, None, 0, 1, None, 0, None))
+    with pytest.raises(ValueError, match="multiple of 4"):
+        kern.residual_layer_norm(xd[:, :1022].contiguous(), norm=(None, None, 1e-5))
+    with pytest.raises(ValueError, match="aligned"):
+        kern.residual_layer_norm(xd.view(-1)[1:1 + 129 * 1024].view(129, 1024), norm=(None, None, 1e-5))
+
+
+def _block(vgo, device, seed, init_values=0.3):
+    torch.manual_seed(seed)
+    block = vgo.SelfAttentionBlock(256, 4, qkv_bias=True, init_values=init_values, mask_k_bias=True,
+                                   use_qk_norm=True).eval().to(device)
+    with torch.no_grad():
+        for norm in (block.norm1, block.norm2):
+            norm.weight.normal_(1.0, 0.2)
+            norm.bias.normal_(0.0, 0.1)
+    return block
+
+
+def _reference_rows(block):
+    """Switch the block to the reference op sequence for its residual rows."""
+    block._fused_rows = lambda x: False
+
+
+@pytest.mark.parametrize("init_values", [0.3, None])
+def test_block_forward_fused_rows_match_reference(vgo, device, init_values):
+    print(f"[rows] block forward init_values={init_values}", flush=True)
+    layers = import_package("layers")
+    block = _block(vgo, device, 5, init_values)
+    x = structured_tokens(6, 3, (16, 16), 5, 256)[0].view(3, 261, 256).to(device)
+    sin, cos = layers.rope_sincos(16, 16, 64, device=device)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        assert block._fused_rows(x)
+        fused = block(x, rope=(sin, cos))
+        _reference_rows(block)
+        ref = block(x, rope=(sin, cos))
+    assert fused.dtype == ref.dtype == torch.float32
+    assert_close(fused.cpu(), ref.cpu(), torch.bfloat16, what="block forward")
+
+
+def test_block_forward_compacted_fused_rows_match_reference(vgo, device):
+    print("[rows] block forward_compacted", flush=True)
+    block = _block(vgo, device, 7)
+    x = structured_tokens(9, 4, (16, 16), 5, 256).to(device)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        normalized, attn_input = block.norm1_for_plan(x)
+        assert normalized.dtype == torch.float32 and attn_input.dtype == torch.bfloat16
+        assert_close(normalized.cpu(), block.norm1.float()(x).cpu(), torch.float32, what="norm1 fp32")
+        plan = vgo.build_sparse_convex_plan(normalized, threshold=0.9, **KW)
+        fused = block.forward_compacted(x, plan, normalized=attn_input)
+        _reference_rows(block)
+        ref = block.forward_compacted(x, plan, normalized=block.norm1(x))
+    assert_close(fused.cpu(), ref.cpu(), torch.bfloat16, what="forward_compacted")
