@@ -13,6 +13,8 @@ reference package `vggt_omega` for the merged global-attention path:
 * `top4_project`                         the restore gather of the plans
 * `plan_io` (`save_plan`, `load_plan`, `load_ttt_trace`, ...)  plan files and
   replay of the TTT planner's trace records (sparse_convex.py:77-80, 1907-1976)
+* `use_tuned_gemms`                      recorded hipBLASLt selections for the
+  block's torch GEMMs (TunableOp)
 
 Every GPU computation of the path runs in the hand-written gfx950 HIP library
 `libvgo.so` (built by `_build.build()`); there is no CPU fallback.
@@ -20,6 +22,7 @@ Every GPU computation of the path runs in the hand-written gfx950 HIP library
 from __future__ import annotations
 
 from . import _lib, plan_io
+from .gemm_tuning import use_tuned_gemms
 from .layers import LinearKMaskedBias, SelfAttention, SelfAttentionBlock
 from .mass_bias_attention import dense_attention, mass_bias_attention
 from .projection import top4_project
@@ -47,4 +50,5 @@ __all__ = [
     "plan_io",
     "streaming_top4",
     "top4_project",
+    "use_tuned_gemms",
 ]

@@ -13,12 +13,15 @@ import os
 import torch
 
 _enabled = os.environ.get("VGO_PROFILE_ATTENTION", "0") == "1"
+_only: frozenset[str] | None = None
 _events: list[tuple[str, torch.cuda.Event, torch.cuda.Event]] = []
 
 
-def enable(flag: bool = True) -> None:
-    global _enabled
+def enable(flag: bool = True, only=None) -> None:
+    """Switch recording on or off; `only` restricts it to the given labels."""
+    global _enabled, _only
     _enabled = flag
+    _only = None if only is None else frozenset(only)
 
 
 def enabled() -> bool:
@@ -39,7 +42,7 @@ class span:
         self.begin = None
 
     def __enter__(self):
-        if _enabled:
+        if _enabled and (_only is None or self.label in _only):
             self.begin = torch.cuda.Event(enable_timing=True)
             self.begin.record()
         return self

@@ -156,3 +156,21 @@ def test_block_forward_compacted_fused_rows_match_reference(vgo, device):
         _reference_rows(block)
         ref = block.forward_compacted(x, plan, normalized=block.norm1(x))
     assert_close(fused.cpu(), ref.cpu(), torch.bfloat16, what="forward_compacted")
+
+
+def test_tuned_gemm_table_loads_and_matches_default(vgo, device):
+    print("[rows] tuned GEMM table", flush=True)
+    tuning = import_package("gemm_tuning")
+    g = torch.Generator(device=device).manual_seed(4)
+    x = torch.randn(32928, 1024, device=device, generator=g)
+    lin = torch.nn.Linear(1024, 3072, device=device)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        default = lin(x)
+        try:
+            assert tuning.use_tuned_gemms()
+            assert torch.cuda.tunable.is_enabled()
+            tuned = lin(x)
+        finally:
+            tuning.default_gemms()
+    assert tuned.dtype == torch.bfloat16
+    assert_close(tuned.float().cpu(), default.float().cpu(), torch.bfloat16, what="tuned GEMM")
