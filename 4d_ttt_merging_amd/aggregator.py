@@ -196,7 +196,8 @@ class Aggregator(nn.Module):
             tokens = self.frame_blocks[block_idx](tokens, rope)
             frame_tokens = tokens.view(batch_size, num_frames, num_tokens, embed_dim)
             tokens = self._run_inter_frame_attention_block(
-                tokens, batch_size, num_frames, num_tokens, embed_dim, block_idx, grid)
+                tokens, batch_size, num_frames, num_tokens, embed_dim, block_idx, grid,
+                reuse_input=block_idx not in self.cached_layer_indices)
             if block_idx in self.cached_layer_indices:
                 outputs.append(torch.cat([frame_tokens, tokens], dim=-1))
             else:
@@ -204,7 +205,10 @@ class Aggregator(nn.Module):
         return outputs, self.patch_token_start
 
     def _run_inter_frame_attention_block(self, tokens, batch_size, num_frames, num_tokens,
-                                         embed_dim, block_idx, patch_hw) -> torch.Tensor:
+                                         embed_dim, block_idx, patch_hw,
+                                         reuse_input: bool = False) -> torch.Tensor:
+        """`reuse_input`: the caller keeps no other reference to `tokens`, so a register
+        block may write its special rows into it instead of concatenating a new tensor."""
         kind = self.inter_frame_attention_types[block_idx]
         block = self.inter_frame_blocks[block_idx]
         tokens = tokens.view(batch_size, num_frames, num_tokens, embed_dim)
@@ -212,6 +216,9 @@ class Aggregator(nn.Module):
             pts = self.patch_token_start
             special = tokens[:, :, :pts].reshape(batch_size, num_frames * pts, embed_dim)
             special = block(special, None).view(batch_size, num_frames, pts, embed_dim)
+            if reuse_input and special.dtype == tokens.dtype and not torch.is_grad_enabled():
+                tokens[:, :, :pts] = special
+                return tokens
             return torch.cat([special, tokens[:, :, pts:]], dim=2)
         if kind != "global":
             raise ValueError(f"Unknown inter-frame attention type: {kind}")

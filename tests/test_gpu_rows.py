@@ -174,3 +174,23 @@ def test_tuned_gemm_table_loads_and_matches_default(vgo, device):
             tuning.default_gemms()
     assert tuned.dtype == torch.bfloat16
     assert_close(tuned.float().cpu(), default.float().cpu(), torch.bfloat16, what="tuned GEMM")
+
+
+def test_aggregator_register_rows_in_place_match_concatenation(device):
+    """A register block writes its special rows into the frame block's output when no
+    cached layer keeps that tensor; the result equals the concatenating path."""
+    print("[rows] aggregator register rows in place", flush=True)
+    agg = import_package("aggregator")
+    torch.manual_seed(0)
+    model = agg.Aggregator(embed_dim=256, depth=3, num_heads=4, num_register_tokens=4,
+                           register_attention_block_indices=(1,),
+                           cached_layer_indices=(2,)).to(device).eval()
+    patches = structured_tokens(2, 4, (16, 16), 5, 256)[0].view(4, 261, 256)[:, 5:].contiguous()
+    model.set_input_patch_tokens_cache(patches.to(device))
+    images = torch.zeros(1, 4, 3, 256, 256, device=device)
+    model.set_fastvggt(True, merge_ratio=0.5, protect_ratio=0.0, mass_bias=True)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        in_place = model(images)[0][2]
+        model.cached_layer_indices = {0, 1, 2}  # every frame output kept: concatenation
+        concatenated = model(images)[0][2]
+    assert torch.equal(in_place, concatenated)
