@@ -63,35 +63,13 @@ __device__ __forceinline__ void store16(T* p, const float* v) {
   }
 }
 
-// LayerNorm over the 64 channels held by four consecutive lanes (16 each).
-__device__ __forceinline__ void head_layer_norm(float* v, const float* w, const float* b, int d0,
-                                                float eps) {
-  float s = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 16; ++j) s += v[j];
-  s += __shfl_xor(s, 1);
-  s += __shfl_xor(s, 2);
-  const float mean = s / 64.0f;
-  float q = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const float d = v[j] - mean;
-    q = fmaf(d, d, q);
-  }
-  q += __shfl_xor(q, 1);
-  q += __shfl_xor(q, 2);
-  const float rstd = 1.0f / sqrtf(q / 64.0f + eps);
-#pragma unroll
-  for (int j = 0; j < 16; ++j) v[j] = (v[j] - mean) * rstd * w[d0 + j] + b[d0 + j];
-}
-
 // x*cos + rotate_half(x)*sin over a 64-channel head; the partner half lives in lane ^ 2.
 __device__ __forceinline__ void rope16(float* v, const float* sin_row, const float* cos_row, int d0) {
   const bool first_half = d0 < 32;
   float rot[16];
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
-    const float partner = __shfl_xor(v[j], 2);
+    const float partner = quad_xor<2>(v[j]);
     rot[j] = first_half ? -partner : partner;
   }
 #pragma unroll
@@ -124,13 +102,13 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(
     float v[16];
     if (q_out) {
       load16(row + c0, v);
-      if (qw) head_layer_norm(v, qw, qb, d0, eps);
+      if (qw) head_layer_norm(v, qw + d0, qb + d0, eps);
       if (rotate) rope16(v, rope_sin + static_cast<int64_t>(pos) * 64, rope_cos + static_cast<int64_t>(pos) * 64, d0);
       store16(q_out + o, v);
     }
     if (k_out) {
       load16(row + C + c0, v);
-      if (kw) head_layer_norm(v, kw, kb, d0, eps);
+      if (kw) head_layer_norm(v, kw + d0, kb + d0, eps);
       if (rotate) rope16(v, rope_sin + static_cast<int64_t>(pos) * 64, rope_cos + static_cast<int64_t>(pos) * 64, d0);
       store16(k_out + o, v);
     }

@@ -287,27 +287,6 @@ __device__ __forceinline__ void v16_store(T* p, const float* v) {
   }
 }
 
-__device__ __forceinline__ void ln64_4lanes(float* v, const float* w, const float* b, int d0,
-                                            float eps) {
-  float s = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 16; ++j) s += v[j];
-  s += __shfl_xor(s, 1);
-  s += __shfl_xor(s, 2);
-  const float mean = s / 64.0f;
-  float q = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const float d = v[j] - mean;
-    q = fmaf(d, d, q);
-  }
-  q += __shfl_xor(q, 1);
-  q += __shfl_xor(q, 2);
-  const float rstd = 1.0f / sqrtf(q / 64.0f + eps);
-#pragma unroll
-  for (int j = 0; j < 16; ++j) v[j] = (v[j] - mean) * rstd * w[d0 + j] + b[d0 + j];
-}
-
 template <typename TI, typename TO>
 __global__ __launch_bounds__(256) void compact16_kernel(
     const TI* __restrict__ x, int64_t xts, int64_t xhs, int64_t x_rows,
@@ -321,6 +300,17 @@ __global__ __launch_bounds__(256) void compact16_kernel(
   if (k >= rows) return;
   const int64_t b = base_rows ? base_rows[k] : -1;
   const float nk = norm ? norm[k] : 1.0f;
+  // This lane's 16 LayerNorm parameters (channel (16 * lane) % 64 onwards, the
+  // same in every 1024-channel chunk), held in registers across the members.
+  float lw[16], lb[16];
+  if (ln_w) {
+    const int d0 = (lane * 16) & 63;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      lw[j] = ln_w[d0 + j];
+      lb[j] = ln_b[d0 + j];
+    }
+  }
   for (int c0 = 0; c0 < dim; c0 += 1024) {
     const int c = c0 + lane * 16;
     const bool active = c < dim;  // whole 4-lane head groups are active together (dim % 64 == 0)
@@ -330,7 +320,7 @@ __global__ __launch_bounds__(256) void compact16_kernel(
     for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
     if (active && b >= 0 && b < x_rows) {
       v16_load(x + b * xts + xoff, acc);
-      if (ln_w) ln64_4lanes(acc, ln_w, ln_b, c & 63, ln_eps);
+      if (ln_w) head_layer_norm(acc, lw, lb, ln_eps);
     }
     for (int sgi = 0; sgi < segs_per_row; ++sgi) {
       const int sb = offsets[k * segs_per_row + sgi], se = offsets[k * segs_per_row + sgi + 1];
@@ -345,7 +335,7 @@ __global__ __launch_bounds__(256) void compact16_kernel(
         const float w = weights ? (static_cast<int>(p) < n_weights ? weights[p] : 0.0f) : 1.0f;
         if (row < 0 || row >= x_rows || !active) continue;
         v16_load(x + row * xts + xoff, v);
-        if (ln_w) ln64_4lanes(v, ln_w, ln_b, c & 63, ln_eps);
+        if (ln_w) head_layer_norm(v, lw, lb, ln_eps);
 #pragma unroll
         for (int j = 0; j < 16; ++j) seg[j] = seg[j] + v[j] * w;
       }

@@ -66,6 +66,42 @@ __device__ __forceinline__ int xcd_remap(int pid, int total) {
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
+// Value held by lane (lane ^ kXor), kXor = 1 or 2, within each group of four
+// lanes: a DPP quad permutation, which stays in the VALU (a ds_bpermute
+// shuffle goes through the LDS unit and waits for it).  The four lanes of a
+// group must be active together.
+template <int kXor>
+__device__ __forceinline__ float quad_xor(float v) {
+  static_assert(kXor == 1 || kXor == 2, "quad_xor: lane ^ 1 or lane ^ 2");
+  constexpr int kCtrl = kXor == 1 ? 0xB1 : 0x4E;  // quad_perm [1,0,3,2] / [2,3,0,1]
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, true));
+}
+
+// LayerNorm over the 64 channels of one head held by four consecutive lanes
+// (16 each, channel d0 + j in v[j]); statistics in fp32, two passes.  w and b
+// point at the affine parameters of this lane's 16 channels.
+__device__ __forceinline__ void head_layer_norm(float* v, const float* w, const float* b,
+                                                float eps) {
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) s += v[j];
+  s += quad_xor<1>(s);
+  s += quad_xor<2>(s);
+  const float mean = s / 64.0f;
+  float q = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const float d = v[j] - mean;
+    q = fmaf(d, d, q);
+  }
+  q += quad_xor<1>(q);
+  q += quad_xor<2>(q);
+  const float rstd = 1.0f / sqrtf(q / 64.0f + eps);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) v[j] = (v[j] - mean) * rstd * w[j] + b[j];
+}
+
 // ------------------------------------------------------------ LDS DMA ----
 // global_load_lds_dword{,x4}: lane i of the wave writes 4 (16) bytes at LDS
 // byte address M0 + 4i (16i).  Issued from inline asm so the compiler does not
