@@ -234,12 +234,14 @@ def residual_layer_norm(x: torch.Tensor, branch: torch.Tensor | None = None,
                         gamma: torch.Tensor | None = None,
                         norm: tuple[torch.Tensor | None, torch.Tensor | None, float] | None = None, *,
                         write_sum: bool = True, norm_dtype: torch.dtype | None = torch.bfloat16,
-                        norm_f32: bool = False):
+                        norm_f32: bool = False, unit_eps: float | None = None):
     """One pass over fp32 rows [..., dim]: s = x + gamma * branch, n = LayerNorm(s).
 
     `norm` = (weight, bias, eps) of the LayerNorm (affine tensors may be None).
-    Returns (s, n, n_f32): s when `write_sum` (and a branch is given), n in
-    `norm_dtype` and its fp32 copy when asked, else None in their places.
+    Returns (s, n, n_f32[, u]): s when `write_sum` (and a branch is given), n in
+    `norm_dtype` and its fp32 copy when asked, else None in their places; with
+    `unit_eps`, also u = n / max(||n||, unit_eps) in `norm_dtype` (the planners'
+    F.normalize front end, equal bit for bit to normalize_rows of n_f32).
     """
     lib = _lib.load()
     _lib.require_gpu(x, branch)
@@ -266,6 +268,11 @@ def residual_layer_norm(x: torch.Tensor, branch: torch.Tensor | None = None,
             normed = torch.empty(x.shape, device=x.device, dtype=norm_dtype)
         if norm_f32:
             normed32 = torch.empty(x.shape, device=x.device, dtype=torch.float32)
+    unit = None
+    if unit_eps is not None:
+        if normed is None:
+            raise ValueError("residual_layer_norm: unit rows need a norm and norm_dtype")
+        unit = torch.empty(x.shape, device=x.device, dtype=normed.dtype)
     if gamma is not None:
         gamma = gamma.detach().to(torch.float32).contiguous()
     status = lib.vgo_residual_layer_norm(
@@ -273,6 +280,8 @@ def residual_layer_norm(x: torch.Tensor, branch: torch.Tensor | None = None,
         _lib.dtype_code(branch.dtype) if branch is not None else _lib.VGO_F32, _c(gamma), _c(w), _c(b),
         float(eps), n, dim, _c(total), dim, _c(normed), dim,
         _lib.dtype_code(normed.dtype) if normed is not None else _lib.VGO_BF16, _c(normed32), dim,
-        _lib.stream_of(x))
+        _c(unit), dim, float(unit_eps or 0.0), _lib.stream_of(x))
     _lib.check(status)
+    if unit_eps is not None:
+        return total, normed, normed32, unit
     return total, normed, normed32

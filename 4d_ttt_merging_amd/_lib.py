@@ -114,7 +114,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "vgo_four_support_projected_gradient": (_c_int, [_c_p, _c_p, _c_i64, _c_int, _c_p, _c_p]),
     "vgo_residual_layer_norm": (_c_int, [
         _c_p, _c_i64, _c_p, _c_i64, _c_int, _c_p, _c_p, _c_p, _c_f32, _c_i64, _c_i64, _c_p, _c_i64,
-        _c_p, _c_i64, _c_int, _c_p, _c_i64, _c_p,
+        _c_p, _c_i64, _c_int, _c_p, _c_i64, _c_p, _c_i64, _c_f32, _c_p,
     ]),
 }
 

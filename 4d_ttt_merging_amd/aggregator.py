@@ -233,7 +233,12 @@ class Aggregator(nn.Module):
                 return tokens.view(batch_size, num_frames, num_tokens, embed_dim)
             layout = dict(frames=num_frames, tokens_per_frame=num_tokens,
                           patch_token_start=self.patch_token_start, patch_hw=patch_hw)
-            normalized, attn_input = block.norm1_for_plan(tokens)
+            unit_rows = None if self.sparse_convex_enabled else block.norm1_unit_rows(tokens)
+            if unit_rows is not None:
+                normalized = None
+                unit_rows, attn_input = unit_rows
+            else:
+                normalized, attn_input = block.norm1_for_plan(tokens)
             with profiling.span("global.plan_build"):
                 if self.sparse_convex_enabled:
                     if self.sparse_convex_qkv_global_layers is not None:
@@ -275,9 +280,10 @@ class Aggregator(nn.Module):
                                                       else plan.original_tokens),
                         **plan.metadata})
                 else:
-                    plan = build_fastvggt_plan(normalized, merge_ratio=self.fastvggt_merge_ratio,
-                                               protect_ratio=self.fastvggt_protect_ratio,
-                                               mass_bias=self.fastvggt_mass_bias, **layout)
+                    plan = build_fastvggt_plan(
+                        normalized if unit_rows is None else unit_rows,
+                        merge_ratio=self.fastvggt_merge_ratio, protect_ratio=self.fastvggt_protect_ratio,
+                        mass_bias=self.fastvggt_mass_bias, prenormalized=unit_rows is not None, **layout)
                     self.fastvggt_last_plan_stats.append({
                         "block_index": block_idx, "original_tokens": plan.original_tokens,
                         "kept_tokens": plan.kept_tokens,

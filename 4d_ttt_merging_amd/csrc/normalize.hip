@@ -10,12 +10,7 @@
 namespace vgo {
 namespace {
 
-template <typename TI>
-__device__ __forceinline__ float load_f32(const TI* p) {
-  return to_f32(*p);
-}
-
-template <typename TI, typename TO>
+template <typename TI, typename TO, bool kVec>
 __global__ __launch_bounds__(256) void normalize_rows_kernel(
     const TI* __restrict__ x, int64_t row_stride, int64_t x_rows, const int64_t* __restrict__ rows,
     int64_t n_rows, int dim, float eps, TO* __restrict__ out, int64_t out_stride) {
@@ -29,33 +24,46 @@ __global__ __launch_bounds__(256) void normalize_rows_kernel(
     return;
   }
   const TI* xr = x + src * row_stride;
-  // Each lane holds up to kMax elements in registers (dim <= 64 * kMax).
-  constexpr int kMax = 32;
-  float v[kMax];
-  float ss = 0.0f;
+  // Lane l holds elements 4(l + 64i) + j (i < kNormChunks, j < 4); the sum of
+  // squares runs over i, then j, then the butterfly -- the order
+  // row_l2_denominator fixes, shared with the fused LayerNorm row pass.
+  float v[kNormChunks][4];
+  const int chunks = dim >> 2;
 #pragma unroll
-  for (int i = 0; i < kMax; ++i) {
-    const int e = i * 64 + lane;
-    v[i] = e < dim ? load_f32(xr + e) : 0.0f;
-    ss = fmaf(v[i], v[i], ss);
+  for (int i = 0; i < kNormChunks; ++i) {
+    const int c = i * 64 + lane;
+    if (kVec && c < chunks) {
+      const f32x4 x4 = load4(xr + 4 * c);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[i][j] = x4[j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[i][j] = c < chunks ? to_f32(xr[4 * c + j]) : 0.0f;
+    }
   }
+  const float denom = row_l2_denominator<kNormChunks>(v, lane, chunks, eps);
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
-  const float denom = fmaxf(sqrtf(ss), eps);
+  for (int i = 0; i < kNormChunks; ++i) {
+    const int c = i * 64 + lane;
+    if (c < chunks) {
 #pragma unroll
-  for (int i = 0; i < kMax; ++i) {
-    const int e = i * 64 + lane;
-    if (e < dim) orow[e] = from_f32<TO>(v[i] / denom);
+      for (int j = 0; j < 4; ++j) orow[4 * c + j] = from_f32<TO>(v[i][j] / denom);
+    }
   }
 }
 
 template <typename TI, typename TO>
 int launch_norm(const void* x, int64_t row_stride, int64_t x_rows, const int64_t* rows,
                 int64_t n_rows, int dim, float eps, void* out, int64_t out_stride, hipStream_t s) {
-  const int64_t blocks = (n_rows + 3) / 4;
-  hipLaunchKernelGGL((normalize_rows_kernel<TI, TO>), dim3(static_cast<unsigned>(blocks)),
-                     dim3(256), 0, s, static_cast<const TI*>(x), row_stride, x_rows, rows, n_rows, dim,
-                     eps, static_cast<TO*>(out), out_stride);
+  const dim3 grid(static_cast<unsigned>((n_rows + 3) / 4));
+  if (aligned(x, 4 * sizeof(TI)) && row_stride % 4 == 0)
+    hipLaunchKernelGGL((normalize_rows_kernel<TI, TO, true>), grid, dim3(256), 0, s,
+                       static_cast<const TI*>(x), row_stride, x_rows, rows, n_rows, dim, eps,
+                       static_cast<TO*>(out), out_stride);
+  else
+    hipLaunchKernelGGL((normalize_rows_kernel<TI, TO, false>), grid, dim3(256), 0, s,
+                       static_cast<const TI*>(x), row_stride, x_rows, rows, n_rows, dim, eps,
+                       static_cast<TO*>(out), out_stride);
   return check_launch("normalize_rows");
 }
 
@@ -69,7 +77,8 @@ extern "C" int vgo_normalize_rows(const void* x, int64_t x_row_stride, int64_t x
   VGO_REQUIRE(n_rows >= 0 && dim >= 0, "normalize_rows: negative size");
   if (n_rows == 0 || dim == 0) return VGO_OK;
   VGO_REQUIRE(x && out, "normalize_rows: null pointer");
-  VGO_REQUIRE(dim <= 64 * 32, "normalize_rows: dim > 2048 is not supported");
+  VGO_REQUIRE(dim <= 4 * 64 * kNormChunks && dim % 4 == 0,
+              "normalize_rows: dim must be a multiple of 4 and at most 2048");
   VGO_REQUIRE(n_rows < (int64_t(1) << 33), "normalize_rows: too many rows");
   hipStream_t s = as_stream(stream);
   const int d = static_cast<int>(dim);

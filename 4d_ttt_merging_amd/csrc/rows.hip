@@ -9,6 +9,10 @@
 // next Linear); here one wave reads a row once and writes the new stream row
 // and its normalised, already-cast copy.
 //
+// Optionally also u = n / max(||n||_2, unit_eps), the F.normalize(...).to(bf16)
+// front end of the merge planners (token_merging.py:1102-1103), from the fp32
+// n in registers, bit-identical to normalize_rows applied to the fp32 n.
+//
 // s is bit-identical to the reference's: the branch element is widened to fp32,
 // multiplied by gamma and added to x with separate IEEE roundings (no fused
 // multiply-add; the library is built with -ffp-contract=off), exactly the two
@@ -29,37 +33,6 @@ namespace {
 // kChunks = 4 (dim <= 1024) and 8 (dim <= 2048), keep the register budget of the
 // common case small.
 constexpr int kRowChunks = 8;
-
-template <typename T>
-struct Vec4;
-template <>
-struct Vec4<float> {
-  using type = f32x4;
-};
-template <>
-struct Vec4<bf16_t> {
-  using type = bf16x4;
-};
-template <>
-struct Vec4<f16_t> {
-  using type = f16x4;
-};
-
-template <typename T>
-__device__ __forceinline__ f32x4 load4(const T* p) {
-  const typename Vec4<T>::type v = *reinterpret_cast<const typename Vec4<T>::type*>(p);
-  return f32x4{to_f32(v[0]), to_f32(v[1]), to_f32(v[2]), to_f32(v[3])};
-}
-
-template <typename T>
-__device__ __forceinline__ void store4(T* p, f32x4 v) {
-  typename Vec4<T>::type o;
-  o[0] = from_f32<T>(v[0]);
-  o[1] = from_f32<T>(v[1]);
-  o[2] = from_f32<T>(v[2]);
-  o[3] = from_f32<T>(v[3]);
-  *reinterpret_cast<typename Vec4<T>::type*>(p) = o;
-}
 
 // Butterfly sum: every lane ends with the same value (each exchange adds the
 // same two operands in either order).
@@ -86,6 +59,9 @@ struct RowArgs {
   int64_t norm_stride;
   float* norm_f32;
   int64_t norm_f32_stride;
+  void* unit;
+  int64_t unit_stride;
+  float unit_eps;
 };
 
 template <int kChunks, bool kBranch, typename TB, typename TN>
@@ -150,7 +126,7 @@ __global__ __launch_bounds__(256) void residual_ln_kernel(RowArgs a) {
     for (int i = 0; i < kChunks; ++i)
       if (live[i]) *reinterpret_cast<f32x4*>(xo + off[i]) = v[i];
   }
-  if (!a.norm && !a.norm_f32) return;
+  if (!a.norm && !a.norm_f32 && !a.unit) return;
 
   const float inv_dim = 1.0f / static_cast<float>(a.dim);
   float s = 0.0f;
@@ -173,10 +149,24 @@ __global__ __launch_bounds__(256) void residual_ln_kernel(RowArgs a) {
     f32x4 n = v[i] * rstd;
     if (a.ln_w) n = n * w[i];
     if (a.ln_b) n = n + bias[i];
+    v[i] = n;
     if (!live[i]) continue;
     if (no) store4(no + off[i], n);
     if (nf) *reinterpret_cast<f32x4*>(nf + off[i]) = n;
   }
+  if (!a.unit) return;
+  // F.normalize of the normalised row, from the same fp32 values and in the
+  // same order as normalize_rows over norm_f32, so the two agree bit for bit.
+  float vv[kChunks][4];
+#pragma unroll
+  for (int i = 0; i < kChunks; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) vv[i][j] = v[i][j];
+  const float denom = row_l2_denominator<kChunks>(vv, lane, chunks, a.unit_eps);
+  TN* uo = static_cast<TN*>(a.unit) + r * a.unit_stride;
+#pragma unroll
+  for (int i = 0; i < kChunks; ++i)
+    if (live[i]) store4(uo + off[i], v[i] / denom);
 }
 
 template <bool kBranch, typename TB, typename TN>
@@ -211,12 +201,14 @@ extern "C" int vgo_residual_layer_norm(const float* x, int64_t x_row_stride, con
                                        const float* ln_bias, float eps, int64_t rows, int64_t dim,
                                        float* x_out, int64_t x_out_row_stride, void* norm_out,
                                        int64_t norm_row_stride, int norm_dtype, float* norm_f32,
-                                       int64_t norm_f32_row_stride, void* stream) {
+                                       int64_t norm_f32_row_stride, void* unit_out,
+                                       int64_t unit_row_stride, float unit_eps, void* stream) {
   using namespace vgo;
   VGO_REQUIRE(rows >= 0 && dim >= 0, "residual_layer_norm: negative size");
   if (rows == 0 || dim == 0) return VGO_OK;
   VGO_REQUIRE(x, "residual_layer_norm: null x");
-  VGO_REQUIRE(x_out || norm_out || norm_f32, "residual_layer_norm: no output");
+  VGO_REQUIRE(x_out || norm_out || norm_f32 || unit_out, "residual_layer_norm: no output");
+  VGO_REQUIRE(!unit_out || norm_out, "residual_layer_norm: unit_out needs norm_out (same dtype)");
   VGO_REQUIRE(branch || !x_out || x_out == x,
               "residual_layer_norm: x_out without a branch must be NULL or x itself");
   VGO_REQUIRE(dim % 4 == 0 && dim <= 4 * 64 * kRowChunks,
@@ -233,14 +225,15 @@ extern "C" int vgo_residual_layer_norm(const float* x, int64_t x_row_stride, con
   VGO_REQUIRE(vec_ok(x, x_row_stride, 4) && vec_ok(x_out, x_out_row_stride, 4) &&
                   vec_ok(norm_f32, norm_f32_row_stride, 4) &&
                   vec_ok(branch, branch_row_stride, dtype_bytes(branch_dtype)) &&
-                  vec_ok(norm_out, norm_row_stride, 2) && vec_ok(gamma, 0, 4) &&
+                  vec_ok(norm_out, norm_row_stride, 2) && vec_ok(unit_out, unit_row_stride, 2) &&
+                  vec_ok(gamma, 0, 4) &&
                   vec_ok(ln_weight, 0, 4) && vec_ok(ln_bias, 0, 4),
               "residual_layer_norm: pointers must be 4-element aligned and row strides multiples of 4");
   VGO_REQUIRE(!x_out || x_out == x || x_out_row_stride != 0,
               "residual_layer_norm: zero x_out row stride");
   RowArgs a{x, x_row_stride, branch, branch_row_stride, gamma, ln_weight, ln_bias, eps, rows,
             static_cast<int>(dim), x_out, x_out_row_stride, norm_out, norm_row_stride, norm_f32,
-            norm_f32_row_stride};
+            norm_f32_row_stride, unit_out, unit_row_stride, unit_eps};
   hipStream_t s = as_stream(stream);
   if (norm_out && norm_dtype == VGO_F16) return dispatch_branch<f16_t>(a, branch_dtype, s);
   return dispatch_branch<bf16_t>(a, branch_dtype, s);

@@ -66,6 +66,61 @@ __device__ __forceinline__ int xcd_remap(int pid, int total) {
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
+// max(||row||_2, eps) of a row held as lane l's elements 4(l + 64i) + j in
+// v[i][j] (chunks past `chunks` ignored): squares summed with fused
+// multiply-adds over i, then j, then a butterfly over the wave, so every lane
+// gets the same value.  normalize_rows and the fused LayerNorm row pass both
+// use this order, so their unit rows agree bit for bit.
+template <int kChunks>
+__device__ __forceinline__ float row_l2_denominator(const float (&v)[kChunks][4], int lane,
+                                                    int chunks, float eps) {
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kChunks; ++i)
+    if (i * 64 + lane < chunks) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) ss = fmaf(v[i][j], v[i][j], ss);
+    }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+  return fmaxf(sqrtf(ss), eps);
+}
+
+constexpr int kNormChunks = 8;  // normalize_rows: dim <= 4 * 64 * 8
+
+// Four consecutive elements as one vector load / store (4-element aligned).
+template <typename T>
+struct Vec4;
+template <>
+struct Vec4<float> {
+  using type = f32x4;
+};
+template <>
+struct Vec4<bf16_t> {
+  using type = bf16x4;
+};
+template <>
+struct Vec4<f16_t> {
+  using type = f16x4;
+};
+
+template <typename T>
+__device__ __forceinline__ f32x4 load4(const T* p) {
+  const typename Vec4<T>::type v = *reinterpret_cast<const typename Vec4<T>::type*>(p);
+  return f32x4{to_f32(v[0]), to_f32(v[1]), to_f32(v[2]), to_f32(v[3])};
+}
+
+template <typename T>
+__device__ __forceinline__ void store4(T* p, f32x4 v) {
+  typename Vec4<T>::type o;
+  o[0] = from_f32<T>(v[0]);
+  o[1] = from_f32<T>(v[1]);
+  o[2] = from_f32<T>(v[2]);
+  o[3] = from_f32<T>(v[3]);
+  *reinterpret_cast<typename Vec4<T>::type*>(p) = o;
+}
+
+
 // Value held by lane (lane ^ kXor), kXor = 1 or 2, within each group of four
 // lanes: a DPP quad permutation, which stays in the VALU (a ds_bpermute
 // shuffle goes through the LDS unit and waits for it).  The four lanes of a

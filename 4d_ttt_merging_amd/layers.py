@@ -424,6 +424,19 @@ class SelfAttentionBlock(nn.Module):
         n = self.norm1(x)
         return n, n
 
+    def norm1_unit_rows(self, x: Tensor, eps: float = 1e-12) -> tuple[Tensor, Tensor] | None:
+        """(F.normalize(norm1(x), eps).to(bf16), norm1(x) in bf16) from one row pass.
+
+        The first tensor is the FastVGGT matcher's input (token_merging.py:1102-1103),
+        equal bit for bit to normalize_rows of the fp32 norm1 rows; the second is the
+        qkv input.  None when the fused row kernel does not apply (or autocast is
+        not bf16); then use `norm1_for_plan`."""
+        if not self._fused_rows(x) or _autocast_dtype() != torch.bfloat16:
+            return None
+        _, h, _, unit = _kernels.residual_layer_norm(x, norm=_ln_args(self.norm1),
+                                                     norm_dtype=torch.bfloat16, unit_eps=eps)
+        return unit, h
+
     # ------------------------------------------------ fused residual rows ----
     def _fused_rows(self, x: Tensor) -> bool:
         """The residual stream runs through vgo_residual_layer_norm: inference under

@@ -444,8 +444,14 @@ def build_fastvggt_plan(
     seed: int = 0,
     match_chunk_size: int = FAST_MATCH_SOURCE_CHUNK,
     mass_bias: bool = False,
+    prenormalized: bool = False,
 ) -> TokenPlan:
     """FastVGGT bipartite plan on Omega's interleaved token layout (reference :1044-1122).
+
+    With `prenormalized=True`, `tokens` already holds the bf16 unit rows
+    `F.normalize(tokens, eps=1e-12).to(bfloat16)` of every token (as the fused
+    norm1 row pass writes them, `SelfAttentionBlock.norm1_unit_rows`), and the
+    matcher reads them directly instead of normalising the rows it gathers.
 
     Sources (non-protected, non-destination patches) are matched against all
     destinations with bf16 cosine scores; the `min(int(total*merge_ratio),
@@ -475,11 +481,17 @@ def build_fastvggt_plan(
 
     best = torch.empty((batch, sources.numel()), device=device, dtype=torch.float32)
     target = torch.empty((batch, sources.numel()), device=device, dtype=torch.int32)
+    if prenormalized and tokens.dtype != torch.bfloat16:
+        raise ValueError("prenormalized FastVGGT tokens must be bf16 unit rows")
     for b in range(batch):
         x = _as_rows(tokens[b])
-        src = _kernels.normalize_rows(x, sources, 1e-12)
-        dst = _kernels.normalize_rows(x, destinations, 1e-12)
-        _kernels.similarity_topk(src, dst, 1, index_dtype=torch.int32,
+        if prenormalized:
+            src, src_rows = x, sources
+            dst = x.index_select(0, destinations)
+        else:
+            src, src_rows = _kernels.normalize_rows(x, sources, 1e-12), None
+            dst = _kernels.normalize_rows(x, destinations, 1e-12)
+        _kernels.similarity_topk(src, dst, 1, src_rows=src_rows, index_dtype=torch.int32,
                                  out=(best[b].view(-1, 1), target[b].view(-1, 1)))
     keep = torch.empty((batch, total - removed), device=device, dtype=torch.int64)
     inverse = torch.empty((batch, total), device=device, dtype=torch.int64)

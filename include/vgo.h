@@ -342,7 +342,10 @@ int vgo_failed_rows(const float* fit, const float* top1, float easy_threshold, i
  *   written to x_out (NULL: not written; may equal x),
  *   LN(s) = (s - mean) / sqrt(var + eps) * ln_weight + ln_bias (either affine
  *   pointer may be NULL), written to norm_out in norm_dtype (bf16 or f16) and/or
- *   to norm_f32 (either may be NULL).
+ *   to norm_f32 (either may be NULL),
+ *   LN(s) / max(||LN(s)||_2, unit_eps), written to unit_out in norm_dtype (NULL:
+ *   not written; needs norm_out), bit-identical to vgo_normalize_rows of the
+ *   fp32 LN(s) rows (the planners' F.normalize front end).
  * s is bit-identical to torch's `x + branch * gamma` in fp32 (branch widened
  * first, separate roundings).  Pointers are 4-element aligned and row strides
  * are multiples of 4 elements.  Replaces the LayerScale multiply, residual add,
@@ -355,7 +358,8 @@ int vgo_residual_layer_norm(const float* x, int64_t x_row_stride, const void* br
                             const float* ln_weight, const float* ln_bias, float eps, int64_t rows,
                             int64_t dim, float* x_out, int64_t x_out_row_stride, void* norm_out,
                             int64_t norm_row_stride, int norm_dtype, float* norm_f32,
-                            int64_t norm_f32_row_stride, void* stream);
+                            int64_t norm_f32_row_stride, void* unit_out, int64_t unit_row_stride,
+                            float unit_eps, void* stream);
 
 #ifdef __cplusplus
 }

@@ -99,12 +99,12 @@ def test_residual_layer_norm_variants(kern, device):
     status = lib.vgo_residual_layer_norm(
         xi.data_ptr(), 1024, bd.data_ptr(), 1024, lib_mod.VGO_BF16, gamma.to(device).data_ptr(),
         None, None, 0.0, 130, 1024, xi.data_ptr(), 1024, None, 0, lib_mod.VGO_BF16, None, 0,
-        torch.cuda.current_stream().cuda_stream)
+        None, 0, 0.0, torch.cuda.current_stream().cuda_stream)
     lib_mod.check(status)
     assert torch.equal(xi.cpu(), x + branch * gamma)
     # Zero rows is a no-op; bad sizes and misaligned rows are rejected on the host.
     lib_mod.check(lib.vgo_residual_layer_norm(None, 0, None, 0, 0, None, None, None, 0.0, 0, 1024, None,
-                                              0, None, 0, 1, None, 0, None))
+                                              0, None, 0, 1, None, 0, None, 0, 0.0, None))
     with pytest.raises(ValueError, match="multiple of 4"):
         kern.residual_layer_norm(xd[:, :1022].contiguous(), norm=(None, None, 1e-5))
     with pytest.raises(ValueError, match="aligned"):
@@ -194,3 +194,36 @@ def test_aggregator_register_rows_in_place_match_concatenation(device):
         model.cached_layer_indices = {0, 1, 2}  # every frame output kept: concatenation
         concatenated = model(images)[0][2]
     assert torch.equal(in_place, concatenated)
+
+
+@pytest.mark.parametrize("rows,dim", [(1029, 1024), (37, 256), (65, 1028)])
+def test_unit_rows_equal_normalize_rows_of_the_fp32_norm(kern, device, rows, dim):
+    """The fused pass's F.normalize output equals normalize_rows over its own fp32
+    LayerNorm rows bit for bit (same values, same reduction order)."""
+    print(f"[rows] unit rows rows={rows} dim={dim}", flush=True)
+    x, _, _, w, b = _inputs(rows, dim, torch.bfloat16, rows + dim)
+    _, n, n32, unit = kern.residual_layer_norm(x.to(device), norm=(w.to(device), b.to(device), 1e-5),
+                                               norm_f32=True, unit_eps=1e-12)
+    assert unit.dtype == torch.bfloat16 and n.dtype == torch.bfloat16
+    assert torch.equal(unit, kern.normalize_rows(n32, None, 1e-12))
+    ref = F.normalize(F.layer_norm(x.double(), (dim,), w.double(), b.double(), 1e-5), dim=-1)
+    _rounded_close(unit, ref, torch.bfloat16, "unit rows")
+
+
+def test_fastvggt_plan_from_fused_unit_rows_is_identical(vgo, device):
+    """norm1_unit_rows + build_fastvggt_plan(prenormalized=True) gives the plan
+    build_fastvggt_plan(norm1_for_plan fp32 rows) gives, bit for bit."""
+    print("[rows] FastVGGT plan from unit rows", flush=True)
+    block = _block(vgo, device, 11)
+    x = structured_tokens(12, 4, (16, 16), 5, 256).to(device)
+    kw = dict(KW, merge_ratio=0.5, protect_ratio=0.0, mass_bias=True)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        unit, attn_input = block.norm1_unit_rows(x)
+        normalized, attn_input2 = block.norm1_for_plan(x)
+    assert torch.equal(attn_input, attn_input2)
+    fused = vgo.build_fastvggt_plan(unit, prenormalized=True, **kw)
+    plain = vgo.build_fastvggt_plan(normalized, **kw)
+    assert torch.equal(fused.keep, plain.keep) and torch.equal(fused.inverse, plain.inverse)
+    assert torch.equal(fused.key_log_mass, plain.key_log_mass)
+    with pytest.raises(ValueError, match="bf16 unit rows"):
+        vgo.build_fastvggt_plan(normalized, prenormalized=True, **kw)
