@@ -227,3 +227,21 @@ def test_fastvggt_plan_from_fused_unit_rows_is_identical(vgo, device):
     assert torch.equal(fused.key_log_mass, plain.key_log_mass)
     with pytest.raises(ValueError, match="bf16 unit rows"):
         vgo.build_fastvggt_plan(normalized, prenormalized=True, **kw)
+
+
+def test_block_forward_fp16_autocast_fused_rows(vgo, device):
+    """fp16 autocast: the rows are cast to fp16, the matcher's unit rows stay with
+    the reference path (they are bf16 by definition), and the block matches the
+    reference op sequence."""
+    print("[rows] block forward fp16 autocast", flush=True)
+    layers = import_package("layers")
+    block = _block(vgo, device, 13)
+    x = structured_tokens(14, 3, (16, 16), 5, 256)[0].view(3, 261, 256).to(device)
+    sin, cos = layers.rope_sincos(16, 16, 64, device=device)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.float16):
+        assert block._fused_rows(x) and block.norm1_unit_rows(x) is None
+        assert block.norm1_for_plan(x)[1].dtype == torch.float16
+        fused = block(x, rope=(sin, cos))
+        _reference_rows(block)
+        ref = block(x, rope=(sin, cos))
+    assert_close(fused.cpu(), ref.cpu(), torch.float16, what="fp16 block forward")
