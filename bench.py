@@ -460,6 +460,47 @@ def only_workload(which: str) -> int:
         print(json.dumps({"workload": "copy", "bytes": n, "launches": 3}), flush=True)
         return 0
     vgo = importlib.import_module("4d_ttt_merging_amd")
+    if which == "projection":
+        # BASELINE config 2, bf16: 1,048,576 rows from a 65,536-row table.
+        n, m, d = 1 << 20, 65536, DIM
+        g = torch.Generator().manual_seed(3)
+        index = (torch.rand(n, 4, generator=g) * m).long().clamp_max(m - 1).int().to(device)
+        e = -torch.rand(n, 4, generator=g, dtype=torch.float64).log()
+        weight = (e / e.sum(1, keepdim=True)).float().to(device)
+        table = torch.randn(m, d, device=device).bfloat16()
+        result = torch.empty(n, d, device=device, dtype=torch.bfloat16)
+        for _ in range(3):
+            vgo.top4_project(table, index, weight, out=result)
+        torch.cuda.synchronize()
+        print(json.dumps({"workload": "projection", "rows": n, "table_rows": m, "dim": d,
+                          "launches": 3}), flush=True)
+        return 0
+    if which == "merge":
+        # The merge side of one C4 global block, three times: norm1 with the
+        # matcher's unit rows, the FastVGGT plan (ratio 0.5, mass bias) and the
+        # q/k/v compaction of a packed qkv projection through it.
+        layers = importlib.import_module("4d_ttt_merging_amd.layers")
+        torch.manual_seed(0)
+        block = layers.SelfAttentionBlock(DIM, HEADS, qkv_bias=True, init_values=0.01,
+                                          mask_k_bias=True, use_qk_norm=True).to(device).eval()
+        n = FRAMES * (SPECIALS + 1024)
+        g = torch.Generator(device=device).manual_seed(6)
+        tokens = torch.randn(1, n, DIM, device=device, generator=g)
+        qkv = torch.randn(n, 3 * DIM, device=device, generator=g).bfloat16()
+        layout = dict(frames=FRAMES, tokens_per_frame=SPECIALS + 1024, patch_token_start=SPECIALS,
+                      patch_hw=GRID, merge_ratio=0.5, protect_ratio=0.0, mass_bias=True)
+        ln = (block.attn.q_norm.weight, block.attn.q_norm.bias, block.attn.q_norm.eps)
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            for _ in range(3):
+                unit, _ = block.norm1_unit_rows(tokens)
+                plan = vgo.build_fastvggt_plan(unit, prenormalized=True, **layout)
+                for i in range(3):
+                    out = torch.empty(HEADS, plan.kept_tokens, 64, device=device, dtype=torch.bfloat16)
+                    plan.compact_into(qkv[:, i * DIM:(i + 1) * DIM], out, layer_norm=ln if i < 2 else None)
+        torch.cuda.synchronize()
+        print(json.dumps({"workload": "merge", "tokens": n, "kept": plan.kept_tokens,
+                          "repeats": 3}), flush=True)
+        return 0
     n = 16464  # C4 compacted tokens
     g = torch.Generator().manual_seed(5)
     q = (torch.randn(1, HEADS, n, 64, generator=g) * 0.125).bfloat16().to(device)
@@ -482,10 +523,12 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-reference", action="store_true")
-    ap.add_argument("--only", choices=("attention", "copy"), default=None,
+    ap.add_argument("--only", choices=("attention", "projection", "merge", "copy"), default=None,
                     help="run one kernel workload for rocprofv3 counter passes, then exit: "
-                         "'attention' = 3 C4-size mass-bias attention launches, 'copy' = 3 "
-                         "plain 256 MiB device copies (the FETCH_SIZE / WRITE_SIZE calibration)")
+                         "'attention' = 3 C4-size mass-bias attention launches, 'projection' = 3 "
+                         "C2 bf16 top-4 projections, 'merge' = 3 x (norm1 unit rows, FastVGGT plan, "
+                         "q/k/v compaction) of a C4 global block, 'copy' = 3 plain 256 MiB device "
+                         "copies (the FETCH_SIZE / WRITE_SIZE calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
