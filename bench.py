@@ -430,6 +430,19 @@ def cpu_baseline(budget_s: float = 30.0):
 
 # ----------------------------------------------------- counter workloads ----
 TRAFFIC_PROFILE = ROOT / "profiles" / "c4_attention_hbm_traffic.md"
+MFMA_PROFILE = ROOT / "profiles" / "c4_attention_mfma_utilisation.md"
+
+
+def attention_mfma_busy() -> float | None:
+    """MFMA-pipe busy fraction of the C4 attention kernel (steady-state launch) from the
+    committed rocprofv3 summary (SQ_VALU_MFMA_BUSY_CYCLES / (active cycles x SIMDs))."""
+    try:
+        for line in MFMA_PROFILE.read_text().splitlines():
+            if line.strip().startswith("mfma_busy_fraction"):
+                return float(line.split("=", 1)[1])
+    except (OSError, ValueError):
+        pass
+    return None
 
 
 def attention_traffic() -> int | None:
@@ -599,7 +612,8 @@ def main() -> int:
                      "achieved": round(attn_flops / (attn_ms / 1e3) / 1e12, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(attn_flops / (attn_ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-                     "traffic": attention_traffic(), "flops_per_launch": attn_flops,
+                     "traffic": attention_traffic(), "mfma_busy": attention_mfma_busy(),
+                     "flops_per_launch": attn_flops,
                      "avg_launch_ms": round(attn_ms, 4)},
         "gemm_selection": "TunableOp table 4d_ttt_merging_amd/tuning/gemm_gfx950.csv" if tuned_gemms
                           else "hipBLASLt default heuristic",
