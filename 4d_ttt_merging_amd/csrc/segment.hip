@@ -328,8 +328,12 @@ __global__ __launch_bounds__(256) void compact16_kernel(
       float seg[16];
 #pragma unroll
       for (int j = 0; j < 16; ++j) seg[j] = 0.0f;
+      // The next member's id is requested before this member's row, so the
+      // two loads overlap instead of forming a chain of round trips.
+      uint32_t p_next = items[sb];
       for (int q = sb; q < se; ++q) {
-        const uint32_t p = items[q];
+        const uint32_t p = p_next;
+        if (q + 1 < se) p_next = items[q + 1];
         const int64_t i = static_cast<int64_t>(p >> item_shift);
         const int64_t row = item_rows ? item_rows[i] : i;
         const float w = weights ? (static_cast<int>(p) < n_weights ? weights[p] : 0.0f) : 1.0f;
