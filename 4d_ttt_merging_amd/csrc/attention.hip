@@ -562,11 +562,16 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attn_reg_kernel(AttnArgs<T> a)
     if (more) stage_load(tile + 1);
     const T* kl = k_lds + buf * kTileElems;
     const T* bl = b_lds + buf * kBiasSlot;
-    f32x16 s[kQB][2];
-    w.scores(kl, bl, s);
-    op8 p[kQB][4];
-    w.softmax(s, kl, bl, p);
-    w.pv(vt_lds + buf * kTileElems, p);
+    // A wave whose 64 queries all lie past n_query (the short last block of a
+    // problem) only stages tiles and meets the barriers; its SIMD is then free
+    // for the other work-group resident on the CU.
+    if (qw0 < a.nq) {
+      f32x16 s[kQB][2];
+      w.scores(kl, bl, s);
+      op8 p[kQB][4];
+      w.softmax(s, kl, bl, p);
+      w.pv(vt_lds + buf * kTileElems, p);
+    }
     if (more) stage_store(tile + 1, buf ^ 1);
     __syncthreads();
   }
