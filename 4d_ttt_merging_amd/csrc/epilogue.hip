@@ -99,22 +99,22 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(
     const int h = c0 >> 6;
     const int d0 = c0 & 63;
     const int64_t o = ((static_cast<int64_t>(seq) * heads + h) * t_out + t) * 64 + d0;
-    float v[16];
+    // The packed row always holds q, k and v, so the three loads are issued
+    // together, whichever outputs are written, and wait once.
+    float vq[16], vk[16], vv[16];
+    load16(row + c0, vq);
+    load16(row + C + c0, vk);
+    load16(row + 2 * C + c0, vv);
+    if (v_out) store16(v_out + o, vv);
     if (q_out) {
-      load16(row + c0, v);
-      if (qw) head_layer_norm(v, qw + d0, qb + d0, eps);
-      if (rotate) rope16(v, rope_sin + static_cast<int64_t>(pos) * 64, rope_cos + static_cast<int64_t>(pos) * 64, d0);
-      store16(q_out + o, v);
+      if (qw) head_layer_norm(vq, qw + d0, qb + d0, eps);
+      if (rotate) rope16(vq, rope_sin + static_cast<int64_t>(pos) * 64, rope_cos + static_cast<int64_t>(pos) * 64, d0);
+      store16(q_out + o, vq);
     }
     if (k_out) {
-      load16(row + C + c0, v);
-      if (kw) head_layer_norm(v, kw + d0, kb + d0, eps);
-      if (rotate) rope16(v, rope_sin + static_cast<int64_t>(pos) * 64, rope_cos + static_cast<int64_t>(pos) * 64, d0);
-      store16(k_out + o, v);
-    }
-    if (v_out) {
-      load16(row + 2 * C + c0, v);
-      store16(v_out + o, v);
+      if (kw) head_layer_norm(vk, kw + d0, kb + d0, eps);
+      if (rotate) rope16(vk, rope_sin + static_cast<int64_t>(pos) * 64, rope_cos + static_cast<int64_t>(pos) * 64, d0);
+      store16(k_out + o, vk);
     }
   }
 }

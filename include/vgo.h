@@ -269,7 +269,8 @@ int vgo_compact(const void* x, int64_t x_token_stride, int64_t x_head_stride, in
  * per-head LayerNorm(64) to q and k (when weights are given) and axial RoPE
  * (when rope_sin/cos are given) to tokens whose position within their
  * tokens_in-long sequence is >= rope_prefix, in fp32, one rounding to
- * out_dtype.  Any of q_out/k_out/v_out may be NULL.  Replaces the reshape,
+ * out_dtype.  Any of q_out/k_out/v_out may be NULL; all 3*heads*64 channels of
+ * every selected row are read whichever outputs are written.  Replaces the reshape,
  * q_norm/k_norm, apply_rope and transposes of
  * vggt_omega/models/layers/attention.py:243-262, 334-341.
  */
