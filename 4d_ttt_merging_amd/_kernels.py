@@ -174,6 +174,49 @@ def compact_into(x: torch.Tensor, out: torch.Tensor, *, base_rows: torch.Tensor 
     return out
 
 
+def compact_multi_into(x: torch.Tensor, outputs, *, base_rows: torch.Tensor | None,
+                       offsets: torch.Tensor, segs_per_row: int, items: torch.Tensor | None,
+                       item_shift: int, item_rows: torch.Tensor | None, weights: torch.Tensor | None,
+                       normalizer: torch.Tensor | None) -> None:
+    """compact_into for 1-3 outputs sharing the segments, in one launch.
+
+    `x` is the [N, W] row table (unit channel stride); `outputs` holds
+    (channel offset, out, layer_norm or None) per output, out being an
+    [K, C] or head-major [H, K, 64] view as in compact_into (all outputs one
+    dtype, that of x; one shared LayerNorm eps)."""
+    lib = _lib.load()
+    _lib.require_gpu(x, *[o[1] for o in outputs])
+    n = len(outputs)
+    first = outputs[0][1]
+    rows = first.shape[0] if first.ndim == 2 else first.shape[1]
+    dim = first.shape[1] if first.ndim == 2 else first.shape[0] * 64
+    keep = []
+    offs = (ctypes.c_int64 * n)(*[int(o[0]) for o in outputs])
+    lw = (ctypes.c_void_p * n)()
+    lb = (ctypes.c_void_p * n)()
+    outs = (ctypes.c_void_p * n)()
+    ots = (ctypes.c_int64 * n)()
+    ohs = (ctypes.c_int64 * n)()
+    eps = 0.0
+    for g, (_, out, ln) in enumerate(outputs):
+        if out.dtype != x.dtype:
+            raise ValueError("compact_multi_into: outputs must have x's dtype")
+        ots[g], ohs[g] = token_layout(out)
+        outs[g] = out.data_ptr()
+        if ln is not None:
+            w = ln[0].detach().to(torch.float32).contiguous()
+            b = ln[1].detach().to(torch.float32).contiguous()
+            keep += [w, b]
+            lw[g], lb[g], eps = w.data_ptr(), b.data_ptr(), float(ln[2])
+    status = lib.vgo_compact_multi(
+        x.data_ptr(), x.stride(0), 64, x.shape[0], _c(base_rows), offsets.data_ptr(), segs_per_row,
+        _c(items), item_shift, _c(item_rows), _c(weights), 0 if weights is None else weights.numel(),
+        _c(normalizer), rows, dim, n, offs, lw, lb, eps, outs, ots, ohs, _lib.dtype_code(x.dtype),
+        _lib.stream_of(x))
+    _lib.check(status)
+    del keep
+
+
 def restore_map(total: int, *, device: torch.device, keep: torch.Tensor | None = None,
                 source: torch.Tensor | None = None, parent: torch.Tensor | None = None,
                 weight: torch.Tensor | None = None,

@@ -98,6 +98,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_int, _c_p, _c_p, _c_i64, _c_p,
         _c_i64, _c_i64, _c_p, _c_p, _c_f32, _c_p, _c_i64, _c_i64, _c_int, _c_int, _c_p,
     ]),
+    "vgo_compact_multi": (_c_int, [
+        _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_int, _c_p, _c_p, _c_i64, _c_p,
+        _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_p, _c_f32, _c_p, _c_p, _c_p, _c_int, _c_p,
+    ]),
     "vgo_qkv_epilogue": (_c_int, [
         _c_p, _c_i64, _c_i64, _c_int, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p,
         _c_p, _c_f32, _c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_int, _c_p,

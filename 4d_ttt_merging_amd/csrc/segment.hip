@@ -287,47 +287,71 @@ __device__ __forceinline__ void v16_store(T* p, const float* v) {
   }
 }
 
-template <typename TI, typename TO>
+// Outputs of one compaction launch that share its segments: output g reads
+// the channels at element offset x_off[g] of every member row, optionally
+// LayerNorms them per head, and writes out[g] with its own strides.
+template <typename TO, int G>
+struct CompactOuts {
+  int64_t x_off[G];
+  const float* ln_w[G];
+  const float* ln_b[G];
+  TO* out[G];
+  int64_t ots[G], ohs[G];
+};
+
+template <typename TI, typename TO, int G>
 __global__ __launch_bounds__(256) void compact16_kernel(
     const TI* __restrict__ x, int64_t xts, int64_t xhs, int64_t x_rows,
     const int64_t* __restrict__ base_rows, const int32_t* __restrict__ offsets, int segs_per_row,
     const uint32_t* __restrict__ items, int item_shift, const int64_t* __restrict__ item_rows,
     const float* __restrict__ weights, int n_weights, const float* __restrict__ norm, int rows,
-    int dim, const float* __restrict__ ln_w, const float* __restrict__ ln_b, float ln_eps,
-    TO* __restrict__ out, int64_t ots, int64_t ohs) {
+    int dim, float ln_eps, CompactOuts<TO, G> o) {
   const int lane = threadIdx.x & 63;
   const int k = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (k >= rows) return;
   const int64_t b = base_rows ? base_rows[k] : -1;
   const float nk = norm ? norm[k] : 1.0f;
-  // This lane's 16 LayerNorm parameters (channel (16 * lane) % 64 onwards, the
-  // same in every 1024-channel chunk), held in registers across the members.
+  const int d0 = (lane * 16) & 63;  // the same in every 1024-channel chunk
+  // One output: this lane's 16 LayerNorm parameters stay in registers across
+  // the members.  Several outputs read theirs from the (cached) vectors.
   float lw[16], lb[16];
-  if (ln_w) {
-    const int d0 = (lane * 16) & 63;
+  if (G == 1 && o.ln_w[0]) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      lw[j] = ln_w[d0 + j];
-      lb[j] = ln_b[d0 + j];
+      lw[j] = o.ln_w[0][d0 + j];
+      lb[j] = o.ln_b[0][d0 + j];
     }
   }
+  auto layer_norm = [&](int g, float* v) {
+    if (!o.ln_w[g]) return;
+    if (G == 1)
+      head_layer_norm(v, lw, lb, ln_eps);
+    else
+      head_layer_norm(v, o.ln_w[g] + d0, o.ln_b[g] + d0, ln_eps);
+  };
   for (int c0 = 0; c0 < dim; c0 += 1024) {
     const int c = c0 + lane * 16;
     const bool active = c < dim;  // whole 4-lane head groups are active together (dim % 64 == 0)
     const int64_t xoff = static_cast<int64_t>(c >> 6) * xhs + (c & 63);
-    float acc[16], v[16];
+    float acc[G][16], v[G][16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[g][j] = 0.0f;
     if (active && b >= 0 && b < x_rows) {
-      v16_load(x + b * xts + xoff, acc);
-      if (ln_w) head_layer_norm(acc, lw, lb, ln_eps);
+#pragma unroll
+      for (int g = 0; g < G; ++g) v16_load(x + b * xts + o.x_off[g] + xoff, acc[g]);
+#pragma unroll
+      for (int g = 0; g < G; ++g) layer_norm(g, acc[g]);
     }
     for (int sgi = 0; sgi < segs_per_row; ++sgi) {
       const int sb = offsets[k * segs_per_row + sgi], se = offsets[k * segs_per_row + sgi + 1];
       if (sb >= se) continue;
-      float seg[16];
+      float seg[G][16];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) seg[j] = 0.0f;
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) seg[g][j] = 0.0f;
       // The next member's id is requested before this member's row, so the
       // two loads overlap instead of forming a chain of round trips.
       uint32_t p_next = items[sb];
@@ -338,18 +362,28 @@ __global__ __launch_bounds__(256) void compact16_kernel(
         const int64_t row = item_rows ? item_rows[i] : i;
         const float w = weights ? (static_cast<int>(p) < n_weights ? weights[p] : 0.0f) : 1.0f;
         if (row < 0 || row >= x_rows || !active) continue;
-        v16_load(x + row * xts + xoff, v);
-        if (ln_w) head_layer_norm(v, lw, lb, ln_eps);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) seg[j] = seg[j] + v[j] * w;
+        for (int g = 0; g < G; ++g) v16_load(x + row * xts + o.x_off[g] + xoff, v[g]);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          layer_norm(g, v[g]);
+#pragma unroll
+          for (int j = 0; j < 16; ++j) seg[g][j] = seg[g][j] + v[g][j] * w;
+        }
       }
 #pragma unroll
-      for (int j = 0; j < 16; ++j) acc[j] = acc[j] + seg[j];
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[g][j] = acc[g][j] + seg[g][j];
     }
     if (active) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) acc[j] = acc[j] / nk;
-      v16_store(out + static_cast<int64_t>(k) * ots + static_cast<int64_t>(c >> 6) * ohs + (c & 63), acc);
+      for (int g = 0; g < G; ++g) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[g][j] = acc[g][j] / nk;
+        v16_store(o.out[g] + static_cast<int64_t>(k) * o.ots[g] + static_cast<int64_t>(c >> 6) * o.ohs[g] + (c & 63),
+                  acc[g]);
+      }
     }
   }
 }
@@ -493,11 +527,15 @@ extern "C" int vgo_compact(const void* x, int64_t x_token_stride, int64_t x_head
                    aligned(x, 16) && aligned(out, 16);
   if (vec) {
 #define VGO_C16(TI, TO)                                                                            \
-  hipLaunchKernelGGL((compact16_kernel<TI, TO>), grid, dim3(256), 0, s, static_cast<const TI*>(x), \
-                     x_token_stride, x_head_stride, x_rows, base_rows, offsets, sp, items,         \
-                     item_shift, item_rows, weights, nw, normalizer, r, d, ln_weight, ln_bias,     \
-                     ln_eps, static_cast<TO*>(out), out_token_stride, out_head_stride);            \
-  return check_launch("compact")
+  {                                                                                                \
+    const CompactOuts<TO, 1> o{{0}, {ln_weight}, {ln_bias}, {static_cast<TO*>(out)},               \
+                               {out_token_stride}, {out_head_stride}};                            \
+    hipLaunchKernelGGL((compact16_kernel<TI, TO, 1>), grid, dim3(256), 0, s,                        \
+                       static_cast<const TI*>(x), x_token_stride, x_head_stride, x_rows, base_rows, \
+                       offsets, sp, items, item_shift, item_rows, weights, nw, normalizer, r, d,    \
+                       ln_eps, o);                                                                 \
+    return check_launch("compact");                                                                \
+  }
     if (in_dtype == VGO_F32 && out_dtype == VGO_F32) { VGO_C16(float, float); }
     if (in_dtype == VGO_BF16 && out_dtype == VGO_BF16) { VGO_C16(bf16_t, bf16_t); }
     if (in_dtype == VGO_F16 && out_dtype == VGO_F16) { VGO_C16(f16_t, f16_t); }
@@ -549,4 +587,101 @@ extern "C" int vgo_restore_map(const int64_t* keep, int64_t n_keep, const int64_
                      keep, static_cast<int>(n_keep), source, parent, weight, static_cast<int>(n_source),
                      inverse, static_cast<int>(total), index_out, weight_out);
   return check_launch("restore_map");
+}
+
+namespace vgo {
+namespace {
+
+template <typename TI, typename TO, int G>
+int launch_compact_multi(const void* x, int64_t xts, int64_t xhs, int64_t x_rows, const int64_t* base_rows,
+                         const int32_t* offsets, int sp, const uint32_t* items, int item_shift,
+                         const int64_t* item_rows, const float* weights, int nw, const float* normalizer,
+                         int rows, int dim, const int64_t* x_offsets, const float* const* ln_weights,
+                         const float* const* ln_biases, float ln_eps, void* const* outs,
+                         const int64_t* ots, const int64_t* ohs, hipStream_t s) {
+  CompactOuts<TO, G> o;
+  for (int g = 0; g < G; ++g) {
+    o.x_off[g] = x_offsets[g];
+    o.ln_w[g] = ln_weights ? ln_weights[g] : nullptr;
+    o.ln_b[g] = ln_biases ? ln_biases[g] : nullptr;
+    o.out[g] = static_cast<TO*>(outs[g]);
+    o.ots[g] = ots[g];
+    o.ohs[g] = ohs[g];
+  }
+  hipLaunchKernelGGL((compact16_kernel<TI, TO, G>), dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0,
+                     s, static_cast<const TI*>(x), xts, xhs, x_rows, base_rows, offsets, sp, items, item_shift,
+                     item_rows, weights, nw, normalizer, rows, dim, ln_eps, o);
+  return check_launch("compact_multi");
+}
+
+template <typename T>
+int dispatch_compact_multi(int n, const void* x, int64_t xts, int64_t xhs, int64_t x_rows,
+                           const int64_t* base_rows, const int32_t* offsets, int sp, const uint32_t* items,
+                           int item_shift, const int64_t* item_rows, const float* weights, int nw,
+                           const float* normalizer, int rows, int dim, const int64_t* x_offsets,
+                           const float* const* lw, const float* const* lb, float eps, void* const* outs,
+                           const int64_t* ots, const int64_t* ohs, hipStream_t s) {
+#define VGO_CM(G)                                                                                      \
+  return launch_compact_multi<T, T, G>(x, xts, xhs, x_rows, base_rows, offsets, sp, items, item_shift,  \
+                                       item_rows, weights, nw, normalizer, rows, dim, x_offsets, lw, lb, \
+                                       eps, outs, ots, ohs, s)
+  switch (n) {
+    case 1: VGO_CM(1);
+    case 2: VGO_CM(2);
+    default: VGO_CM(3);
+  }
+#undef VGO_CM
+}
+
+}  // namespace
+}  // namespace vgo
+
+extern "C" int vgo_compact_multi(const void* x, int64_t x_token_stride, int64_t x_head_stride, int64_t x_rows,
+                                 const int64_t* base_rows, const int32_t* offsets, int64_t segs_per_row,
+                                 const uint32_t* items, int item_shift, const int64_t* item_rows,
+                                 const float* weights, int64_t n_weights, const float* normalizer,
+                                 int64_t rows, int64_t dim, int n_outputs, const int64_t* x_offsets,
+                                 const float* const* ln_weights, const float* const* ln_biases,
+                                 float ln_eps, void* const* outs, const int64_t* out_token_strides,
+                                 const int64_t* out_head_strides, int dtype, void* stream) {
+  VGO_REQUIRE(rows >= 0 && dim >= 0 && segs_per_row >= 1, "compact_multi: bad size");
+  VGO_REQUIRE(n_outputs >= 1 && n_outputs <= 3, "compact_multi: 1 to 3 outputs");
+  if (rows == 0 || dim == 0) return VGO_OK;
+  VGO_REQUIRE(x && offsets && x_offsets && outs && out_token_strides && out_head_strides,
+              "compact_multi: null pointer");
+  VGO_REQUIRE(item_shift >= 0 && item_shift < 8, "compact_multi: bad item shift");
+  VGO_REQUIRE(rows < (1LL << 31) && dim < (1 << 20), "compact_multi: size too large");
+  const int64_t vec = dtype == VGO_F32 ? 4 : 8;
+  bool ok = dim % 64 == 0 && x_token_stride % vec == 0 && x_head_stride % vec == 0 && aligned(x, 16);
+  for (int g = 0; g < n_outputs; ++g) {
+    VGO_REQUIRE(outs[g], "compact_multi: null output");
+    VGO_REQUIRE((ln_weights == nullptr || ln_weights[g] == nullptr) ==
+                    (ln_biases == nullptr || ln_biases[g] == nullptr),
+                "compact_multi: LayerNorm weight and bias go together");
+    ok = ok && x_offsets[g] >= 0 && x_offsets[g] % vec == 0 && out_token_strides[g] % vec == 0 &&
+         out_head_strides[g] % vec == 0 && aligned(outs[g], 16);
+  }
+  VGO_REQUIRE(ok, "compact_multi: needs 64-aligned channels, 16-byte rows and vector-aligned offsets");
+  hipStream_t s = as_stream(stream);
+  const int r = static_cast<int>(rows), d = static_cast<int>(dim), sp = static_cast<int>(segs_per_row);
+  const int nw = static_cast<int>(n_weights);
+  switch (dtype) {
+    case VGO_BF16:
+      return dispatch_compact_multi<bf16_t>(n_outputs, x, x_token_stride, x_head_stride, x_rows, base_rows, offsets,
+                                            sp, items, item_shift, item_rows, weights, nw, normalizer, r, d,
+                                            x_offsets, ln_weights, ln_biases, ln_eps, outs, out_token_strides,
+                                            out_head_strides, s);
+    case VGO_F16:
+      return dispatch_compact_multi<f16_t>(n_outputs, x, x_token_stride, x_head_stride, x_rows, base_rows, offsets,
+                                           sp, items, item_shift, item_rows, weights, nw, normalizer, r, d,
+                                           x_offsets, ln_weights, ln_biases, ln_eps, outs, out_token_strides,
+                                           out_head_strides, s);
+    case VGO_F32:
+      return dispatch_compact_multi<float>(n_outputs, x, x_token_stride, x_head_stride, x_rows, base_rows, offsets,
+                                           sp, items, item_shift, item_rows, weights, nw, normalizer, r, d,
+                                           x_offsets, ln_weights, ln_biases, ln_eps, outs, out_token_strides,
+                                           out_head_strides, s);
+    default:
+      return fail(VGO_EINVAL, "compact_multi: unsupported dtype");
+  }
 }

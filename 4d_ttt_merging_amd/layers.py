@@ -251,6 +251,13 @@ class SelfAttention(nn.Module):
                         plan.compact_query_into(qs, q_c[b], layer_norm=qn)
                         plan.compact_into(ks, k_c[b], layer_norm=kn)
                     plan.compact_into(vs, v_c[b])
+                elif hasattr(plan, "compact_multi_into") and rows.stride(-1) == 1 and k_c.dtype == rows.dtype and (
+                        qn is None or kn is None or qn[2] == kn[2]):
+                    # q, k and v share the plan's clusters: one launch reads each
+                    # member's packed row once for all three.
+                    outputs = [] if preserve_queries else [(0, q_c[b], qn)]
+                    outputs += [(C, k_c[b], kn), (2 * C, v_c[b], None)]
+                    plan.compact_multi_into(rows, outputs, b=b, merge=plan.pool_sources)
                 else:
                     merge = plan.pool_sources
                     if not preserve_queries:

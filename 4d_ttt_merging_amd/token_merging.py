@@ -181,6 +181,21 @@ class TokenPlan:
                                      weights=self._contribution(b), normalizer=counts,
                                      layer_norm=layer_norm)
 
+    def compact_multi_into(self, x: torch.Tensor, outputs, *, b: int = 0, merge: bool = True) -> None:
+        """compact_into of several channel ranges of one [N, W] row table in one launch.
+
+        `outputs` holds (channel offset, out, layer_norm or None) per output, as
+        for q, k and v of a packed qkv projection; results equal compact_into's."""
+        if not merge and self.pool_mask is None:
+            for off, out, ln in outputs:
+                self.compact_into(x[:, off:off + (out.shape[1] if out.ndim == 2 else out.shape[0] * 64)],
+                                  out, b=b, merge=merge, layer_norm=ln)
+            return
+        csr, counts = self._cluster_csr(b)
+        _kernels.compact_multi_into(x, outputs, base_rows=None, offsets=csr.offsets, segs_per_row=1,
+                                    items=csr.order, item_shift=0, item_rows=None,
+                                    weights=self._contribution(b), normalizer=counts)
+
     def restore(self, value: torch.Tensor) -> torch.Tensor:
         if self.kept_tokens == self.original_tokens:
             return value

@@ -263,6 +263,25 @@ int vgo_compact(const void* x, int64_t x_token_stride, int64_t x_head_stride, in
                 void* stream);
 
 /*
+ * vgo_compact for up to three outputs that share one segment structure, in one
+ * launch: output g pools the channels at element offset x_offsets[g] of every
+ * member row (LayerNorm per head with ln_weights[g] / ln_biases[g] when given;
+ * either array may be NULL) into outs[g] with its own token / head strides.
+ * Same arithmetic and order as vgo_compact per output; in and out share
+ * `dtype`; needs the vector layout (dim % 64 == 0, 16-byte aligned rows and
+ * offsets).  Replaces the three compact calls over q, k and v of one plan
+ * (vggt_omega/models/layers/attention.py:346-375).
+ */
+int vgo_compact_multi(const void* x, int64_t x_token_stride, int64_t x_head_stride, int64_t x_rows,
+                      const int64_t* base_rows, const int32_t* offsets, int64_t segs_per_row,
+                      const uint32_t* items, int item_shift, const int64_t* item_rows,
+                      const float* weights, int64_t n_weights, const float* normalizer, int64_t rows,
+                      int64_t dim, int n_outputs, const int64_t* x_offsets,
+                      const float* const* ln_weights, const float* const* ln_biases, float ln_eps,
+                      void* const* outs, const int64_t* out_token_strides,
+                      const int64_t* out_head_strides, int dtype, void* stream);
+
+/*
  * Fused QKV epilogue: from packed projection rows qkv[src] = [q | k | v] (each
  * heads*64 channels), write head-major q/k/v [seq, heads, tokens_out, 64] for
  * output rows r (src = rows ? rows[r] : r; seq = r / tokens_out), applying the

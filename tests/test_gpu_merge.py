@@ -531,3 +531,24 @@ def test_dense_fused_attention_matches_reference_ops(vgo, device):
         layer._fusable = lambda *a: False  # reference op sequence: torch LN, RoPE, SDPA
         general = layer(x, rope=(sin, cos))
     assert_close(fused.float().cpu(), general.float().cpu(), torch.bfloat16, what="frame attention")
+
+
+@pytest.mark.parametrize("merge,n_out", [(True, 3), (True, 2), (False, 3)])
+def test_token_plan_compact_multi_equals_single(vgo, device, merge, n_out):
+    """q/k/v compaction of one plan in one launch (vgo_compact_multi) equals the
+    three single-output launches bit for bit."""
+    print(f"[merge] compact multi merge={merge} outputs={n_out}", flush=True)
+    tokens = structured_tokens(21, 4, (16, 16), 5, 256).to(device)
+    plan = vgo.build_fastvggt_plan(tokens, merge_ratio=0.5, protect_ratio=0.0, mass_bias=True, **KW)
+    g = torch.Generator(device=device).manual_seed(22)
+    qkv = torch.randn(tokens.shape[1], 3 * 256, device=device, generator=g).bfloat16()
+    ln = (1 + 0.1 * torch.randn(64, device=device, generator=g), 0.1 * torch.randn(64, device=device, generator=g), 1e-5)
+    specs = [(0, ln), (256, ln), (512, None)][3 - n_out:]
+    kept = plan.kept_tokens if merge else plan.kept_tokens
+    multi = [torch.empty(4, kept, 64, device=device, dtype=torch.bfloat16) for _ in specs]
+    single = [torch.empty_like(m) for m in multi]
+    plan.compact_multi_into(qkv, [(off, out, norm) for (off, norm), out in zip(specs, multi)], merge=merge)
+    for (off, norm), out in zip(specs, single):
+        plan.compact_into(qkv[:, off:off + 256], out, merge=merge, layer_norm=norm)
+    for a, b in zip(multi, single):
+        assert torch.equal(a, b)
