@@ -187,9 +187,27 @@ def compact_multi_into(x: torch.Tensor, outputs, *, base_rows: torch.Tensor | No
     lib = _lib.load()
     _lib.require_gpu(x, *[o[1] for o in outputs])
     n = len(outputs)
+    if not 1 <= n <= 3:
+        raise ValueError(f"compact_multi_into: 1-3 outputs, got {n}")
+    if x.ndim != 2 or x.stride(1) != 1:
+        raise ValueError("compact_multi_into: x must be an [N, W] row table with unit channel stride")
     first = outputs[0][1]
     rows = first.shape[0] if first.ndim == 2 else first.shape[1]
     dim = first.shape[1] if first.ndim == 2 else first.shape[0] * 64
+    eps_values = set()
+    for off, out, ln in outputs:
+        o_rows = out.shape[0] if out.ndim == 2 else out.shape[1]
+        o_dim = out.shape[1] if out.ndim == 2 else out.shape[0] * 64
+        if (o_rows, o_dim) != (rows, dim):
+            raise ValueError(f"compact_multi_into: every output must be {rows} rows x {dim} "
+                             f"channels, got {o_rows} x {o_dim}")
+        if int(off) < 0 or int(off) + dim > x.shape[1]:
+            raise ValueError(f"compact_multi_into: channels {int(off)}..{int(off) + dim} lie "
+                             f"outside x's {x.shape[1]}")
+        if ln is not None:
+            eps_values.add(float(ln[2]))
+    if len(eps_values) > 1:
+        raise ValueError("compact_multi_into: the outputs' LayerNorms must share one eps")
     keep = []
     offs = (ctypes.c_int64 * n)(*[int(o[0]) for o in outputs])
     lw = (ctypes.c_void_p * n)()

@@ -230,6 +230,14 @@ class Aggregator(nn.Module):
         with profiling.span("global.block"):
             if self.sparse_convex_enabled and global_ordinal in self.sparse_convex_dense_global_layers:
                 tokens = block(tokens, None)
+                # The reference records the bypass too (aggregator.py:885-899).
+                self.sparse_convex_last_plan_stats.append({
+                    "block_index": block_idx, "global_ordinal": global_ordinal,
+                    "original_tokens": int(tokens.shape[1]), "kept_tokens": int(tokens.shape[1]),
+                    "merged_tokens": 0, "merge_ratio": 0.0, "compact_queries": False,
+                    "physical_keys": True, "reused_plan": False,
+                    "attention_query_tokens": int(tokens.shape[1]),
+                    "planner": "dense_layer_bypass"})
                 return tokens.view(batch_size, num_frames, num_tokens, embed_dim)
             layout = dict(frames=num_frames, tokens_per_frame=num_tokens,
                           patch_token_start=self.patch_token_start, patch_hw=patch_hw)

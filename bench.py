@@ -299,18 +299,35 @@ def plan_replay(vgo, device, steps):
             "load_ms": load * 1e3}
 
 
+def c2_inputs(n: int = 1 << 20, m: int = 65536) -> tuple[torch.Tensor, torch.Tensor]:
+    """BASELINE config 2 indices and weights (CPU): per row four distinct uniform ids in
+    [0, m) by Floyd's subset sampling (seed 3) in random order, int32; Dirichlet(1,1,1,1)
+    weights E / sum(E), E = -log U in float64 (seed 4), stored fp32."""
+    g = torch.Generator().manual_seed(3)
+    chosen = torch.empty(n, 4, dtype=torch.int64)
+    for step, j in enumerate(range(m - 4, m)):
+        t = torch.randint(0, j + 1, (n,), generator=g)
+        if step:
+            dup = (chosen[:, :step] == t[:, None]).any(dim=1)
+            t = torch.where(dup, torch.full_like(t, j), t)
+        chosen[:, step] = t
+    order = torch.rand(n, 4, generator=g).argsort(dim=1)
+    index = chosen.gather(1, order).int()
+    gw = torch.Generator().manual_seed(4)
+    e = -torch.rand(n, 4, generator=gw, dtype=torch.float64).log()
+    weight = (e / e.sum(1, keepdim=True)).float()
+    return index, weight
+
+
 def c2_projection(vgo, device, steps):
     """top-4 projection, N=1,048,576 rows from a 65,536-row table."""
     n, m, d = 1 << 20, 65536, 1024
-    g = torch.Generator().manual_seed(3)
-    keys = torch.rand(n, 8, generator=g)
-    index = (keys * m).long().clamp_max(m - 1)
-    index = index[:, :4].int().to(device)  # uniform ids; distinctness is irrelevant to traffic
-    e = -torch.rand(n, 4, generator=g, dtype=torch.float64).log()
-    weight = (e / e.sum(1, keepdim=True)).float().to(device)
+    index, weight = c2_inputs(n, m)
+    index, weight = index.to(device), weight.to(device)
+    gt = torch.Generator(device=device).manual_seed(2)
     out = {}
     for dtype, size in ((torch.bfloat16, 2), (torch.float32, 4)):
-        table = torch.randn(m, d, device=device).to(dtype)
+        table = torch.randn(m, d, device=device, generator=gt).to(dtype)
         result = torch.empty(n, d, device=device, dtype=dtype)
         sec = event_time(lambda: vgo.top4_project(table, index, weight, out=result), steps, 3)
         compulsory = n * d * size + m * d * size + 32 * n
@@ -476,11 +493,9 @@ def only_workload(which: str) -> int:
     if which == "projection":
         # BASELINE config 2, bf16: 1,048,576 rows from a 65,536-row table.
         n, m, d = 1 << 20, 65536, DIM
-        g = torch.Generator().manual_seed(3)
-        index = (torch.rand(n, 4, generator=g) * m).long().clamp_max(m - 1).int().to(device)
-        e = -torch.rand(n, 4, generator=g, dtype=torch.float64).log()
-        weight = (e / e.sum(1, keepdim=True)).float().to(device)
-        table = torch.randn(m, d, device=device).bfloat16()
+        index, weight = c2_inputs(n, m)
+        index, weight = index.to(device), weight.to(device)
+        table = torch.randn(m, d, device=device, generator=torch.Generator(device=device).manual_seed(2)).bfloat16()
         result = torch.empty(n, d, device=device, dtype=torch.bfloat16)
         for _ in range(3):
             vgo.top4_project(table, index, weight, out=result)

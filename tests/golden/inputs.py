@@ -66,5 +66,39 @@ def attention_weights(seed: int, dim: int) -> dict[str, torch.Tensor]:
     }
 
 
+def aggregator_state(seed: int, keys_and_shapes: list[tuple[str, tuple[int, ...]]],
+                     dim: int) -> dict[str, torch.Tensor]:
+    """Seeded values for the aggregator's block parameters and camera/register tokens.
+
+    `keys_and_shapes` lists state-dict entries (names as in the reference's
+    Aggregator: frame_blocks.i.*, inter_frame_blocks.i.*, camera_token,
+    register_token); the values depend only on the seed and each entry's name
+    and shape, so the reference model and this build load identical weights.
+    LayerScale gammas are large (0.2-0.6, not the 1e-5 init) so that every
+    block moves the residual stream and a dropped term shows in the output.
+    """
+    out = {}
+    for key, shape in sorted(keys_and_shapes):
+        g = torch.Generator().manual_seed(seed * 1_000_003 + int(hashlib.sha256(key.encode()).hexdigest()[:8], 16))
+        leaf = key.rsplit(".", 1)[-1]
+        if leaf == "bias_mask":
+            value = torch.ones(shape)
+            value[shape[0] // 3:2 * shape[0] // 3] = 0
+        elif leaf == "gamma":
+            value = 0.2 + 0.4 * torch.rand(shape, generator=g)
+        elif key in ("camera_token", "register_token"):
+            value = torch.randn(shape, generator=g)
+        elif "norm" in key and leaf == "weight":
+            value = 1.0 + 0.1 * torch.randn(shape, generator=g)
+        elif leaf == "bias":
+            value = 0.05 * torch.randn(shape, generator=g)
+        elif leaf == "weight":
+            value = torch.randn(shape, generator=g) * shape[-1] ** -0.5
+        else:
+            raise KeyError(f"aggregator_state: no rule for {key}")
+        out[key] = value
+    return out
+
+
 def sha256(tensor: torch.Tensor) -> str:
     return hashlib.sha256(tensor.detach().cpu().contiguous().numpy().tobytes()).hexdigest()

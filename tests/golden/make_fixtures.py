@@ -9,7 +9,18 @@ the seeded inputs of tests/golden/inputs.py, and stores inputs' sha256 and all
 outputs in tests/golden/fixtures_c1.npz plus a JSON manifest.  Only data is
 stored; nothing of the reference is copied.  The GPU box never runs this.
 
-Usage:  PYTHONDONTWRITEBYTECODE=1 python tests/golden/make_fixtures.py
+A second file, tests/golden/fixtures_agg.npz (+ .json), holds a reduced
+reference Aggregator run (S=4 frames of 16x16 patches + 5 special tokens, dim
+128, 2 heads, depth 3 with one register block, so two merged global blocks),
+fp32 on CPU, from the patch-token cache, with seeded weights
+(tests/golden/inputs.py `aggregator_state`) loaded into the reference model:
+the cached outputs, every plan the global blocks built and the plan stats,
+for the FastVGGT arm and the sparse-convex arm (with and without a dense
+bypass layer).  The reference Aggregator module is loaded by registering
+`vggt_omega` and `vggt_omega.models` as bare package shells, so the package
+__init__ (the whole VGGT-Omega model) never runs.
+
+Usage:  PYTHONDONTWRITEBYTECODE=1 python tests/golden/make_fixtures.py [c1|agg|all]
 """
 from __future__ import annotations
 
@@ -24,7 +35,13 @@ import torch
 
 HERE = Path(__file__).resolve().parent
 sys.path.insert(0, str(HERE.parents[1]))
-from tests.golden.inputs import attention_weights, seeded_values, sha256, structured_tokens  # noqa: E402
+from tests.golden.inputs import (  # noqa: E402
+    aggregator_state,
+    attention_weights,
+    seeded_values,
+    sha256,
+    structured_tokens,
+)
 
 REFERENCE_MODELS = Path("/root/reference/vggt_omega/models")
 PKG = "_reference_models"
@@ -58,6 +75,41 @@ def load_reference():
     return tm, sc, attn
 
 
+class _RecordBf16Products:
+    """Records the bf16 outputs of torch.bmm / Tensor.__matmul__ while active.
+
+    The planners rank the bf16 products they compute (token_merging.py:1106-1111,
+    sparse_convex.py:2402-2404, 2430); recording them keeps the reference's own
+    score matrices, so tests can measure how often a score sits within one bf16
+    ulp of a competitor (the tie band) instead of assuming it never does."""
+
+    def __init__(self):
+        self.products: list[torch.Tensor] = []
+
+    def __enter__(self):
+        self._bmm, self._matmul = torch.bmm, torch.Tensor.__matmul__
+        record = self.products
+
+        def bmm(a, b, *args, **kwargs):
+            out = self._bmm(a, b, *args, **kwargs)
+            if out.dtype == torch.bfloat16:
+                record.append(out.detach().clone())
+            return out
+
+        def matmul(a, b):
+            out = self._matmul(a, b)
+            if out.dtype == torch.bfloat16:
+                record.append(out.detach().clone())
+            return out
+
+        torch.bmm, torch.Tensor.__matmul__ = bmm, matmul
+        return self
+
+    def __exit__(self, *exc):
+        torch.bmm, torch.Tensor.__matmul__ = self._bmm, self._matmul
+        return False
+
+
 def main() -> None:
     tm, sc, attn = load_reference()
     out: dict[str, np.ndarray] = {}
@@ -70,12 +122,19 @@ def main() -> None:
     with torch.no_grad():
         # FastVGGT bipartite plans: the BASELINE ratio-0.5 case and the reference defaults.
         for tag, ratio, protect in (("fv50", 0.5, 0.0), ("fvdef", 0.9, 0.10)):
-            plan = tm.build_fastvggt_plan(tokens, merge_ratio=ratio, protect_ratio=protect, **kw)
+            with _RecordBf16Products() as rec:
+                plan = tm.build_fastvggt_plan(tokens, merge_ratio=ratio, protect_ratio=protect, **kw)
             out[f"{tag}_keep"] = plan.keep[0].numpy()
             out[f"{tag}_inverse"] = plan.inverse[0].numpy()
+            # the reference's bf16 score matrix [sources, destinations] (one chunk at C1)
+            out[f"{tag}_scores"] = torch.cat([p[0] for p in rec.products]).view(torch.int16).numpy()
 
         # Sparse-convex fixed-topology plan.
-        plan = sc.build_sparse_convex_plan(tokens, threshold=0.90, **kw)
+        with _RecordBf16Products() as rec:
+            plan = sc.build_sparse_convex_plan(tokens, threshold=0.90, **kw)
+        # local-group scores [576 candidates, 448 dictionary] and the global fallback's
+        out["sc_local_scores"] = rec.products[0].view(torch.int16).numpy()
+        out["sc_fallback_scores"] = torch.cat(rec.products[1:]).view(torch.int16).numpy()
         out["sc_keep"] = plan.keep[0].numpy()
         out["sc_source"] = plan.source_original[0].numpy()
         out["sc_parent"] = plan.source_parent_compact[0].numpy()
@@ -118,5 +177,120 @@ def main() -> None:
     print(f"wrote {len(out)} arrays")
 
 
+# Reduced aggregator: S=4 frames x (5 specials + 16x16 patches), dim 128, 2 heads of 64,
+# depth 3 with a register block at index 1 -> merged global blocks at 0 and 2.
+AGG = dict(embed_dim=128, depth=3, num_heads=2, num_register_tokens=4,
+           register_attention_block_indices=[1], cached_layer_indices=(0, 2))
+AGG_WEIGHT_SEED = 17
+AGG_PATCH_SEED = 18
+
+
+def load_reference_aggregator():
+    """vggt_omega.models.aggregator without running the package __init__ files."""
+    sys.dont_write_bytecode = True
+    root = REFERENCE_MODELS.parent
+    for name, path in (("vggt_omega", root), ("vggt_omega.models", REFERENCE_MODELS)):
+        if name not in sys.modules:
+            shell = types.ModuleType(name)
+            shell.__path__ = [str(path)]
+            sys.modules[name] = shell
+    import importlib
+    return importlib.import_module("vggt_omega.models.aggregator")
+
+
+def aggregator_inputs(dim: int):
+    """Patch-token cache [frames, 256, dim] (the patches of structured tokens)."""
+    tokens = structured_tokens(AGG_PATCH_SEED, FRAMES, HW, SPECIALS, dim)[0]
+    return tokens.view(FRAMES, TPF, dim)[:, SPECIALS:].contiguous()
+
+
+def aggregator_fixture() -> None:
+    agg_mod = load_reference_aggregator()
+    torch.manual_seed(0)
+    model = agg_mod.Aggregator(**AGG).eval()
+    names = [(k, tuple(v.shape)) for k, v in model.state_dict().items()
+             if k.startswith(("frame_blocks.", "inter_frame_blocks.", "camera_token", "register_token"))]
+    state = aggregator_state(AGG_WEIGHT_SEED, names, AGG["embed_dim"])
+    missing, unexpected = model.load_state_dict(state, strict=False)
+    assert not unexpected and all(not m.startswith(("frame_blocks", "inter_frame_blocks")) for m in missing)
+    patches = aggregator_inputs(AGG["embed_dim"])
+    images = torch.zeros(1, FRAMES, 3, HW[0] * 16, HW[1] * 16)
+    model.set_input_patch_tokens_cache(patches)
+
+    # Record every plan the global blocks build (the builders are module globals).
+    built = []
+    originals = (agg_mod.build_fastvggt_plan, agg_mod.build_sparse_convex_plan)
+
+    def recording(builder):
+        def wrapped(*args, **kwargs):
+            with _RecordBf16Products() as rec:
+                plan = builder(*args, **kwargs)
+            built.append((plan, rec.products))
+            return plan
+        return wrapped
+
+    agg_mod.build_fastvggt_plan = recording(originals[0])
+    agg_mod.build_sparse_convex_plan = recording(originals[1])
+    out: dict[str, np.ndarray] = {}
+    manifest: dict[str, object] = {
+        "config": dict(AGG, frames=FRAMES, patch_hw=HW, weight_seed=AGG_WEIGHT_SEED,
+                       patch_seed=AGG_PATCH_SEED),
+        "patches_sha256": sha256(patches),
+        "state_sha256": sha256(torch.cat([state[k].flatten() for k in sorted(state)])),
+        "state_keys": [[k, list(shape)] for k, shape in names],
+    }
+    runs = {
+        "fv": lambda: model.set_fastvggt(True, merge_ratio=0.5, protect_ratio=0.0),
+        "sc": lambda: model.set_sparse_convex(True, threshold=0.9, qkv_global_layers=(0,),
+                                              qkv_global_blocks=1),
+        "scd": lambda: model.set_sparse_convex(True, threshold=0.9, qkv_global_layers=(0,),
+                                               qkv_global_blocks=1, dense_global_layers=(1,)),
+    }
+    try:
+        for tag, configure in runs.items():
+            model.set_fastvggt(False)
+            model.set_sparse_convex(False, qkv_global_blocks=0, qkv_global_layers=())
+            configure()
+            built.clear()
+            with torch.no_grad():
+                outputs, start = model(images)
+            assert start == SPECIALS
+            # the last cached output (frame and global tokens of block 2) depends on every block
+            last = max(AGG["cached_layer_indices"])
+            out[f"{tag}_out{last}"] = outputs[last].numpy()
+            stats = model.fastvggt_last_plan_stats if tag == "fv" else model.sparse_convex_last_plan_stats
+            manifest[f"{tag}_stats"] = stats
+            for i, (plan, products) in enumerate(built):
+                out[f"{tag}_plan{i}_keep"] = plan.keep[0].numpy()
+                if tag == "fv":
+                    out[f"{tag}_plan{i}_inverse"] = plan.inverse[0].numpy()
+                else:
+                    if tag == "sc":
+                        # The planner's bf16 scores, so tests can tell a top-4 tie from a
+                        # different support choice.  At this layout the single local group's
+                        # dictionary is the global one, and every global-fallback row equals
+                        # its candidate's local row, so the local matrix covers both.
+                        local = products[0]
+                        rows = {bytes(r.view(torch.int16).numpy()) for r in local}
+                        assert all(bytes(r.view(torch.int16).numpy()) in rows for r in torch.cat(products[1:]))
+                        out[f"{tag}_plan{i}_local_scores"] = local.view(torch.int16).numpy()
+                    out[f"{tag}_plan{i}_source"] = plan.source_original[0].numpy()
+                    out[f"{tag}_plan{i}_parent"] = plan.source_parent_compact[0].numpy()
+                    out[f"{tag}_plan{i}_weight"] = plan.source_pool_weights[0].numpy()
+                    out[f"{tag}_plan{i}_mass"] = plan.normalizer[0, :, 0].numpy()
+                    out[f"{tag}_plan{i}_special_compact"] = plan.special_query_compact.numpy()
+            manifest[f"{tag}_plans"] = len(built)
+    finally:
+        agg_mod.build_fastvggt_plan, agg_mod.build_sparse_convex_plan = originals
+    np.savez_compressed(HERE / "fixtures_agg.npz", **out)
+    manifest["arrays"] = {k: [list(v.shape), str(v.dtype)] for k, v in out.items()}
+    (HERE / "fixtures_agg.json").write_text(json.dumps(manifest, indent=1, default=str) + "\n")
+    print(f"wrote {len(out)} aggregator arrays")
+
+
 if __name__ == "__main__":
-    main()
+    which = sys.argv[1] if len(sys.argv) > 1 else "all"
+    if which in ("c1", "all"):
+        main()
+    if which in ("agg", "all"):
+        aggregator_fixture()

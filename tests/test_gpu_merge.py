@@ -210,23 +210,68 @@ def test_fastvggt_assemble_exact(vgo, kern, device, batch, ns, nd, removed, keys
 
 # --------------------------------------------------------- FastVGGT plan ----
 @pytest.mark.parametrize("tag,ratio,protect", [("fv50", 0.5, 0.0), ("fvdef", 0.9, 0.10)])
-def test_fastvggt_plan_vs_reference(vgo, device, fx, tag, ratio, protect):
+def test_fastvggt_plan_vs_reference(vgo, kern, device, fx, tag, ratio, protect):
+    """The GPU plan against the reference's own plan, unconditionally.
+
+    keep/inverse must equal the reference fixture, except where a source lies in
+    the tie band of the scores: the kernel's bf16 scores and the reference's
+    recorded bf16 scores each lie within one ulp of the exact dot product, so
+    they may differ by up to two; a source whose best score is that close to
+    the removal cutoff may swap removal status, and a source whose best and
+    another destination's score are that close may swap target.  Every
+    difference must be explained that way; the fractions are printed."""
     tokens = structured_tokens(1, 4, (16, 16), 5, 1024)
     plan = vgo.build_fastvggt_plan(tokens.to(device), merge_ratio=ratio, protect_ratio=protect, **KW)
     sources, dests, best, target, _ = plan._derived["match"]
+    total, removed = 1044, plan.original_tokens - plan.kept_tokens
     # selection is exact given the kernel's scores
     rk, ri = om.fastvggt_select(best[0].cpu(), target[0].cpu().long(), sources.cpu(), dests.cpu(),
-                                1044, plan.original_tokens - plan.kept_tokens)
+                                total, removed)
     assert torch.equal(plan.keep[0].cpu(), rk) and torch.equal(plan.inverse[0].cpu(), ri)
-    # and the kernel's match agrees with the oracle's exact-score match
-    o = om.fastvggt_plan(tokens, merge_ratio=ratio, protect_ratio=protect, **KW)
-    assert (best[0].cpu() - o["best"]).abs().max() <= float(ulp_bf16(o["best"]).max())
-    agree = best[0].cpu() == o["best"]
-    assert torch.equal(target[0].cpu().long()[agree], o["targets"][agree])
-    # end to end against the reference's own plan
-    if agree.all():
-        assert np.array_equal(plan.keep[0].cpu().numpy(), fx[f"{tag}_keep"])
-        assert np.array_equal(plan.inverse[0].cpu().numpy(), fx[f"{tag}_inverse"])
+    # the kernel's full score matrix on the planner's operands
+    x = tokens[0].to(device)
+    src = kern.normalize_rows(x, sources, 1e-12)
+    dst = kern.normalize_rows(x, dests, 1e-12)
+    scores = torch.full((sources.numel(), dests.numel()), float("nan"), dtype=torch.bfloat16, device=device)
+    kern.similarity_topk(src, dst, 1, scores=scores)
+    ks = scores.float().cpu()
+    assert torch.equal(ks.max(1).values, best[0].cpu())
+    ref = torch.from_numpy(fx[f"{tag}_scores"]).view(torch.bfloat16).float()
+    mismatch = ks != ref
+    assert ((ks - ref).abs()[mismatch] <= 2 * score_tolerance(ref)[mismatch]).all()
+    # the oracle's selection on the reference's own scores is the reference's plan
+    ref_best, ref_target = ref.max(1)
+    ok_keep, ok_inv = om.fastvggt_select(ref_best, ref_target, sources.cpu(), dests.cpu(), total, removed)
+    assert np.array_equal(ok_keep.numpy(), fx[f"{tag}_keep"])
+    assert np.array_equal(ok_inv.numpy(), fx[f"{tag}_inverse"])
+    # GPU plan vs the reference's, source by source
+    src_cpu, dst_cpu = sources.cpu(), dests.cpu()
+    fx_keep = torch.from_numpy(fx[f"{tag}_keep"])
+    fx_inv = torch.from_numpy(fx[f"{tag}_inverse"])
+    removed_gpu = ~torch.isin(src_cpu, plan.keep[0].cpu())
+    removed_ref = ~torch.isin(src_cpu, fx_keep)
+    kbest = best[0].cpu()
+    cutoff = kbest.sort(descending=True).values[removed - 1]
+    rank_band = (kbest - cutoff).abs() <= 2 * score_tolerance(cutoff.expand_as(kbest))
+    top2 = ks.topk(2, dim=1).values
+    target_band = (top2[:, 0] - top2[:, 1]) <= 2 * score_tolerance(top2[:, 0])
+    status_diff = removed_gpu != removed_ref
+    assert rank_band[status_diff].all(), "a removal difference outside the tie band"
+    both = removed_gpu & removed_ref
+    gpu_target = plan.keep[0].cpu()[plan.inverse[0].cpu()[src_cpu]]
+    ref_target_orig = fx_keep[fx_inv[src_cpu]]
+    target_diff = both & (gpu_target != ref_target_orig)
+    if target_diff.any():
+        col = {int(d): j for j, d in enumerate(dst_cpu.tolist())}
+        for i in target_diff.nonzero().flatten().tolist():
+            other = ks[i, col[int(ref_target_orig[i])]]
+            assert ks[i].max() - other <= 2 * score_tolerance(ks[i].max()), "target difference outside the tie band"
+    if not (status_diff.any() or target_diff.any()):
+        assert torch.equal(plan.keep[0].cpu(), fx_keep) and torch.equal(plan.inverse[0].cpu(), fx_inv)
+    print(f"[fastvggt vs reference] {tag}: scores differ in {mismatch.float().mean().item():.2e} of "
+          f"entries (<= 2 ulp); tie band: {target_band.float().mean().item():.3f} of sources (target), "
+          f"{rank_band.float().mean().item():.3f} (cutoff); plan differences: "
+          f"{int(status_diff.sum())} removal, {int(target_diff.sum())} target", flush=True)
 
 
 def test_fastvggt_plan_batch_and_determinism(vgo, device):
@@ -533,22 +578,55 @@ def test_dense_fused_attention_matches_reference_ops(vgo, device):
     assert_close(fused.float().cpu(), general.float().cpu(), torch.bfloat16, what="frame attention")
 
 
-@pytest.mark.parametrize("merge,n_out", [(True, 3), (True, 2), (False, 3)])
-def test_token_plan_compact_multi_equals_single(vgo, device, merge, n_out):
+@pytest.mark.parametrize("case,n_out", [("fastvggt", 3), ("fastvggt", 2), ("pool_mask", 1), ("pool_mask", 3)])
+def test_token_plan_compact_multi_equals_single(vgo, device, case, n_out):
     """q/k/v compaction of one plan in one launch (vgo_compact_multi) equals the
-    three single-output launches bit for bit."""
-    print(f"[merge] compact multi merge={merge} outputs={n_out}", flush=True)
+    single-output launches bit for bit.  `pool_mask` plans (reference
+    token_merging.py:161-191: only masked members contribute) take the same CSR
+    path with 0/1 member weights."""
+    print(f"[merge] compact multi {case} outputs={n_out}", flush=True)
     tokens = structured_tokens(21, 4, (16, 16), 5, 256).to(device)
     plan = vgo.build_fastvggt_plan(tokens, merge_ratio=0.5, protect_ratio=0.0, mass_bias=True, **KW)
+    if case == "pool_mask":
+        g = torch.Generator().manual_seed(23)
+        mask = torch.rand(1, plan.original_tokens, generator=g) < 0.6
+        mask[0, plan.keep[0].cpu()] = True  # every cluster keeps its physical member
+        plan = vgo.TokenPlan(plan.keep, plan.inverse, plan.original_tokens, pool_mask=mask.to(device))
     g = torch.Generator(device=device).manual_seed(22)
     qkv = torch.randn(tokens.shape[1], 3 * 256, device=device, generator=g).bfloat16()
     ln = (1 + 0.1 * torch.randn(64, device=device, generator=g), 0.1 * torch.randn(64, device=device, generator=g), 1e-5)
     specs = [(0, ln), (256, ln), (512, None)][3 - n_out:]
-    kept = plan.kept_tokens if merge else plan.kept_tokens
+    kept = plan.kept_tokens
     multi = [torch.empty(4, kept, 64, device=device, dtype=torch.bfloat16) for _ in specs]
     single = [torch.empty_like(m) for m in multi]
-    plan.compact_multi_into(qkv, [(off, out, norm) for (off, norm), out in zip(specs, multi)], merge=merge)
+    plan.compact_multi_into(qkv, [(off, out, norm) for (off, norm), out in zip(specs, multi)])
     for (off, norm), out in zip(specs, single):
-        plan.compact_into(qkv[:, off:off + 256], out, merge=merge, layer_norm=norm)
+        plan.compact_into(qkv[:, off:off + 256], out, layer_norm=norm)
     for a, b in zip(multi, single):
         assert torch.equal(a, b)
+    if case == "pool_mask":
+        # the masked mean in float64 (one bf16 rounding of the fp32 result)
+        x = qkv[:, 512:].float().cpu().double()
+        inv, m = plan.inverse[0].cpu(), plan.pool_mask[0].cpu().double()
+        sums = torch.zeros(kept, 256, dtype=torch.float64).index_add_(0, inv, x * m[:, None])
+        counts = torch.zeros(kept, dtype=torch.float64).index_add_(0, inv, m)
+        ref = sums / counts[:, None]
+        got = multi[-1].transpose(0, 1).reshape(kept, 256).double().cpu()
+        assert_close(got, ref, torch.bfloat16, rtol=8e-3, what="pool_mask compaction")
+
+
+def test_compact_multi_rejects_mismatched_outputs(vgo, device):
+    tokens = structured_tokens(21, 4, (16, 16), 5, 256).to(device)
+    plan = vgo.build_fastvggt_plan(tokens, merge_ratio=0.5, protect_ratio=0.0, **KW)
+    qkv = torch.zeros(tokens.shape[1], 3 * 256, device=device, dtype=torch.bfloat16)
+    kept = plan.kept_tokens
+    a = torch.empty(4, kept, 64, device=device, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="every output"):
+        plan.compact_multi_into(qkv, [(0, a, None), (256, torch.empty(2, kept, 64, device=device,
+                                                                      dtype=torch.bfloat16), None)])
+    with pytest.raises(ValueError, match="outside"):
+        plan.compact_multi_into(qkv, [(600, a, None)])
+    ln1 = (torch.ones(64, device=device), torch.zeros(64, device=device), 1e-5)
+    ln2 = (torch.ones(64, device=device), torch.zeros(64, device=device), 1e-6)
+    with pytest.raises(ValueError, match="eps"):
+        plan.compact_multi_into(qkv, [(0, a, ln1), (256, torch.empty_like(a), ln2)])

@@ -169,3 +169,38 @@ def test_checks_have_teeth(fx):
     small = seeded_values(8, (1, keep.numel(), 32), torch.float32)[0]
     bad = om.weighted_restore(keep, src, parent.flip(1), w, 1044, small)
     assert not torch.equal(bad, torch.from_numpy(fx["sc_restore_f32"]))
+
+
+def _ulp_bf16(x: torch.Tensor) -> torch.Tensor:
+    e = torch.frexp(x.abs().clamp_min(1e-30))[1]
+    return torch.ldexp(torch.ones_like(x), e - 8)
+
+
+@pytest.mark.parametrize("tag", ["fv50", "sc_local"])
+def test_reference_score_matrices_within_one_ulp_of_exact(fx, tokens, tag):
+    """The reference's own bf16 score matrices (recorded from its bmm / matmul,
+    token_merging.py:1106-1111, sparse_convex.py:2402-2404) against the oracle's
+    rule (exact dot product of the bf16 operands, rounded once to bf16): every
+    entry within one bf16 ulp, and the fraction that differs is reported.  The
+    tie band -- sources whose two best scores lie within one ulp, so a rounding
+    difference can move their argmax -- is reported as well."""
+    ref = torch.from_numpy(fx[f"{tag}_scores"]).view(torch.bfloat16).float()
+    x = tokens[0]
+    if tag == "fv50":
+        o = om.fastvggt_plan(tokens, merge_ratio=0.5, protect_ratio=0.0, **KW)
+        src = torch.nn.functional.normalize(x[o["sources"]], dim=-1).bfloat16()
+        dst = torch.nn.functional.normalize(x[o["destinations"]], dim=-1).bfloat16()
+    else:
+        layout = om.sparse_convex_layout(x.shape[0], 4, 261, 5, (16, 16))
+        normalized = torch.nn.functional.normalize(x, dim=-1, eps=1e-6)
+        src = normalized[layout["candidate"]].bfloat16()
+        dst = normalized[layout["destination"]].bfloat16()
+    exact = om.bf16_scores(src, dst)
+    assert exact.shape == ref.shape
+    mismatch = exact != ref
+    assert ((exact - ref).abs()[mismatch] <= 1.01 * _ulp_bf16(exact)[mismatch]).all()
+    top2 = ref.topk(2, dim=1).values
+    band = (top2[:, 0] - top2[:, 1]) <= 1.01 * _ulp_bf16(top2[:, 0])
+    print(f"[scores] {tag}: {mismatch.float().mean().item():.2e} of entries differ from the exact-dot "
+          f"rounding (max one ulp); tie band {band.float().mean().item():.3f} of rows")
+    assert mismatch.float().mean() < 5e-3
