@@ -58,6 +58,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
         _i64x3, _i64x3, _i64x3, _i64x3, _c_int, _c_p, _c_size, _c_p,
     ]),
+    "vgo_mass_bias_attn_fwd_static": (_c_int, [
+        _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+        _i64x3, _i64x3, _i64x3, _i64x3, _c_int, _c_p,
+    ]),
     "vgo_mass_bias_attn_pair_workspace": (_c_int, [
         ctypes.POINTER(AttnProblem), _c_int, _c_int, ctypes.POINTER(_c_size),
     ]),

@@ -39,6 +39,7 @@
 //    attn_merge_kernel from fp32 partial states.
 // fp32 path: exact fp32 arithmetic, one query row per lane, K/V tiles in LDS.
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "vgo_common.h"
@@ -1344,6 +1345,37 @@ Problem from_c(const vgo_attn_problem& p) {
                  p.q_stride, p.k_stride, p.v_stride, p.o_stride};
 }
 
+// Scratch of vgo_mass_bias_attn_fwd_static: every GPU the library runs on holds
+// one copy until the process ends.  VGO_ATTN_STATIC_SCRATCH_BYTES covers the
+// workspace of every BASELINE configuration on a 256-CU MI355X (C5: 108.5 MB of
+// V^T + 69 MB of partial states).  Host code never passes the array's name to a
+// kernel (on the host it is a stand-in, not a device address); it uses the
+// per-device address from hipGetSymbolAddress below.
+__device__ __align__(256) unsigned char scratch[VGO_ATTN_STATIC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's scratch, looked up once per device.
+int static_scratch(void** out) {
+  using namespace vgo;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(VGO_ELAUNCH, "mass_bias_attention(static): no current device");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || ptr == nullptr)
+      return fail(VGO_ELAUNCH, std::string("mass_bias_attention(static): hipGetSymbolAddress: ") +
+                                   hipGetErrorString(err));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return VGO_OK;
+}
+
 }  // namespace
 
 extern "C" int vgo_mass_bias_attn_fwd(const void* q, const void* k, const void* v,
@@ -1374,6 +1406,32 @@ extern "C" int vgo_mass_bias_attn_fwd_ws(const void* q, const void* k, const voi
   const Problem p = single_problem(q, k, v, log_mass, out, batch, heads, n_query, n_key, q_stride,
                                    k_stride, v_stride, o_stride);
   return attn_run(&p, &head_dim, 1, dtype, workspace, workspace_bytes, true, stream);
+}
+
+extern "C" int vgo_mass_bias_attn_fwd_static(const void* q, const void* k, const void* v,
+                                             const void* log_mass, void* out, int64_t batch,
+                                             int64_t heads, int64_t n_query, int64_t n_key,
+                                             int64_t head_dim, const int64_t q_stride[3],
+                                             const int64_t k_stride[3], const int64_t v_stride[3],
+                                             const int64_t o_stride[3], int dtype, void* stream) {
+  using namespace vgo;
+  const Problem p = single_problem(q, k, v, log_mass, out, batch, heads, n_query, n_key, q_stride,
+                                   k_stride, v_stride, o_stride);
+  size_t need = 0;
+  const int status = attn_workspace_bytes(&p, 1, dtype, &need);
+  if (status != VGO_OK) return status;
+  if (need > VGO_ATTN_STATIC_SCRATCH_BYTES)
+    return fail(VGO_EWORKSPACE,
+                "mass_bias_attention(static): the problem needs " + std::to_string(need) +
+                    " bytes of scratch, more than the static " +
+                    std::to_string(static_cast<size_t>(VGO_ATTN_STATIC_SCRATCH_BYTES)) +
+                    "; use vgo_mass_bias_attn_fwd_ws with a workspace");
+  void* ptr = nullptr;
+  if (need > 0) {
+    const int found = static_scratch(&ptr);
+    if (found != VGO_OK) return found;
+  }
+  return attn_run(&p, &head_dim, 1, dtype, ptr, VGO_ATTN_STATIC_SCRATCH_BYTES, true, stream);
 }
 
 extern "C" int vgo_mass_bias_attn_pair_workspace(const vgo_attn_problem* problems, int count,

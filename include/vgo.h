@@ -1,10 +1,11 @@
 /*
  * vgo.h — C ABI of the MI355X (gfx950) merged-token global-attention library.
  *
- * Every entry point is stateless and re-entrant: device pointers in, device
- * pointers out, launches only on the stream passed in (`void*` is a
- * hipStream_t; NULL is the null stream), no host synchronisation and no device
- * allocation inside.  Callers own every buffer, including workspaces whose size
+ * Every entry point is stateless and re-entrant (except
+ * vgo_mass_bias_attn_fwd_static, which uses a static device scratch): device
+ * pointers in, device pointers out, launches only on the stream passed in
+ * (`void*` is a hipStream_t; NULL is the null stream), no host synchronisation
+ * and no device allocation inside.  Callers own every buffer, including workspaces whose size
  * is reported by the matching `*_workspace_bytes` query.
  *
  * Return value: VGO_OK (0) or a negative status.  `vgo_last_error()` returns a
@@ -83,6 +84,28 @@ int vgo_mass_bias_attn_fwd_ws(const void* q, const void* k, const void* v, const
                               const int64_t k_stride[3], const int64_t v_stride[3],
                               const int64_t o_stride[3], int dtype, void* workspace,
                               size_t workspace_bytes, void* stream);
+
+/*
+ * Allocation-free variant of vgo_mass_bias_attn_fwd_ws: same arguments (minus
+ * the workspace), kernels and result, bit for bit.  It has no counterpart in
+ * the reference; it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The scratch is a static device array of
+ * VGO_ATTN_STATIC_SCRATCH_BYTES that the library holds on every GPU it runs on
+ * until the process ends; the first call on a device looks up its address.  A
+ * problem whose workspace (vgo_mass_bias_attn_workspace) exceeds it returns
+ * VGO_EWORKSPACE before launching anything.  Calls on one GPU share that
+ * array: calls that overlap on one GPU (different streams, or host threads)
+ * race and must be serialised by the caller.  Nothing in the scratch needs
+ * clearing between calls; each call writes what it reads.
+ */
+#define VGO_ATTN_STATIC_SCRATCH_BYTES (192u * 1024u * 1024u)
+int vgo_mass_bias_attn_fwd_static(const void* q, const void* k, const void* v,
+                                  const void* log_mass, void* out, int64_t batch, int64_t heads,
+                                  int64_t n_query, int64_t n_key, int64_t head_dim,
+                                  const int64_t q_stride[3], const int64_t k_stride[3],
+                                  const int64_t v_stride[3], const int64_t o_stride[3], int dtype,
+                                  void* stream);
 
 /*
  * One attention problem of vgo_mass_bias_attn_pair_fwd_ws, with the meaning of
