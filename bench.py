@@ -28,6 +28,7 @@ import argparse
 import importlib
 import json
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -207,6 +208,127 @@ def c3_attention(vgo, device, steps):
             "frac": flops / sec / 1e12 / PEAK_BF16_TFLOPS, "torch_sdpa_ms": sdpa * 1e3}
 
 
+def _global_block_step(vgo, prof, block, x, layout, ratio):
+    """One merged global block as the aggregator's global arm runs it
+    (aggregator.py:1002-1052, 1215): fused norm1 + unit rows, FastVGGT plan with
+    log-cluster-size bias, forward_compacted -- under bf16 autocast."""
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        with prof.span("global.block"):
+            unit, h = block.norm1_unit_rows(x)
+            with prof.span("global.plan_build"):
+                plan = vgo.build_fastvggt_plan(unit, merge_ratio=ratio, protect_ratio=0.0, mass_bias=True,
+                                               prenormalized=True, **layout)
+            out = block.forward_compacted(x, plan, normalized=h)
+    return out, plan
+
+
+def c3_block(vgo, device, steps):
+    """BASELINE config 3 as a whole block: one merged global block at S=16 (16,464
+    tokens, dim 1,024, 16 heads): plan build, q/k/v compaction, mass-bias attention
+    (8,232 x 8,232 after the FastVGGT merge at ratio 0.5), output projection,
+    restore, residual rows and MLP, with the reference's global.* breakdown; the
+    same block on the torch restatement of the reference's op sequence beside it."""
+    layers = importlib.import_module("4d_ttt_merging_amd.layers")
+    prof = importlib.import_module("4d_ttt_merging_amd.profiling")
+    tm = importlib.import_module("4d_ttt_merging_amd.token_merging")
+    frames = 16
+    n = frames * (SPECIALS + 1024)
+    torch.manual_seed(0)
+    block = layers.SelfAttentionBlock(DIM, HEADS, qkv_bias=True, init_values=1e-5, mask_k_bias=True,
+                                      use_qk_norm=True).to(device).eval()
+    g = torch.Generator(device=device).manual_seed(5)
+    x = torch.randn(1, n, DIM, device=device, generator=g)
+    layout = dict(frames=frames, tokens_per_frame=SPECIALS + 1024, patch_token_start=SPECIALS, patch_hw=GRID)
+    sec = event_time(lambda: _global_block_step(vgo, prof, block, x, layout, 0.5), steps, 3)
+    prof.reset()
+    prof.enable(True)
+    _, plan = _global_block_step(vgo, prof, block, x, layout, 0.5)
+    prof.enable(False)
+    spans = {label: round(total / calls, 4) for label, (total, calls) in sorted(prof.summary().items())}
+    prof.reset()
+    kept = plan.kept_tokens
+    attn_ms = spans.get("global.main_attention", float("nan"))
+    flops = 4 * HEADS * kept * kept * 64
+    ref = TorchReferenceGlobal(frames, SPECIALS + 1024, SPECIALS, GRID, 0.5, tm)
+
+    def torch_block():
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            return ref.block(block, x)
+
+    sec_ref = event_time(torch_block, max(2, steps // 4), 1)
+    return {"tokens": n, "kept": kept, "block_ms": round(sec * 1e3, 4), "breakdown_ms": spans,
+            "attention_tflops": round(flops / (attn_ms / 1e3) / 1e12, 1),
+            "attention_frac": round(flops / (attn_ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "torch_restatement_block_ms": round(sec_ref * 1e3, 4),
+            "speedup": round(sec_ref / sec, 3)}
+
+
+def c5_long(vgo, device, steps):
+    """S=200 frames x 1,029 = 205,800 tokens merged to 25 %
+    (FastVGGT at protect 0 and ratio 0.75 removes every source: 52,968 keys =
+    frame-0 patches + one anchor per 2x2 cell + specials; masses = cluster sizes),
+    then mass-bias attention of all 205,800 queries over those keys (16 x 64
+    heads, bf16).  Peak device memory over the leg is reported."""
+    frames = 200
+    n = frames * (SPECIALS + 1024)
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
+    g = torch.Generator(device=device).manual_seed(9)
+    tokens = torch.randn(1, n, DIM, device=device, generator=g)
+    layout = dict(frames=frames, tokens_per_frame=SPECIALS + 1024, patch_token_start=SPECIALS, patch_hw=GRID)
+    build = lambda: vgo.build_fastvggt_plan(tokens, merge_ratio=0.75, protect_ratio=0.0,  # noqa: E731
+                                            mass_bias=True, **layout)
+    plan = build()
+    plan_sec = event_time(build, max(2, steps // 2), 1)
+    del tokens
+    nk = plan.kept_tokens
+    q = (torch.randn(1, HEADS, n, 64, device=device, generator=g) * 0.125).bfloat16()
+    k = (torch.randn(1, HEADS, nk, 64, device=device, generator=g) * 0.125).bfloat16()
+    v = torch.randn(1, HEADS, nk, 64, device=device, generator=g).bfloat16()
+    bias = plan.key_log_mass.reshape(-1)
+    sec = event_time(lambda: vgo.mass_bias_attention(q, k, v, bias), steps, 2)
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated() - base
+    flops = 4 * HEADS * n * nk * 64
+    counts = plan.cluster_counts(0)
+    return {"tokens": n, "keys": nk, "mass_range": [int(counts.min()), int(counts.max())],
+            "plan_ms": round(plan_sec * 1e3, 3), "attention_ms": round(sec * 1e3, 3),
+            "attention_tflops": round(flops / sec / 1e12, 1),
+            "attention_frac": round(flops / sec / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "peak_memory_gb": round(peak / 1e9, 3)}
+
+
+def gather_ceiling(device, steps):
+    """Random-row gather bandwidth through the memory fabric, measured with torch's own
+    index_select (independent of this build's kernels): 1,048,576 rows of 2 KB (bf16 x
+    1,024) gathered from tables of 4 MB (L2-resident), 32 MB (MALL) and 512 MB (HBM);
+    GB/s counts the bytes gathered plus the bytes written.  Beside it: a plain 2 GB
+    device copy, and this build's projection kernel with one-hot weights (one gather
+    per row) on the 512 MB table."""
+    vgo = importlib.import_module("4d_ttt_merging_amd")
+    n, d = 1 << 20, DIM
+    g = torch.Generator(device=device).manual_seed(7)
+    out = torch.empty(n, d, device=device, dtype=torch.bfloat16)
+    res = {}
+    for rows in (2048, 16384, 262144):
+        table = torch.randn(rows, d, device=device, generator=g).bfloat16()
+        idx = torch.randint(0, rows, (n,), device=device, generator=g)
+        sec = event_time(lambda: torch.index_select(table, 0, idx, out=out), steps, 2)
+        res[f"index_select_{rows * d * 2 >> 20}MB_gbs"] = round(2 * n * d * 2 / sec / 1e9, 1)
+        if rows == 262144:
+            index = torch.stack([idx.int()] * 4, 1)
+            weight = torch.zeros(n, 4, device=device)
+            weight[:, 0] = 1.0
+            sec = event_time(lambda: vgo.top4_project(table, index, weight, out=out), steps, 2)
+            res["top4_project_one_hot_512MB_gbs"] = round(2 * n * d * 2 / sec / 1e9, 1)
+        del table
+    src = torch.empty(n * d, device=device, dtype=torch.bfloat16).fill_(1)
+    sec = event_time(lambda: out.view(-1).copy_(src), steps, 2)
+    res["copy_2GB_gbs"] = round(2 * n * d * 2 / sec / 1e9, 1)
+    return res
+
+
 def block_rows(device, steps):
     """Residual stream of one block at C4 sizes (32,928 x 1,024 fp32 rows).
 
@@ -363,71 +485,115 @@ def simplex_solvers(device, steps):
 
 
 # ------------------------------------------------------------ CPU baseline ----
-def cpu_baseline(budget_s: float = 30.0):
-    """The CPU oracle on a bounded sample of the C4 workload, extrapolated.
+def _median_seconds(fn, warmup: int = 2, runs: int = 5) -> float:
+    """Two untimed warm-up calls, then the median wall time of five."""
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
 
-    Sample: one merged global block at S=32 on the host cores in fp32 -- the
-    FastVGGT plan on all 32,928 tokens (oracle scores), compaction of Q/K/V,
-    mass-bias attention for one of 16 heads and 1,024 of the 16,464 compacted
-    queries (scaled by 16 x 16,464/1,024), projection and restore -- plus one
-    frame block on 4 of the 32 frames (scaled by 8).  Reported frames/s =
-    32 / (24 x (t_frame + t_global)), the per-pair extrapolation the
-    measurement plan prescribes.
+
+class _CpuBlocks:
+    """The bench model's first frame block and first global block on the host cores
+    (fp32 copies of their weights), run with the CPU oracle's op sequence."""
+
+    def __init__(self, model):
+        cpu = lambda t: t.detach().float().cpu()  # noqa: E731
+        self.frame = {k: cpu(v) for k, v in model.frame_blocks[0].state_dict().items()}
+        self.glob = {k: cpu(v) for k, v in model.inter_frame_blocks[0].state_dict().items()}
+
+    @staticmethod
+    def _qkv(w, x):
+        bias = w["attn.qkv.bias"] * w["attn.qkv.bias_mask"]
+        return F.linear(x, w["attn.qkv.weight"], bias)
+
+    @staticmethod
+    def _tail(w, x, y):
+        """x + ls1(proj(y)) then + ls2(mlp(norm2(.))) (block.py:126-127, 219-226)."""
+        x_attn = x + w["ls1.gamma"] * F.linear(y, w["attn.proj.weight"], w["attn.proj.bias"])
+        h = F.layer_norm(x_attn, (DIM,), w["norm2.weight"], w["norm2.bias"], 1e-5)
+        h = F.linear(F.gelu(F.linear(h, w["mlp.fc1.weight"], w["mlp.fc1.bias"])),
+                     w["mlp.fc2.weight"], w["mlp.fc2.bias"])
+        return x_attn + w["ls2.gamma"] * h
+
+    def global_block(self, x, frames, q_sample):
+        """One merged global block on tokens x [N, D]: the FastVGGT plan on all tokens
+        (oracle scores), q/k/v compaction, attention for one head and `q_sample`
+        queries (returned time scaled to 16 heads and every query), the tail on all
+        rows.  Returns (seconds, attention seconds before scaling)."""
+        from oracle import attention as oa
+        from oracle import merging as om
+        w = self.glob
+        t0 = time.perf_counter()
+        n1 = F.layer_norm(x, (DIM,), w["norm1.weight"], w["norm1.bias"], 1e-5)
+        plan = om.fastvggt_plan(n1[None], frames=frames, tokens_per_frame=SPECIALS + 1024,
+                                patch_token_start=SPECIALS, patch_hw=GRID, merge_ratio=0.5,
+                                protect_ratio=0.0)
+        q, k, v = self._qkv(w, n1).split(DIM, dim=-1)
+        q = F.layer_norm(q.reshape(-1, HEADS, 64), (64,), w["attn.q_norm.weight"], w["attn.q_norm.bias"], 1e-5)
+        k = F.layer_norm(k.reshape(-1, HEADS, 64), (64,), w["attn.k_norm.weight"], w["attn.k_norm.bias"], 1e-5)
+        kept, inv = plan["keep"].numel(), plan["inverse"]
+        counts = torch.bincount(inv, minlength=kept).float()
+        pool = lambda t: torch.zeros(kept, DIM).index_add_(0, inv, t.reshape(-1, DIM)) / counts[:, None]  # noqa: E731
+        qc, kc, vc = pool(q), pool(k), pool(v)
+        t_rest = time.perf_counter() - t0
+        t1 = time.perf_counter()
+        head = lambda t: t[:, :64].reshape(1, 1, -1, 64)  # noqa: E731
+        oa.mass_bias_attention(head(qc[:q_sample]), head(kc), head(vc), counts.log())
+        t_att = time.perf_counter() - t1
+        t2 = time.perf_counter()
+        self._tail(w, x, qc[inv])  # restore of the compact update, then the tail on all rows
+        t_tail = time.perf_counter() - t2
+        return t_rest + t_tail + t_att * HEADS * kept / q_sample, t_att
+
+    def frame_block(self, x, frames):
+        """Frame attention (per-frame SDPA, q/k LayerNorm, RoPE omitted) + tail."""
+        w = self.frame
+        n1 = F.layer_norm(x, (DIM,), w["norm1.weight"], w["norm1.bias"], 1e-5)
+        qkv = self._qkv(w, n1).reshape(frames, -1, 3, HEADS, 64)
+        q, k, v = [t.transpose(1, 2) for t in qkv.unbind(2)]
+        o = F.scaled_dot_product_attention(q, k, v).transpose(1, 2).reshape(x.shape[0], DIM)
+        return self._tail(w, x, o)
+
+
+def cpu_baseline(model) -> dict:
+    """The CPU oracle (fp32, the reference's op sequence) on bounded samples, on the
+    host cores: two warm-ups, then the median of five, per configuration.
+
+    * C4 (the bench workload): one frame block on 4 of 32 frames (scaled x8) plus
+      one merged global block at S=32 whose attention runs for one head and 1,024
+      compacted queries (scaled to 16 heads x 16,464); frames/s = 32 / (24 x pair),
+      the per-pair extrapolation of the measurement plan.  The blocks carry the
+      bench model's own weights.
+    * C3: the merged global block at S=16 the same way (attention scaled from one
+      head x 1,024 of 8,232 queries).
+    * C2: the top-4 projection of 131,072 of the 1,048,576 rows (fp32, full
+      65,536-row table) with the reference's restore op sequence (gather, multiply,
+      sum), scaled x8.
     """
-    from oracle import attention as oa
-    from oracle import merging as om
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
+    blocks = _CpuBlocks(model)
     g = torch.Generator().manual_seed(2)
-    total = FRAMES * (SPECIALS + GRID[0] * GRID[1])
-    tokens = torch.randn(1, total, DIM, generator=g)
-    w_qkv = torch.randn(3 * DIM, DIM, generator=g) * DIM ** -0.5
-    w_proj = torch.randn(DIM, DIM, generator=g) * DIM ** -0.5
-    w1 = torch.randn(4 * DIM, DIM, generator=g) * DIM ** -0.5
-    w2 = torch.randn(DIM, 4 * DIM, generator=g) * (4 * DIM) ** -0.5
-    t0 = time.perf_counter()
-    plan = om.fastvggt_plan(tokens, frames=FRAMES, tokens_per_frame=SPECIALS + GRID[0] * GRID[1],
-                            patch_token_start=SPECIALS, patch_hw=GRID, merge_ratio=0.5,
-                            protect_ratio=0.0)
-    t_plan = time.perf_counter() - t0
-    x = tokens[0]
-    t0 = time.perf_counter()
-    qkv = x @ w_qkv.T
-    q, k, v = qkv.split(DIM, dim=-1)
-    kept = plan["keep"].numel()
-    inv = plan["inverse"]
-    counts = torch.bincount(inv, minlength=kept).float()
-
-    def compact(t):
-        sums = torch.zeros(kept, DIM).index_add_(0, inv, t)
-        return sums / counts[:, None]
-
-    qc, kc, vc = compact(q), compact(k), compact(v)
-    t_pack = time.perf_counter() - t0
-    q_sample = 1024
-    t0 = time.perf_counter()
-    head = lambda t: t[:, :64].reshape(1, 1, -1, 64)  # noqa: E731
-    att = oa.mass_bias_attention(head(qc[:q_sample]), head(kc), head(vc), counts.log())
-    t_att = (time.perf_counter() - t0) * HEADS * (kept / q_sample)
-    t0 = time.perf_counter()
-    y = qc @ w_proj.T
-    restored = y[inv]
-    h = restored + (F.gelu(restored @ w1.T) @ w2.T)
-    t_tail = time.perf_counter() - t0
-    del att, h
-    t_global = t_plan + t_pack + t_att + t_tail
-    # frame block on 4 frames: qkv, per-frame SDPA, proj, MLP
-    f = 4
-    xf = tokens[0, : f * (SPECIALS + GRID[0] * GRID[1])]
-    t0 = time.perf_counter()
-    qkv = (xf @ w_qkv.T).reshape(f, -1, 3, HEADS, 64)
-    qf, kf, vf = [t.transpose(1, 2) for t in qkv.unbind(2)]
-    o = F.scaled_dot_product_attention(qf, kf, vf).transpose(1, 2).reshape(xf.shape[0], DIM)
-    o = o @ w_proj.T
-    o = o + F.gelu(o @ w1.T) @ w2.T
-    t_frame = (time.perf_counter() - t0) * (FRAMES / f)
-    pair = t_frame + t_global
-    value = FRAMES / (24 * pair)
+    tpf = SPECIALS + 1024
+    x32 = torch.randn(FRAMES * tpf, DIM, generator=g)
+    x16 = x32[:16 * tpf].contiguous()
+    x4 = x32[:4 * tpf].contiguous()
+    c4_global = _median_seconds(lambda: blocks.global_block(x32, FRAMES, 1024))
+    c4_frame = _median_seconds(lambda: blocks.frame_block(x4, 4)) * (FRAMES / 4)
+    pair = c4_frame + c4_global
+    c3 = _median_seconds(lambda: blocks.global_block(x16, 16, 1024))
+    index, weight = c2_inputs(1 << 20, 65536)
+    table = torch.randn(65536, DIM, generator=g)
+    rows = 131072
+    idx, wts = index[:rows].long(), weight[:rows]
+    # the reference's restore op sequence (token_merging.py:405-413) on the host cores
+    c2 = _median_seconds(lambda: (table[idx] * wts[..., None]).sum(1)) * ((1 << 20) / rows)
+    c2_bytes = (1 << 20) * DIM * 4 + 65536 * DIM * 4 + 32 * (1 << 20)
     cpu = "unknown"
     try:
         for line in open("/proc/cpuinfo"):
@@ -436,13 +602,17 @@ def cpu_baseline(budget_s: float = 30.0):
                 break
     except OSError:
         pass
-    return {"value": value, "unit": "frames/s", "cores": threads, "kind": "port",
-            "sample": ("one merged global block at S=32 (plan on all 32,928 tokens, attention for "
-                       "1/16 heads x 1,024 queries scaled) + one frame block on 4/32 frames "
-                       "scaled; fp32 CPU oracle; frames/s = 32 / (24 x pair)"),
-            "cpu_model": cpu, "pair_seconds": pair,
-            "parts_s": {"plan": t_plan, "compaction": t_pack, "attention_scaled": t_att,
-                        "proj_restore_mlp": t_tail, "frame_block_scaled": t_frame}}
+    return {"value": round(FRAMES / (24 * pair), 5), "unit": "frames/s", "cores": threads, "kind": "port",
+            "sample": ("C4: one frame block on 4/32 frames (x8) + one merged global block at S=32 with "
+                       "attention for 1/16 heads x 1,024 queries (scaled), fp32 CPU oracle with the "
+                       "bench model's block weights, frames/s = 32 / (24 x pair); median of 5 after 2 "
+                       "warm-ups"),
+            "cpu_model": cpu, "threads": threads,
+            "c4_pair_s": round(pair, 4), "c4_frame_block_s": round(c4_frame, 4),
+            "c4_global_block_s": round(c4_global, 4),
+            "c3_block_ms": round(c3 * 1e3, 2),
+            "c2_fp32_ms": round(c2 * 1e3, 2), "c2_fp32_gbs": round(c2_bytes / c2 / 1e9, 2),
+            "c2_sample": "131,072 of 1,048,576 rows (x8), fp32, gather-multiply-sum"}
 
 
 # ----------------------------------------------------- counter workloads ----
@@ -488,6 +658,9 @@ def only_workload(which: str) -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"workload": "copy", "bytes": n, "launches": 3}), flush=True)
+        return 0
+    if which == "gather":
+        print(json.dumps({"workload": "gather", **gather_ceiling(device, 3)}), flush=True)
         return 0
     vgo = importlib.import_module("4d_ttt_merging_amd")
     if which == "projection":
@@ -551,12 +724,13 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-reference", action="store_true")
-    ap.add_argument("--only", choices=("attention", "projection", "merge", "copy"), default=None,
+    ap.add_argument("--only", choices=("attention", "projection", "merge", "copy", "gather"), default=None,
                     help="run one kernel workload for rocprofv3 counter passes, then exit: "
                          "'attention' = 3 C4-size mass-bias attention launches, 'projection' = 3 "
                          "C2 bf16 top-4 projections, 'merge' = 3 x (norm1 unit rows, FastVGGT plan, "
                          "q/k/v compaction) of a C4 global block, 'copy' = 3 plain 256 MiB device "
-                         "copies (the FETCH_SIZE / WRITE_SIZE calibration)")
+                         "copies (the FETCH_SIZE / WRITE_SIZE calibration), 'gather' = the random-row "
+                         "gather ceiling probe (torch index_select, 4 / 32 / 512 MB tables)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
@@ -636,6 +810,17 @@ def main() -> int:
         "global_block_breakdown_ms": breakdown,
     }
     torch.cuda.synchronize()
+    restore_ms = spans.get("global.update_restore", (float("nan"), 1))
+    restore_ms = restore_ms[0] / restore_ms[1]
+    n_tok = FRAMES * (SPECIALS + 1024)
+    restore_bytes = n_tok * DIM * 2 + kept * DIM * 2 + 32 * n_tok
+    result["global_restore"] = {"ms": round(restore_ms, 4), "bytes": restore_bytes,
+                                "gbs": round(restore_bytes / (restore_ms / 1e3) / 1e9, 1),
+                                "frac": round(restore_bytes / (restore_ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4)}
+    log("C3 global block")
+    result["c3_block"] = c3_block(vgo, device, 20)
+    log("C5 long sequence")
+    result["c5_long"] = c5_long(vgo, device, 5)
     log("C3 attention microbench")
     result["c3_attention"] = c3_attention(vgo, device, 20)
     log("block residual rows microbench")
@@ -646,6 +831,8 @@ def main() -> int:
     result["plan_replay"] = plan_replay(vgo, device, 10)
     log("C2 projection microbench")
     result["c2_projection"] = c2_projection(vgo, device, 10)
+    log("gather ceiling probe")
+    result["gather_ceiling"] = gather_ceiling(device, 10)
     log("simplex solvers microbench")
     result["simplex_solvers"] = simplex_solvers(device, 20)
     if not args.no_reference:
@@ -663,7 +850,7 @@ def main() -> int:
                                      "speedup": round(fps / (FRAMES / sec), 3)}
     if not args.no_cpu_baseline:
         log("CPU oracle baseline (bounded sample)")
-        result["cpu_baseline"] = cpu_baseline()
+        result["cpu_baseline"] = cpu_baseline(model)
     print(json.dumps(result), flush=True)
     return 0
 
