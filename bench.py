@@ -695,9 +695,10 @@ def only_workload(which: str) -> int:
             for _ in range(3):
                 unit, _ = block.norm1_unit_rows(tokens)
                 plan = vgo.build_fastvggt_plan(unit, prenormalized=True, **layout)
-                for i in range(3):
-                    out = torch.empty(HEADS, plan.kept_tokens, 64, device=device, dtype=torch.bfloat16)
-                    plan.compact_into(qkv[:, i * DIM:(i + 1) * DIM], out, layer_norm=ln if i < 2 else None)
+                outs = [torch.empty(HEADS, plan.kept_tokens, 64, device=device, dtype=torch.bfloat16)
+                        for _ in range(3)]
+                # q, k (with the per-head LayerNorm) and v in one launch, as the block does
+                plan.compact_multi_into(qkv, [(0, outs[0], ln), (DIM, outs[1], ln), (2 * DIM, outs[2], None)])
         torch.cuda.synchronize()
         print(json.dumps({"workload": "merge", "tokens": n, "kept": plan.kept_tokens,
                           "repeats": 3}), flush=True)
@@ -724,6 +725,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-reference", action="store_true")
+    ap.add_argument("--aggregator-only", action="store_true",
+                    help="time the C4 aggregator and print its line without the other legs "
+                         "(for kernel traces of the forward alone)")
     ap.add_argument("--only", choices=("attention", "projection", "merge", "copy", "gather"), default=None,
                     help="run one kernel workload for rocprofv3 counter passes, then exit: "
                          "'attention' = 3 C4-size mass-bias attention launches, 'projection' = 3 "
@@ -817,6 +821,9 @@ def main() -> int:
     result["global_restore"] = {"ms": round(restore_ms, 4), "bytes": restore_bytes,
                                 "gbs": round(restore_bytes / (restore_ms / 1e3) / 1e9, 1),
                                 "frac": round(restore_bytes / (restore_ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4)}
+    if args.aggregator_only:
+        print(json.dumps(result), flush=True)
+        return 0
     log("C3 global block")
     result["c3_block"] = c3_block(vgo, device, 20)
     log("C5 long sequence")
