@@ -15,13 +15,16 @@ reference package `vggt_omega` for the merged global-attention path:
   replay of the TTT planner's trace records (sparse_convex.py:77-80, 1907-1976)
 * `use_tuned_gemms`                      recorded hipBLASLt selections for the
   block's torch GEMMs (TunableOp)
+* `ops` -- the torch.library operators `torch.ops.vgo.*` (mass_bias_attention,
+  top4_project, compaction, QKV epilogue, residual rows) with fake
+  implementations for tracing
 
 Every GPU computation of the path runs in the hand-written gfx950 HIP library
 `libvgo.so` (built by `_build.build()`); there is no CPU fallback.
 """
 from __future__ import annotations
 
-from . import _lib, plan_io
+from . import _lib, ops, plan_io
 from .gemm_tuning import use_tuned_gemms
 from .layers import LinearKMaskedBias, SelfAttention, SelfAttentionBlock
 from .mass_bias_attention import dense_attention, mass_bias_attention
@@ -47,6 +50,7 @@ __all__ = [
     "dense_attention",
     "deterministic_weighted_normalizer",
     "mass_bias_attention",
+    "ops",
     "plan_io",
     "streaming_top4",
     "top4_project",

@@ -2,7 +2,10 @@
 
 Each wrapper validates shapes/dtypes on the host, allocates outputs and
 workspaces with torch (device memory only), and launches on torch's current
-stream.  No wrapper synchronises the device.
+stream.  No wrapper synchronises the device.  The kernels a merged block runs
+(compaction, the QKV epilogue, the residual rows) go through the torch.library
+operators of `ops.py` (`torch.ops.vgo.*`), whose implementations are the
+`_*_impl` functions here; the plan-building kernels are called directly.
 """
 from __future__ import annotations
 
@@ -142,7 +145,7 @@ def token_layout(t: torch.Tensor) -> tuple[int, int]:
     raise ValueError("compaction operands must be [N, C] or [H, N, 64] views")
 
 
-def compact_into(x: torch.Tensor, out: torch.Tensor, *, base_rows: torch.Tensor | None,
+def _compact_into_impl(x: torch.Tensor, out: torch.Tensor, *, base_rows: torch.Tensor | None,
                  offsets: torch.Tensor, segs_per_row: int, items: torch.Tensor | None,
                  item_shift: int, item_rows: torch.Tensor | None, weights: torch.Tensor | None,
                  normalizer: torch.Tensor | None,
@@ -174,7 +177,7 @@ def compact_into(x: torch.Tensor, out: torch.Tensor, *, base_rows: torch.Tensor 
     return out
 
 
-def compact_multi_into(x: torch.Tensor, outputs, *, base_rows: torch.Tensor | None,
+def _compact_multi_into_impl(x: torch.Tensor, outputs, *, base_rows: torch.Tensor | None,
                        offsets: torch.Tensor, segs_per_row: int, items: torch.Tensor | None,
                        item_shift: int, item_rows: torch.Tensor | None, weights: torch.Tensor | None,
                        normalizer: torch.Tensor | None) -> None:
@@ -252,7 +255,7 @@ def restore_map(total: int, *, device: torch.device, keep: torch.Tensor | None =
     return index_out, weight_out
 
 
-def qkv_epilogue(qkv: torch.Tensor, heads: int, *, tokens_in: int, tokens_out: int | None = None,
+def _qkv_epilogue_impl(qkv: torch.Tensor, heads: int, *, tokens_in: int, tokens_out: int | None = None,
                  rows: torch.Tensor | None = None, q_norm=None, k_norm=None, eps: float = 1e-5,
                  rope: tuple[torch.Tensor, torch.Tensor] | None = None, rope_prefix: int = 0,
                  want=(True, True, True), out_dtype: torch.dtype | None = None):
@@ -291,7 +294,7 @@ def qkv_epilogue(qkv: torch.Tensor, heads: int, *, tokens_in: int, tokens_out: i
     return tuple(outs)
 
 
-def residual_layer_norm(x: torch.Tensor, branch: torch.Tensor | None = None,
+def _residual_layer_norm_impl(x: torch.Tensor, branch: torch.Tensor | None = None,
                         gamma: torch.Tensor | None = None,
                         norm: tuple[torch.Tensor | None, torch.Tensor | None, float] | None = None, *,
                         write_sum: bool = True, norm_dtype: torch.dtype | None = torch.bfloat16,
@@ -345,4 +348,65 @@ def residual_layer_norm(x: torch.Tensor, branch: torch.Tensor | None = None,
     _lib.check(status)
     if unit_eps is not None:
         return total, normed, normed32, unit
+    return total, normed, normed32
+
+
+# --------------------------------------------- operator-backed entry points ----
+def compact_into(x: torch.Tensor, out: torch.Tensor, *, base_rows: torch.Tensor | None,
+                 offsets: torch.Tensor, segs_per_row: int, items: torch.Tensor | None,
+                 item_shift: int, item_rows: torch.Tensor | None, weights: torch.Tensor | None,
+                 normalizer: torch.Tensor | None,
+                 layer_norm: tuple[torch.Tensor, torch.Tensor, float] | None = None) -> torch.Tensor:
+    """Segmented weighted pooling into `out` (torch.ops.vgo.compact_into); see _compact_into_impl."""
+    ln_w, ln_b, eps = layer_norm if layer_norm is not None else (None, None, 0.0)
+    torch.ops.vgo.compact_into(x, out, base_rows, offsets, segs_per_row, items, item_shift, item_rows,
+                               weights, normalizer, ln_w, ln_b, float(eps))
+    return out
+
+
+def compact_multi_into(x: torch.Tensor, outputs, *, base_rows: torch.Tensor | None,
+                       offsets: torch.Tensor, segs_per_row: int, items: torch.Tensor | None,
+                       item_shift: int, item_rows: torch.Tensor | None, weights: torch.Tensor | None,
+                       normalizer: torch.Tensor | None) -> None:
+    """1-3 outputs of one segment structure in one launch (torch.ops.vgo.compact_multi_into);
+    `outputs` holds (channel offset, out, layer_norm or None) per output."""
+    torch.ops.vgo.compact_multi_into(
+        x, [int(off) for off, _, _ in outputs], [out for _, out, _ in outputs],
+        [None if ln is None else ln[0] for _, _, ln in outputs],
+        [None if ln is None else ln[1] for _, _, ln in outputs],
+        [0.0 if ln is None else float(ln[2]) for _, _, ln in outputs],
+        base_rows, offsets, segs_per_row, items, item_shift, item_rows, weights, normalizer)
+
+
+def qkv_epilogue(qkv: torch.Tensor, heads: int, *, tokens_in: int, tokens_out: int | None = None,
+                 rows: torch.Tensor | None = None, q_norm=None, k_norm=None, eps: float = 1e-5,
+                 rope: tuple[torch.Tensor, torch.Tensor] | None = None, rope_prefix: int = 0,
+                 want=(True, True, True), out_dtype: torch.dtype | None = None):
+    """Head-major q/k/v from packed projection rows (torch.ops.vgo.qkv_epilogue); see
+    _qkv_epilogue_impl.  Returns (q, k, v) with None for unwanted ones."""
+    outs = torch.ops.vgo.qkv_epilogue(
+        qkv, heads, tokens_in, tokens_out or tokens_in, rows,
+        None if q_norm is None else q_norm[0], None if q_norm is None else q_norm[1],
+        None if k_norm is None else k_norm[0], None if k_norm is None else k_norm[1], float(eps),
+        None if rope is None else rope[0], None if rope is None else rope[1], rope_prefix,
+        [bool(w) for w in want], out_dtype or qkv.dtype)
+    return tuple(o if w else None for o, w in zip(outs, want))
+
+
+def residual_layer_norm(x: torch.Tensor, branch: torch.Tensor | None = None,
+                        gamma: torch.Tensor | None = None,
+                        norm: tuple[torch.Tensor | None, torch.Tensor | None, float] | None = None, *,
+                        write_sum: bool = True, norm_dtype: torch.dtype | None = torch.bfloat16,
+                        norm_f32: bool = False, unit_eps: float | None = None):
+    """One residual-row pass (torch.ops.vgo.residual_layer_norm); see _residual_layer_norm_impl.
+    Returns (s, n, n_f32[, u]) with None for outputs not asked for."""
+    w, b, eps = norm if norm is not None else (None, None, 0.0)
+    outs = torch.ops.vgo.residual_layer_norm(
+        x, branch, gamma, w, b, float(eps), norm is not None, write_sum, norm_dtype, norm_f32,
+        -1.0 if unit_eps is None else float(unit_eps))
+    total = outs[0] if write_sum and branch is not None else None
+    normed = outs[1] if norm is not None and norm_dtype is not None else None
+    normed32 = outs[2] if norm is not None and norm_f32 else None
+    if unit_eps is not None:
+        return total, normed, normed32, outs[3]
     return total, normed, normed32

@@ -153,9 +153,19 @@ __host__ __device__ __forceinline__ int64_t sk_owner(int64_t u, int64_t units, i
   return ((u + 1) * groups - 1) / units;
 }
 
-// LDS stages: 2 (register-staged kernel) or 3 (DMA kernel); a stage holds a
-// K tile, a V^T tile and the tile's 64 bias pairs (hi, lo).
-constexpr int kBiasSlot = 2 * kBN;
+// LDS stages: 2 (register-staged kernel) or 4 (DMA kernel); a stage holds a
+// K tile, a V^T tile and the tile's 64 bias pairs (hi, lo), followed by 32
+// zero dwords: the bias k-step's A operand of lanes 32-63 is zero, and those
+// lanes read it from there, so the loaded dword is the operand as it stands
+// (no VALU step on it, hence no early wait for the read inside an MFMA run).
+constexpr int kBiasPairs = 2 * kBN;
+constexpr int kBiasSlot = kBiasPairs + kBN;
+// Every kernel zeroes the tail of its stages once, before its first barrier.
+template <typename T>
+__device__ __forceinline__ void zero_bias_tails(T* b_lds, int stages) {
+  for (int i = threadIdx.x; i < stages * (kBN / 2); i += blockDim.x)
+    reinterpret_cast<uint32_t*>(b_lds + (i / (kBN / 2)) * kBiasSlot + kBiasPairs)[i % (kBN / 2)] = 0u;
+}
 // Largest per-lane sum of 32 probabilities the lazy softmax accepts without
 // moving its reference max (bounds every P by 2^8).
 constexpr float kLazyLimit = 256.0f;
@@ -176,6 +186,7 @@ struct WaveAttn {
   float mref[kQB], lsum[kQB];
   f32x16 o[kQB][2];
   int off[4];  // LDS element offsets of logical chunk pair t of row l32
+  int boff[2];  // bias dword of sub-tile sub: key 32*sub + l32's pair, or a zero (lanes 32-63)
   uint32_t low_lanes, one_bits;
   int l32, hh;
 
@@ -202,6 +213,8 @@ struct WaveAttn {
 #pragma unroll
     for (int t = 0; t < 4; ++t) off[t] = l32 * kD + (((2 * t + hh) ^ s0) << 3);
 #pragma unroll
+    for (int sub = 0; sub < 2; ++sub) boff[sub] = hh == 0 ? 2 * (sub * 32 + l32) : kBiasPairs + 2 * l32;
+#pragma unroll
     for (int qb = 0; qb < kQB; ++qb) {
       mref[qb] = -__builtin_inff();
       qneg[qb] = neg_bits(mref[qb]);
@@ -223,8 +236,8 @@ struct WaveAttn {
     return __builtin_bit_cast(op8, w);
   }
   __device__ __forceinline__ op8 bias_a(const T* bl, int sub) const {
-    const uint32_t bw = *reinterpret_cast<const uint32_t*>(bl + 2 * (sub * 32 + l32));
-    const i32x4 w = {static_cast<int>(bw & low_lanes), static_cast<int>(one_bits & low_lanes), 0, 0};
+    const uint32_t bw = *reinterpret_cast<const uint32_t*>(bl + boff[sub]);
+    const i32x4 w = {static_cast<int>(bw), static_cast<int>(one_bits & low_lanes), 0, 0};
     return __builtin_bit_cast(op8, w);
   }
   // A operand of rows 32*half.. of a K or V^T tile, k-chunk pair t.
@@ -509,6 +522,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attn_reg_kernel(AttnArgs<T> a)
 
   WaveAttn<T> w;
   w.init(a.q + b * a.qsb + h * a.qsh, a.qsn, qw0, a.nq, a.c);
+  zero_bias_tails(b_lds, 2);
 
   // K: rows st and st+32, chunk sc.  V: keys 2st, 2st+1, dims 8sc..8sc+7.
   // Row offsets fit in 32 bits (checked on the host).
@@ -804,6 +818,7 @@ __global__ __launch_bounds__(kPPWaves * 64, 1) void attn_pp_kernel(PPLaunch<T> L
   __shared__ __attribute__((aligned(16))) T b_lds[kPPStages * kBiasSlot];
   const PPSchedule& sc = L.s;
   const int64_t w = xcd_remap(blockIdx.x, gridDim.x);
+  zero_bias_tails(b_lds, kPPStages);  // ordered before any read by the segment's first barrier
   // Whole tasks first: consecutive work-groups (one XCD's, after the remap)
   // take consecutive tasks of a round, so they stream one head's K/V in step
   // and share it in that XCD's L2.  Then the stream-K range.  One call site

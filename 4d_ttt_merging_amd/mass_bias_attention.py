@@ -56,6 +56,19 @@ REG_MAX_KEYS = 2560
 def _attention_into(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                     bias: torch.Tensor | None, out: torch.Tensor, *,
                     split: bool | None = None) -> torch.Tensor:
+    """`_attention_into_impl` through the operator torch.ops.vgo.attention_into."""
+    torch.ops.vgo.attention_into(q, k, v, bias, out, -1 if split is None else int(split))
+    return out
+
+
+def _attention_pair_into(main: tuple, special: tuple) -> None:
+    """`_attention_pair_into_impl` through the operator torch.ops.vgo.attention_pair_into."""
+    torch.ops.vgo.attention_pair_into(*main, *special)
+
+
+def _attention_into_impl(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                         bias: torch.Tensor | None, out: torch.Tensor, *,
+                         split: bool | None = None) -> torch.Tensor:
     """Run the kernel on [B,H,N,64] views (any batch/head/token strides) into `out`.
 
     split=True takes the workspace entry: V^T packed per head, 512-query
@@ -87,7 +100,7 @@ def _attention_into(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     return out
 
 
-def _attention_pair_into(main: tuple, special: tuple) -> None:
+def _attention_pair_into_impl(main: tuple, special: tuple) -> None:
     """Merged attention and the dense special-query pass in one launch.
 
     `main` and `special` are (q, k, v, bias, out) as for `_attention_into`;
@@ -124,6 +137,7 @@ def mass_bias_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         _lib.load()
     except _lib.ExtensionUnavailable as error:
         raise RuntimeError(str(error)) from error
+    _lib.require_gpu(q, k, v, log_key_mass)
     if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
         raise ValueError("q, k and v must be [batch, heads, tokens, channels]")
     if q.shape[-1] != 64 or k.shape[-1] != 64 or v.shape[-1] != 64:
@@ -143,13 +157,12 @@ def mass_bias_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     bias = log_key_mass.reshape(-1).to(q.dtype)
     if bias.numel() != k.shape[-2]:
         raise ValueError("log_key_mass length does not match key tokens")
-    output = torch.empty(q.shape, device=q.device, dtype=output_dtype)
-    return _attention_into(q, k, v, bias, output)
+    return torch.ops.vgo.mass_bias_attention(q, k, v, bias)
 
 
 def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
     """Unbiased attention (the dense special-query pass), same kernel, no bias."""
     if q.shape[-1] != 64:
         raise ValueError("the initial fused kernel supports head_dim=64 only")
-    output = torch.empty(q.shape, device=q.device, dtype=q.dtype)
-    return _attention_into(q, k.to(q.dtype), v.to(q.dtype), None, output)
+    _lib.require_gpu(q, k, v)
+    return torch.ops.vgo.mass_bias_attention(q, k.to(q.dtype), v.to(q.dtype), None)

@@ -8,6 +8,7 @@ Enabled by `enable()` or by the environment variable VGO_PROFILE_ATTENTION=1.
 """
 from __future__ import annotations
 
+import contextlib
 import os
 
 import torch
@@ -32,8 +33,16 @@ def reset() -> None:
     _events.clear()
 
 
-class span:
-    """Context manager recording a begin/end event pair under `label`."""
+def span(label: str):
+    """Context manager recording a begin/end event pair under `label` (a no-op context
+    when recording is off or while torch.compile traces the caller)."""
+    if not _enabled or torch.compiler.is_compiling() or (_only is not None and label not in _only):
+        return contextlib.nullcontext()
+    return _Span(label)
+
+
+class _Span:
+    """Records a begin/end event pair under `label`."""
 
     __slots__ = ("label", "begin")
 
@@ -42,9 +51,8 @@ class span:
         self.begin = None
 
     def __enter__(self):
-        if _enabled and (_only is None or self.label in _only):
-            self.begin = torch.cuda.Event(enable_timing=True)
-            self.begin.record()
+        self.begin = torch.cuda.Event(enable_timing=True)
+        self.begin.record()
         return self
 
     def __exit__(self, *exc):

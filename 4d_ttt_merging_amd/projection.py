@@ -15,6 +15,18 @@ from . import _lib
 
 def top4_project(table: torch.Tensor, index: torch.Tensor, weight: torch.Tensor, *,
                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """Gather four rows of `table` [M, D] per output row and take their weighted sum
+    (torch.ops.vgo.top4_project, or top4_project_into with `out`); see
+    `_top4_project_impl`."""
+    _lib.require_gpu(table, index, weight, out)
+    if out is None:
+        return torch.ops.vgo.top4_project(table, index, weight)
+    torch.ops.vgo.top4_project_into(table, index, weight, out)
+    return out
+
+
+def _top4_project_impl(table: torch.Tensor, index: torch.Tensor, weight: torch.Tensor, *,
+                       out: torch.Tensor | None = None) -> torch.Tensor:
     """Gather four rows of `table` [M, D] per output row and take their weighted sum.
 
     index: [N, 4] int32, weight: [N, 4] float32 (both contiguous).  Zero weights

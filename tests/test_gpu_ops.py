@@ -1,0 +1,97 @@
+"""The torch.library operators `torch.ops.vgo.*` (4d_ttt_merging_amd/ops.py).
+
+CPU: every operator is registered with its schema, has no CPU kernel, and its
+fake implementation describes the outputs (fake-tensor tracing needs no GPU).
+GPU: the operators give the library's results bit for bit, and a merged global
+block (`SelfAttentionBlock.forward_compacted` over a FastVGGT plan, bf16
+autocast) traces into one graph with `torch.compile(fullgraph=True)` and
+returns the eager result exactly (backend aot_eager: the traced graph runs op
+by op, the vgo operators as single nodes).
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from tests.conftest import import_package
+from tests.golden.inputs import structured_tokens
+
+OPS = {
+    "mass_bias_attention": "vgo::mass_bias_attention(Tensor q, Tensor k, Tensor v, Tensor? log_key_mass) -> Tensor",
+    "top4_project": "vgo::top4_project(Tensor table, Tensor index, Tensor weight) -> Tensor",
+    "attention_into": None, "attention_pair_into": None, "top4_project_into": None,
+    "compact_into": None, "compact_multi_into": None, "qkv_epilogue": None, "residual_layer_norm": None,
+}
+
+
+def test_operators_are_registered_without_cpu_kernels():
+    import_package()
+    for name, schema in OPS.items():
+        op = getattr(torch.ops.vgo, name).default
+        if schema is not None:
+            assert str(op._schema) == schema
+        assert not torch._C._dispatch_has_kernel_for_dispatch_key(op.name(), "CPU")
+    with pytest.raises(Exception):
+        torch.ops.vgo.top4_project(torch.zeros(4, 8), torch.zeros(2, 4, dtype=torch.int32), torch.zeros(2, 4))
+
+
+def test_fake_implementations_describe_outputs():
+    import_package()
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    with FakeTensorMode():
+        q = torch.empty(1, 16, 100, 64, dtype=torch.bfloat16, device="cuda")
+        k = torch.empty(1, 16, 50, 64, dtype=torch.bfloat16, device="cuda")
+        out = torch.ops.vgo.mass_bias_attention(q, k, k, None)
+        assert out.shape == q.shape and out.dtype == torch.bfloat16
+        table = torch.empty(30, 256, dtype=torch.float32, device="cuda")
+        proj = torch.ops.vgo.top4_project(table, torch.empty(70, 4, dtype=torch.int32, device="cuda"),
+                                          torch.empty(70, 4, device="cuda"))
+        assert proj.shape == (70, 256) and proj.dtype == torch.float32
+        qkv = torch.empty(3 * 261, 3 * 256, dtype=torch.bfloat16, device="cuda")
+        q3, k3, v3 = torch.ops.vgo.qkv_epilogue(qkv, 4, 261, 261, None, None, None, None, None, 1e-5,
+                                                None, None, 0, [True, False, True], torch.bfloat16)
+        assert q3.shape == (3, 4, 261, 64) and k3.numel() == 0 and v3.shape == (3, 4, 261, 64)
+        x = torch.empty(10, 256, device="cuda")
+        total, norm, norm32, unit = torch.ops.vgo.residual_layer_norm(
+            x, x.bfloat16(), None, None, None, 1e-5, True, True, torch.bfloat16, False, 1e-12)
+        assert total.shape == x.shape and norm.dtype == torch.bfloat16 and norm32.numel() == 0
+        assert unit.shape == x.shape
+
+
+@pytest.mark.gpu
+def test_operators_match_the_library_entry_points(vgo, device):
+    g = torch.Generator(device=device).manual_seed(3)
+    q = (torch.randn(1, 4, 700, 64, device=device, generator=g) * 0.125).bfloat16()
+    k = (torch.randn(1, 4, 3000, 64, device=device, generator=g) * 0.125).bfloat16()
+    v = torch.randn(1, 4, 3000, 64, device=device, generator=g).bfloat16()
+    mass = torch.randint(1, 9, (3000,), device=device, generator=g).float().log()
+    ref = vgo.mass_bias_attention(q, k, v, mass)
+    assert torch.equal(torch.ops.vgo.mass_bias_attention(q, k, v, mass.bfloat16()), ref)
+    out = torch.empty_like(q)
+    torch.ops.vgo.attention_into(q, k, v, mass.bfloat16(), out, -1)
+    assert torch.equal(out, ref)
+    table = torch.randn(500, 256, device=device, generator=g)
+    index = torch.randint(0, 500, (900, 4), device=device, generator=g, dtype=torch.int32)
+    weight = torch.rand(900, 4, device=device, generator=g)
+    assert torch.equal(torch.ops.vgo.top4_project(table, index, weight),
+                       vgo.top4_project(table, index, weight))
+
+
+@pytest.mark.gpu
+def test_forward_compacted_traces_into_one_graph(vgo, device):
+    print("[ops] torch.compile fullgraph over forward_compacted", flush=True)
+    torch.manual_seed(0)
+    block = vgo.SelfAttentionBlock(256, 4, qkv_bias=True, init_values=0.5, mask_k_bias=True,
+                                   use_qk_norm=True).eval().to(device)
+    x = structured_tokens(9, 4, (16, 16), 5, 256).to(device)
+    kw = dict(frames=4, tokens_per_frame=261, patch_token_start=5, patch_hw=(16, 16))
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        unit, h = block.norm1_unit_rows(x)
+        plan = vgo.build_fastvggt_plan(unit, merge_ratio=0.5, protect_ratio=0.0, mass_bias=True,
+                                       prenormalized=True, **kw)
+        eager = block.forward_compacted(x, plan, normalized=h)  # also builds the plan's CSR / map
+        torch._dynamo.reset()
+        compiled = torch.compile(block.forward_compacted, backend="aot_eager", fullgraph=True)
+        traced = compiled(x, plan, normalized=h)
+        again = compiled(x, plan, normalized=h)
+    assert torch.equal(traced, eager) and torch.equal(again, eager)
