@@ -29,7 +29,7 @@ import torch.nn as nn
 
 from . import profiling
 from .layers import Mlp, SelfAttentionBlock, init_weights_vit, rope_sincos
-from .sparse_convex import build_sparse_convex_plan
+from .sparse_convex import build_sparse_convex_plan, start_sparse_convex_plan
 from .token_merging import build_fastvggt_plan
 
 _DEFAULT_SPARSE_CONVEX_QKV_LAYERS = tuple(layer for layer in range(19) if layer not in {8, 10, 11, 12})
@@ -241,6 +241,7 @@ class Aggregator(nn.Module):
                 return tokens.view(batch_size, num_frames, num_tokens, embed_dim)
             layout = dict(frames=num_frames, tokens_per_frame=num_tokens,
                           patch_token_start=self.patch_token_start, patch_hw=patch_hw)
+            precomputed_qkv = None
             unit_rows = None if self.sparse_convex_enabled else block.norm1_unit_rows(tokens)
             if unit_rows is not None:
                 normalized = None
@@ -270,10 +271,15 @@ class Aggregator(nn.Module):
                                 preserve_queries, preserve_keys)
                             self._sparse_convex_replayed += 1
                         else:
-                            plan = build_sparse_convex_plan(
+                            # The plan's size reaches the host by an asynchronous copy; the
+                            # qkv projection (independent of the plan) is enqueued before the
+                            # wait for it, so the GPU stays busy while the host sizes the plan.
+                            pending = start_sparse_convex_plan(
                                 normalized, threshold=self.sparse_convex_threshold,
                                 preserve_queries=preserve_queries,
                                 preserve_destination_keys=preserve_keys, **layout)
+                            precomputed_qkv = block.attn.qkv(attn_input)
+                            plan = pending.result()
                         if reuse_plan:
                             self._sparse_convex_reuse_plan = plan
                     self.sparse_convex_last_plan_stats.append({
@@ -297,7 +303,16 @@ class Aggregator(nn.Module):
                         "kept_tokens": plan.kept_tokens,
                         "merged_tokens": plan.original_tokens - plan.kept_tokens,
                         "merge_ratio": 1.0 - plan.keep_ratio, **plan.metadata})
-            tokens = block.forward_compacted(tokens, plan, normalized=attn_input)
+            if precomputed_qkv is None:
+                tokens = block.forward_compacted(tokens, plan, normalized=attn_input)
+            else:
+                # This layer's projection rides on the plan for this call only (a reused
+                # plan serves later layers with their own projections).
+                plan.precomputed_qkv = precomputed_qkv
+                try:
+                    tokens = block.forward_compacted(tokens, plan, normalized=attn_input)
+                finally:
+                    plan.precomputed_qkv = None
         return tokens.view(batch_size, num_frames, num_tokens, embed_dim)
 
 

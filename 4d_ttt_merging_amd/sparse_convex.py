@@ -122,6 +122,26 @@ def convex_fit(tokens: torch.Tensor, rows: torch.Tensor, supports: torch.Tensor,
     return fit, alpha
 
 
+class PendingSparseConvexPlan:
+    """A sparse-convex plan whose kernels are enqueued and whose size is on its way.
+
+    The plan's shapes depend on how many candidates merged, a count the
+    assemble kernel leaves on the device.  It travels to pinned host memory by
+    an asynchronous copy; `result()` waits for that copy alone (an event right
+    after it), so work enqueued on the stream in between -- the block's qkv
+    projection, say -- keeps the GPU busy while the host sizes the plan."""
+
+    def __init__(self, finish, stats_host: torch.Tensor, event: torch.cuda.Event):
+        self._finish, self._stats_host, self._event = finish, stats_host, event
+        self._plan = None
+
+    def result(self) -> WeightedBilinearTokenPlan:
+        if self._plan is None:
+            self._event.synchronize()
+            self._plan = self._finish(self._stats_host)
+        return self._plan
+
+
 @torch.no_grad()
 def build_sparse_convex_plan(
     tokens: torch.Tensor, *, frames: int, tokens_per_frame: int,
@@ -134,6 +154,22 @@ def build_sparse_convex_plan(
     `match_chunk_size` / `fit_chunk_size` are accepted for signature
     compatibility; the HIP kernels stream without chunk loops.
     """
+    return start_sparse_convex_plan(
+        tokens, frames=frames, tokens_per_frame=tokens_per_frame,
+        patch_token_start=patch_token_start, patch_hw=patch_hw, threshold=threshold,
+        preserve_queries=preserve_queries, match_chunk_size=match_chunk_size,
+        fit_chunk_size=fit_chunk_size, preserve_destination_keys=preserve_destination_keys).result()
+
+
+@torch.no_grad()
+def start_sparse_convex_plan(
+    tokens: torch.Tensor, *, frames: int, tokens_per_frame: int,
+    patch_token_start: int, patch_hw: tuple[int, int], threshold: float = .90,
+    preserve_queries: bool = False, match_chunk_size: int = FAST_MATCH_SOURCE_CHUNK,
+    fit_chunk_size: int = 16384, preserve_destination_keys: bool | None = None,
+) -> PendingSparseConvexPlan:
+    """build_sparse_convex_plan without waiting: enqueues every kernel of the plan and an
+    asynchronous copy of its four counts, and returns before the host has them."""
     del match_chunk_size, fit_chunk_size
     if tokens.shape[0] != 1:
         raise ValueError("sparse-convex compaction currently supports batch size one")
@@ -191,7 +227,23 @@ def build_sparse_convex_plan(
         top1.data_ptr(), float(easy_threshold), failed_count.data_ptr(), n_cand, total,
         float(threshold), keep_buf.data_ptr(), o2c.data_ptr(), source_buf.data_ptr(),
         parent_buf.data_ptr(), weight_buf.data_ptr(), stats.data_ptr(), stream))
-    merged, hard, fallback, fit_sum = (float(v) for v in stats.cpu())
+    stats_host = torch.empty(4, dtype=torch.float32, pin_memory=True)
+    stats_host.copy_(stats, non_blocking=True)
+    copied = torch.cuda.Event()
+    copied.record(torch.cuda.current_stream(device))
+
+    def finish(counts: torch.Tensor) -> WeightedBilinearTokenPlan:
+        return _finish_plan(counts, lay, total, keep_buf, o2c, source_buf, parent_buf, weight_buf,
+                            threshold, preserve_queries, preserve_destination_keys,
+                            (fit, alpha, support, top1, failed_list, failed_count))
+
+    return PendingSparseConvexPlan(finish, stats_host, copied)
+
+
+def _finish_plan(counts, lay, total, keep_buf, o2c, source_buf, parent_buf, weight_buf, threshold,
+                 preserve_queries, preserve_destination_keys, fit_state) -> WeightedBilinearTokenPlan:
+    """The plan over the assemble kernel's buffers, sized by its counts (host copy)."""
+    merged, hard, fallback, fit_sum = (float(v) for v in counts)
     m = int(merged)
     keep = keep_buf[:total - m].view(1, -1)
     source_original = source_buf[:m].view(1, -1)
@@ -203,7 +255,7 @@ def build_sparse_convex_plan(
         keep=keep, source_original=source_original,
         source_parent_compact=parent_compact,
         source_pool_weights=weights, source_restore_weights=weights,
-        original_tokens=total, normalizer=torch.empty(0, device=device),
+        original_tokens=total, normalizer=torch.empty(0, device=keep_buf.device),
         preserve_queries=preserve_queries,
         preserve_destination_keys=(
             preserve_queries if preserve_destination_keys is None else preserve_destination_keys
@@ -227,6 +279,6 @@ def build_sparse_convex_plan(
     mass, log_mass = plan.plan_mass()
     plan.normalizer = mass.view(1, -1, 1)
     plan.key_log_mass = log_mass.view(1, -1)
-    plan._derived["fit"] = (fit, alpha, support, top1, failed_list, failed_count)
+    plan._derived["fit"] = fit_state
     return plan
 

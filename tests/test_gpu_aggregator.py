@@ -75,20 +75,35 @@ def _configure(model, tag: str) -> None:
 
 
 class _Recorder:
-    """Records the plans the aggregator's planners return during one forward."""
+    """Records the plans the aggregator's planners return during one forward (built at
+    once, or started and then waited for)."""
 
     def __init__(self, monkeypatch):
         self.plans = []
         self.inputs = []
         agg = import_package("aggregator")
-        for name in ("build_fastvggt_plan", "build_sparse_convex_plan"):
+        recorder = self
+
+        class Pending:
+            def __init__(self, pending, tokens):
+                self.pending, self.tokens = pending, tokens
+
+            def result(self):
+                plan = self.pending.result()
+                recorder.plans.append(plan)
+                recorder.inputs.append(self.tokens)
+                return plan
+
+        for name in ("build_fastvggt_plan", "build_sparse_convex_plan", "start_sparse_convex_plan"):
             builder = getattr(agg, name)
 
-            def wrapped(*args, _builder=builder, **kwargs):
-                plan = _builder(*args, **kwargs)
-                self.plans.append(plan)
+            def wrapped(*args, _builder=builder, _name=name, **kwargs):
+                out = _builder(*args, **kwargs)
+                if _name.startswith("start_"):
+                    return Pending(out, args[0])
+                self.plans.append(out)
                 self.inputs.append(args[0])
-                return plan
+                return out
 
             monkeypatch.setattr(agg, name, wrapped)
 
