@@ -8,6 +8,7 @@ reference package `vggt_omega` for the merged global-attention path:
 * `TokenPlan`, `WeightedBilinearTokenPlan`, `deterministic_weighted_normalizer`,
   `build_fastvggt_plan`                  vggt_omega/models/token_merging.py
 * `build_sparse_convex_plan`             vggt_omega/models/sparse_convex.py
+  (`start_sparse_convex_plan`: the same without waiting for its sizes)
 * `streaming_top4`                       vggt_omega/models/sparse_convex_kernels.py
 * `SelfAttention`, `SelfAttentionBlock`  vggt_omega/models/layers/{attention,block}.py
 * `top4_project`                         the restore gather of the plans
@@ -29,7 +30,7 @@ from .gemm_tuning import use_tuned_gemms
 from .layers import LinearKMaskedBias, SelfAttention, SelfAttentionBlock
 from .mass_bias_attention import dense_attention, mass_bias_attention
 from .projection import top4_project
-from .sparse_convex import build_sparse_convex_plan, convex_fit
+from .sparse_convex import build_sparse_convex_plan, convex_fit, start_sparse_convex_plan
 from .sparse_convex_kernels import streaming_top4
 from .token_merging import (
     TokenPlan,
@@ -52,6 +53,7 @@ __all__ = [
     "mass_bias_attention",
     "ops",
     "plan_io",
+    "start_sparse_convex_plan",
     "streaming_top4",
     "top4_project",
     "use_tuned_gemms",

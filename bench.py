@@ -663,6 +663,36 @@ def only_workload(which: str) -> int:
         print(json.dumps({"workload": "gather", **gather_ceiling(device, 3)}), flush=True)
         return 0
     vgo = importlib.import_module("4d_ttt_merging_amd")
+    if which == "similarity":
+        # The C4 matcher problem (23,808 source rows x 8,960 dictionary rows x 1,024,
+        # unit rows, top-1), then the plain bf16 GEMM of the same shape through
+        # torch.mm (hipBLASLt), which writes the 427 MB score matrix instead of
+        # selecting from it: three launches each, timed with events.
+        kernels = importlib.import_module("4d_ttt_merging_amd._kernels")
+        g = torch.Generator(device=device).manual_seed(5)
+        ns, nd = 23808, 8960
+        src = torch.nn.functional.normalize(torch.randn(ns, DIM, device=device, generator=g), dim=-1).bfloat16()
+        dic = torch.nn.functional.normalize(torch.randn(nd, DIM, device=device, generator=g), dim=-1).bfloat16()
+        scores = torch.empty(ns, nd, device=device, dtype=torch.bfloat16)
+        flop = 2 * ns * nd * DIM
+        result = {"workload": "similarity", "n_src": ns, "n_dict": nd, "dim": DIM, "flop": flop}
+        for name, fn in (("similarity_top1", lambda: kernels.similarity_topk(src, dic, 1)),
+                         ("hipblaslt_mm", lambda: torch.mm(src, dic.t(), out=scores))):
+            fn()
+            torch.cuda.synchronize()
+            times = []
+            for _ in range(3):
+                begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                begin.record()
+                fn()
+                end.record()
+                end.synchronize()
+                times.append(begin.elapsed_time(end))
+            ms = min(times)
+            result[name] = {"ms": round(ms, 4), "tflops": round(flop / ms / 1e9, 1),
+                            "frac": round(flop / ms / 1e9 / PEAK_BF16_TFLOPS, 4)}
+        print(json.dumps(result), flush=True)
+        return 0
     if which == "projection":
         # BASELINE config 2, bf16: 1,048,576 rows from a 65,536-row table.
         n, m, d = 1 << 20, 65536, DIM
@@ -728,13 +758,15 @@ def main() -> int:
     ap.add_argument("--aggregator-only", action="store_true",
                     help="time the C4 aggregator and print its line without the other legs "
                          "(for kernel traces of the forward alone)")
-    ap.add_argument("--only", choices=("attention", "projection", "merge", "copy", "gather"), default=None,
+    ap.add_argument("--only", choices=("attention", "projection", "merge", "copy", "gather", "similarity"), default=None,
                     help="run one kernel workload for rocprofv3 counter passes, then exit: "
                          "'attention' = 3 C4-size mass-bias attention launches, 'projection' = 3 "
                          "C2 bf16 top-4 projections, 'merge' = 3 x (norm1 unit rows, FastVGGT plan, "
                          "q/k/v compaction) of a C4 global block, 'copy' = 3 plain 256 MiB device "
                          "copies (the FETCH_SIZE / WRITE_SIZE calibration), 'gather' = the random-row "
-                         "gather ceiling probe (torch index_select, 4 / 32 / 512 MB tables)")
+                         "gather ceiling probe (torch index_select, 4 / 32 / 512 MB tables), "
+                         "'similarity' = 3 C4 matcher top-1 launches and 3 torch.mm (hipBLASLt) "
+                         "GEMMs of the same shape")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
