@@ -351,6 +351,47 @@ def _residual_layer_norm_impl(x: torch.Tensor, branch: torch.Tensor | None = Non
     return total, normed, normed32
 
 
+def _restore_residual_layer_norm_impl(x: torch.Tensor, table: torch.Tensor, index: torch.Tensor,
+                                      weight: torch.Tensor, gamma: torch.Tensor | None,
+                                      norm: tuple[torch.Tensor | None, torch.Tensor | None, float],
+                                      norm_dtype: torch.dtype):
+    """One pass over fp32 rows x [N, dim] with the branch restored from `table` on the fly:
+    branch = top4_project(table, index, weight) (same rounding), s = x + gamma * branch,
+    n = LayerNorm(s) in `norm_dtype`.  Returns (s, n)."""
+    lib = _lib.load()
+    _lib.require_gpu(x, table, index, weight, gamma)
+    if x.dtype != torch.float32:
+        raise ValueError("restore_residual_layer_norm: x must be float32")
+    dim = x.shape[-1]
+    rows = x.reshape(-1, dim)
+    n = rows.shape[0]
+    if table.ndim != 2 or table.shape[1] != dim:
+        raise ValueError(f"restore_residual_layer_norm: table {tuple(table.shape)} must be [M, {dim}]")
+    if index.shape != (n, 4) or weight.shape != (n, 4):
+        raise ValueError("restore_residual_layer_norm: index and weight must be [rows, 4]")
+    if index.dtype != torch.int32 or weight.dtype != torch.float32:
+        raise ValueError("restore_residual_layer_norm: int32 indices and float32 weights")
+    if norm_dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("restore_residual_layer_norm: norm_dtype must be bfloat16 or float16")
+    index, weight = index.contiguous(), weight.contiguous()
+    if table.stride(-1) != 1:
+        table = table.contiguous()
+    w, b, eps = norm
+    w = None if w is None else w.detach().to(torch.float32).contiguous()
+    b = None if b is None else b.detach().to(torch.float32).contiguous()
+    if gamma is not None:
+        gamma = gamma.detach().to(torch.float32).contiguous()
+    total = torch.empty_like(x, memory_format=torch.contiguous_format)
+    normed = torch.empty(x.shape, device=x.device, dtype=norm_dtype)
+    status = lib.vgo_restore_residual_layer_norm(
+        rows.data_ptr(), rows.stride(0), table.data_ptr(), table.stride(0), table.shape[0],
+        _lib.dtype_code(table.dtype), index.data_ptr(), weight.data_ptr(), _c(gamma), _c(w), _c(b),
+        float(eps), n, dim, total.data_ptr(), dim, normed.data_ptr(), dim,
+        _lib.dtype_code(norm_dtype), _lib.stream_of(x))
+    _lib.check(status)
+    return total, normed
+
+
 # --------------------------------------------- operator-backed entry points ----
 def compact_into(x: torch.Tensor, out: torch.Tensor, *, base_rows: torch.Tensor | None,
                  offsets: torch.Tensor, segs_per_row: int, items: torch.Tensor | None,
@@ -410,3 +451,16 @@ def residual_layer_norm(x: torch.Tensor, branch: torch.Tensor | None = None,
     if unit_eps is not None:
         return total, normed, normed32, outs[3]
     return total, normed, normed32
+
+
+def restore_residual_layer_norm(x: torch.Tensor, table: torch.Tensor, index: torch.Tensor,
+                                weight: torch.Tensor, gamma: torch.Tensor | None,
+                                norm: tuple[torch.Tensor | None, torch.Tensor | None, float], *,
+                                norm_dtype: torch.dtype = torch.bfloat16):
+    """The residual-row pass with the plan restore fused in
+    (torch.ops.vgo.restore_residual_layer_norm); see _restore_residual_layer_norm_impl.
+    Returns (s, n)."""
+    w, b, eps = norm
+    total, normed = torch.ops.vgo.restore_residual_layer_norm(x, table, index, weight, gamma, w, b,
+                                                              float(eps), norm_dtype)
+    return total, normed

@@ -124,6 +124,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_p, _c_i64, _c_p, _c_i64, _c_int, _c_p, _c_p, _c_p, _c_f32, _c_i64, _c_i64, _c_p, _c_i64,
         _c_p, _c_i64, _c_int, _c_p, _c_i64, _c_p, _c_i64, _c_f32, _c_p,
     ]),
+    "vgo_restore_residual_layer_norm": (_c_int, [
+        _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_p, _c_p, _c_p, _c_f32, _c_i64,
+        _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_int, _c_p,
+    ]),
 }
 
 _lock = threading.Lock()

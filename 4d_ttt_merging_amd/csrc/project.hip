@@ -35,24 +35,6 @@ struct Vec16<f16_t> {
   static constexpr int n = 8;
 };
 
-template <typename T>
-__device__ __forceinline__ float weight_as_value(float w) {
-  return to_f32(from_f32<T>(w));
-}
-template <>
-__device__ __forceinline__ float weight_as_value<float>(float w) {
-  return w;
-}
-
-// Product rounded to the value type (bf16/f16 multiply semantics), fp32 as is.
-template <typename T>
-__device__ __forceinline__ float rounded_product(float y, float w) {
-  return to_f32(from_f32<T>(y * w));
-}
-template <>
-__device__ __forceinline__ float rounded_product<float>(float y, float w) {
-  return y * w;
-}
 
 // Persistent waves: each wave owns R consecutive output rows per step and issues
 // the gathers of all R rows (4 corners x CH 16-byte chunks per lane each) before

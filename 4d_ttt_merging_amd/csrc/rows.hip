@@ -24,6 +24,14 @@
 // 4(l + 64i) + 3, so each load or store instruction of a wave covers one
 // contiguous 1 KB (fp32) or 512 B (16-bit) span.  HBM-bound: per row it reads
 // 4*dim (x) + s_b*dim (branch) and writes 4*dim (s) + s_n*dim (n).
+//
+// Restore variant (vgo_restore_residual_layer_norm): the branch row is the
+// merge plan's restore of the attention output, branch[r,:] =
+// sum_c w[r,c] * table[index[r,c],:] rounded as the projection kernel rounds it
+// (token_merging.py:387-414, 193-196: weight and each product in the value type,
+// fp32 sum, result in the value type), so the restored rows never go to memory:
+// the row's (index, weight) is loaded first, the table rows of its non-zero
+// weights next, under the loads of x and the parameter vectors.
 #include "vgo_common.h"
 
 namespace vgo {
@@ -62,13 +70,26 @@ struct RowArgs {
   void* unit;
   int64_t unit_stride;
   float unit_eps;
+  // Restore variant: branch is the [table_rows, dim] table, branch_stride its row stride.
+  const int32_t* r_index;  // [rows, 4]
+  const float* r_weight;   // [rows, 4]
+  int64_t table_rows;
 };
 
-template <int kChunks, bool kBranch, typename TB, typename TN>
+template <int kChunks, bool kBranch, bool kGather, typename TB, typename TN>
 __global__ __launch_bounds__(256) void residual_ln_kernel(RowArgs a) {
   const int lane = lane_id();
-  const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 +
+                    __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   if (r >= a.rows) return;
+  // The restore map of the row goes out before everything else: only the
+  // table loads wait for it.
+  i32x4 id4 = {0, 0, 0, 0};
+  f32x4 w4 = {0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (kGather) {
+    id4 = *reinterpret_cast<const i32x4*>(a.r_index + 4 * r);
+    w4 = *reinterpret_cast<const f32x4*>(a.r_weight + 4 * r);
+  }
   const int chunks = a.dim >> 2;
   // Every load is unconditional, so one wait covers them all: a lane's chunk
   // offset is clamped into the row and chunks past its end are zeroed after
@@ -90,17 +111,57 @@ __global__ __launch_bounds__(256) void residual_ln_kernel(RowArgs a) {
 #pragma unroll
   for (int i = 0; i < kChunks; ++i) v[i] = *reinterpret_cast<const f32x4*>(xr + off[i]);
   if constexpr (kBranch) {
-    const TB* br = static_cast<const TB*>(a.branch) + r * a.branch_stride;
     f32x4 b[kChunks], g[kChunks];
+    if constexpr (!kGather) {
+      const TB* br = static_cast<const TB*>(a.branch) + r * a.branch_stride;
 #pragma unroll
-    for (int i = 0; i < kChunks; ++i) {
-      b[i] = load4(br + off[i]);
-      g[i] = *reinterpret_cast<const f32x4*>(gp + off[i]);
+      for (int i = 0; i < kChunks; ++i) b[i] = load4(br + off[i]);
     }
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) g[i] = *reinterpret_cast<const f32x4*>(gp + off[i]);
 #pragma unroll
     for (int i = 0; i < kChunks; ++i) {
       w[i] = *reinterpret_cast<const f32x4*>(wp + off[i]);
       bias[i] = *reinterpret_cast<const f32x4*>(bp + off[i]);
+    }
+    if constexpr (kGather) {
+      // Table rows of the non-zero weights, raw, all requested before any is
+      // used; an out-of-range id with a non-zero weight makes the row NaN, as
+      // in the projection kernel (the table is never read out of range).
+      typedef typename Vec4<TB>::type Raw;
+      Raw y[4][kChunks];
+      bool use[4];
+      bool bad = false;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        use[c] = w4[c] != 0.0f;
+        if (use[c] && static_cast<uint32_t>(id4[c]) >= static_cast<uint64_t>(a.table_rows)) {
+          bad = true;
+          use[c] = false;
+        }
+        if (use[c]) {
+          const TB* tr = static_cast<const TB*>(a.branch) + static_cast<int64_t>(id4[c]) * a.branch_stride;
+#pragma unroll
+          for (int i = 0; i < kChunks; ++i) y[c][i] = *reinterpret_cast<const Raw*>(tr + off[i]);
+        }
+      }
+      f32x4 acc[kChunks];
+#pragma unroll
+      for (int i = 0; i < kChunks; ++i) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (!use[c]) continue;
+        const float wq = weight_as_value<TB>(w4[c]);
+#pragma unroll
+        for (int i = 0; i < kChunks; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j] = acc[i][j] + rounded_product<TB>(to_f32(y[c][i][j]), wq);
+      }
+      // The restored element in the value type, widened again as the branch.
+#pragma unroll
+      for (int i = 0; i < kChunks; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) b[i][j] = to_f32(from_f32<TB>(bad ? __builtin_nanf("") : acc[i][j]));
     }
     // Empty asm reading the loaded registers: the loads that are only used
     // under a NULL test cannot sink into that branch behind a wait of their own.
@@ -169,14 +230,14 @@ __global__ __launch_bounds__(256) void residual_ln_kernel(RowArgs a) {
     if (live[i]) store4(uo + off[i], v[i] / denom);
 }
 
-template <bool kBranch, typename TB, typename TN>
+template <bool kBranch, typename TB, typename TN, bool kGather = false>
 int launch_rows(const RowArgs& a, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>((a.rows + 3) / 4));
   if (a.dim <= 4 * 64 * 4)
-    hipLaunchKernelGGL((residual_ln_kernel<4, kBranch, TB, TN>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((residual_ln_kernel<4, kBranch, kGather, TB, TN>), grid, dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL((residual_ln_kernel<kRowChunks, kBranch, TB, TN>), grid, dim3(256), 0, s, a);
-  return check_launch("residual_layer_norm");
+    hipLaunchKernelGGL((residual_ln_kernel<kRowChunks, kBranch, kGather, TB, TN>), grid, dim3(256), 0, s, a);
+  return check_launch(kGather ? "restore_residual_layer_norm" : "residual_layer_norm");
 }
 
 template <typename TN>
@@ -187,6 +248,16 @@ int dispatch_branch(const RowArgs& a, int branch_dtype, hipStream_t s) {
     case VGO_F16: return launch_rows<true, f16_t, TN>(a, s);
     case VGO_F32: return launch_rows<true, float, TN>(a, s);
     default: return fail(VGO_EINVAL, "residual_layer_norm: unsupported branch dtype");
+  }
+}
+
+template <typename TN>
+int dispatch_restore(const RowArgs& a, int table_dtype, hipStream_t s) {
+  switch (table_dtype) {
+    case VGO_BF16: return launch_rows<true, bf16_t, TN, true>(a, s);
+    case VGO_F16: return launch_rows<true, f16_t, TN, true>(a, s);
+    case VGO_F32: return launch_rows<true, float, TN, true>(a, s);
+    default: return fail(VGO_EINVAL, "restore_residual_layer_norm: unsupported table dtype");
   }
 }
 
@@ -233,8 +304,46 @@ extern "C" int vgo_residual_layer_norm(const float* x, int64_t x_row_stride, con
               "residual_layer_norm: zero x_out row stride");
   RowArgs a{x, x_row_stride, branch, branch_row_stride, gamma, ln_weight, ln_bias, eps, rows,
             static_cast<int>(dim), x_out, x_out_row_stride, norm_out, norm_row_stride, norm_f32,
-            norm_f32_row_stride, unit_out, unit_row_stride, unit_eps};
+            norm_f32_row_stride, unit_out, unit_row_stride, unit_eps, nullptr, nullptr, 0};
   hipStream_t s = as_stream(stream);
   if (norm_out && norm_dtype == VGO_F16) return dispatch_branch<f16_t>(a, branch_dtype, s);
   return dispatch_branch<bf16_t>(a, branch_dtype, s);
+}
+
+extern "C" int vgo_restore_residual_layer_norm(
+    const float* x, int64_t x_row_stride, const void* table, int64_t table_row_stride,
+    int64_t table_rows, int table_dtype, const int32_t* index, const float* weight,
+    const float* gamma, const float* ln_weight, const float* ln_bias, float eps, int64_t rows,
+    int64_t dim, float* x_out, int64_t x_out_row_stride, void* norm_out, int64_t norm_row_stride,
+    int norm_dtype, void* stream) {
+  using namespace vgo;
+  VGO_REQUIRE(rows >= 0 && dim >= 0 && table_rows >= 0, "restore_residual_layer_norm: negative size");
+  if (rows == 0 || dim == 0) return VGO_OK;
+  VGO_REQUIRE(x && table && index && weight, "restore_residual_layer_norm: null input");
+  VGO_REQUIRE(x_out || norm_out, "restore_residual_layer_norm: no output");
+  VGO_REQUIRE(dim % 4 == 0 && dim <= 4 * 64 * kRowChunks,
+              "restore_residual_layer_norm: dim must be a multiple of 4 and at most 2048");
+  VGO_REQUIRE(rows < (int64_t(1) << 33) && table_rows < (int64_t(1) << 31),
+              "restore_residual_layer_norm: too many rows");
+  VGO_REQUIRE(norm_dtype == VGO_BF16 || norm_dtype == VGO_F16 || !norm_out,
+              "restore_residual_layer_norm: norm_out must be bf16 or f16");
+  VGO_REQUIRE(table_dtype == VGO_BF16 || table_dtype == VGO_F16 || table_dtype == VGO_F32,
+              "restore_residual_layer_norm: unsupported table dtype");
+  auto vec_ok = [](const void* p, int64_t stride, size_t elem) {
+    return !p || (aligned(p, 4 * elem) && stride % 4 == 0);
+  };
+  VGO_REQUIRE(vec_ok(x, x_row_stride, 4) && vec_ok(x_out, x_out_row_stride, 4) &&
+                  vec_ok(table, table_row_stride, dtype_bytes(table_dtype)) &&
+                  vec_ok(norm_out, norm_row_stride, 2) && vec_ok(gamma, 0, 4) &&
+                  vec_ok(ln_weight, 0, 4) && vec_ok(ln_bias, 0, 4) && vec_ok(index, 0, 4) &&
+                  vec_ok(weight, 0, 4),
+              "restore_residual_layer_norm: pointers must be 4-element aligned and row strides multiples of 4");
+  VGO_REQUIRE(!x_out || x_out == x || x_out_row_stride != 0,
+              "restore_residual_layer_norm: zero x_out row stride");
+  RowArgs a{x, x_row_stride, table, table_row_stride, gamma, ln_weight, ln_bias, eps, rows,
+            static_cast<int>(dim), x_out, x_out_row_stride, norm_out, norm_row_stride, nullptr, 0,
+            nullptr, 0, 0.0f, index, weight, table_rows};
+  hipStream_t s = as_stream(stream);
+  if (norm_out && norm_dtype == VGO_F16) return dispatch_restore<f16_t>(a, table_dtype, s);
+  return dispatch_restore<bf16_t>(a, table_dtype, s);
 }

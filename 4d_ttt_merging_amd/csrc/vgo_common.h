@@ -104,6 +104,27 @@ struct Vec4<f16_t> {
   using type = f16x4;
 };
 
+// A restore weight as the value type sees it: `w.to(value.dtype)` in the
+// reference's projection (token_merging.py:408-413); fp32 values keep it.
+template <typename T>
+__device__ __forceinline__ float weight_as_value(float w) {
+  return to_f32(from_f32<T>(w));
+}
+template <>
+__device__ __forceinline__ float weight_as_value<float>(float w) {
+  return w;
+}
+
+// Product rounded to the value type (bf16/f16 multiply semantics), fp32 as is.
+template <typename T>
+__device__ __forceinline__ float rounded_product(float y, float w) {
+  return to_f32(from_f32<T>(y * w));
+}
+template <>
+__device__ __forceinline__ float rounded_product<float>(float y, float w) {
+  return y * w;
+}
+
 template <typename T>
 __device__ __forceinline__ f32x4 load4(const T* p) {
   const typename Vec4<T>::type v = *reinterpret_cast<const typename Vec4<T>::type*>(p);

@@ -150,6 +150,13 @@ class SelfAttention(nn.Module):
             qkv = self.qkv(x)
             return self.proj_drop(self.proj(self.compute_attention(qkv=qkv, attn_bias=attn_bias,
                                                                    rope=rope)))
+        x = self._forward_merged(x, attn_bias, rope, token_plan)
+        with profiling.span("global.update_restore"):
+            return token_plan.restore(x)
+
+    def _forward_merged(self, x: Tensor, attn_bias, rope, token_plan) -> Tensor:
+        """The merged forward up to the output projection: attention.py:284-303 without
+        the final `token_plan.restore`, which the caller applies (or fuses)."""
         with profiling.span("global.qkv_projection"):
             qkv = (token_plan.precomputed_qkv
                    if getattr(token_plan, "precomputed_qkv", None) is not None else self.qkv(x))
@@ -159,8 +166,7 @@ class SelfAttention(nn.Module):
         if (getattr(token_plan, "source_query_correction", False)
                 and not getattr(token_plan, "preserve_queries", False)):
             raise NotImplementedError("source-query correction is outside the merged path")
-        with profiling.span("global.update_restore"):
-            return token_plan.restore(x)
+        return x
 
     # ---------------------------------------------------------------------
     def _attention_dtype(self, qkv: Tensor) -> torch.dtype:
@@ -414,7 +420,15 @@ class SelfAttentionBlock(nn.Module):
         if normalized is None:
             normalized = self._norm1_input(x) if self._fused_rows(x) else self.norm1(x)
         if self._fused_rows(x):
-            return self._fused_tail(x, self.attn(normalized, token_plan=token_plan))
+            self.attn._check_hooks()
+            y = self.attn._forward_merged(normalized, None, None, token_plan)
+            restore_map_for = getattr(token_plan, "restore_map_for", None)
+            restore_map = restore_map_for(y) if restore_map_for is not None else None
+            if restore_map is None:
+                with profiling.span("global.update_restore"):
+                    y = token_plan.restore(y)
+                return self._fused_tail(x, y)
+            return self._fused_restore_tail(x, y[0], *restore_map)
         x_attn = x + self.ls1(self.attn(normalized, token_plan=token_plan))
         return x_attn + self.ls2(self.mlp(self.norm2(x_attn)))
 
@@ -466,6 +480,18 @@ class SelfAttentionBlock(nn.Module):
 
     def _norm1_input(self, x: Tensor) -> Tensor:
         return _kernels.residual_layer_norm(x, norm=_ln_args(self.norm1), norm_dtype=_autocast_dtype())[1]
+
+    def _fused_restore_tail(self, x: Tensor, table: Tensor, index: Tensor, weight: Tensor) -> Tensor:
+        """_fused_tail of the plan's restore of `table` (the merged rows): the first row
+        pass projects each row's parents itself, so the restored rows never go to memory.
+        The `global.update_restore` label then spans restore, residual add and norm2."""
+        with profiling.span("global.update_restore"):
+            x_attn, h = _kernels.restore_residual_layer_norm(
+                x, table, index, weight, _ls_gamma(self.ls1), _ln_args(self.norm2),
+                norm_dtype=_autocast_dtype())
+        out, _, _ = _kernels.residual_layer_norm(x_attn, self.mlp(h).reshape(x.shape),
+                                                 _ls_gamma(self.ls2))
+        return out
 
     def _fused_tail(self, x: Tensor, y: Tensor) -> Tensor:
         """x_attn = x + ls1(y); return x_attn + ls2(mlp(norm2(x_attn))) with two row passes."""

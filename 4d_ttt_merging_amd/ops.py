@@ -15,7 +15,9 @@ dispatcher, `torch.compile` and fake-tensor tracing see them as single ops:
 * `vgo::qkv_epilogue` -- the packed projection split into head-major q/k/v with
   LayerNorm64 and RoPE (layers/attention.py:243-262, 334-341);
 * `vgo::residual_layer_norm` -- LayerScale, residual add, LayerNorm and the
-  autocast cast of a block (layers/block.py:126-127, 219-226).
+  autocast cast of a block (layers/block.py:126-127, 219-226);
+  `vgo::restore_residual_layer_norm` -- the same with the plan restore
+  (token_merging.py:387-414, 193-196) computed in the pass.
 
 Each has a CUDA (HIP) implementation that calls `libvgo.so` through its C ABI
 and a fake implementation that only describes the outputs (for tracing).
@@ -197,3 +199,19 @@ def _(x, branch, gamma, ln_weight, ln_bias, eps, has_norm, write_sum, norm_dtype
     normed32 = x.new_empty(x.shape) if has_norm and norm_f32 else empty
     unit = x.new_empty(x.shape, dtype=norm_dtype) if unit_eps >= 0 and norm_dtype is not None else empty
     return [total, normed, normed32, unit]
+
+
+@torch.library.custom_op("vgo::restore_residual_layer_norm", mutates_args=(), device_types="cuda")
+def restore_residual_layer_norm(x: Tensor, table: Tensor, index: Tensor, weight: Tensor,
+                                gamma: Optional[Tensor], ln_weight: Optional[Tensor],
+                                ln_bias: Optional[Tensor], eps: float,
+                                norm_dtype: torch.dtype) -> List[Tensor]:
+    """[x + gamma * restore(table), LN of that in norm_dtype] with restore = the top-4
+    projection of `table` by (index, weight), never written to memory."""
+    return list(_kernels._restore_residual_layer_norm_impl(x, table, index, weight, gamma,
+                                                           (ln_weight, ln_bias, eps), norm_dtype))
+
+
+@restore_residual_layer_norm.register_fake
+def _(x, table, index, weight, gamma, ln_weight, ln_bias, eps, norm_dtype):
+    return [x.new_empty(x.shape), x.new_empty(x.shape, dtype=norm_dtype)]

@@ -154,6 +154,15 @@ class TokenPlan:
         """Members per compact token (float32 [K]) in batch element b."""
         return self._cluster_csr(b)[1]
 
+    def restore_map_for(self, value: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor] | None:
+        """(index [N, 4] int32, weight [N, 4] float32) with which `restore(value)` projects
+        value[0], for a caller that fuses the restore into its next pass; None when restore
+        returns `value` itself or value holds more than one batch element."""
+        if self.kept_tokens == self.original_tokens or value.shape[0] != 1:
+            return None
+        _check_value(value)
+        return self._restore_map(0)
+
     def compact(self, value: torch.Tensor, *, merge: bool = True) -> torch.Tensor:
         if self.kept_tokens == self.original_tokens:
             return value
@@ -372,6 +381,23 @@ class WeightedBilinearTokenPlan:
         for b in range(value.shape[0]):
             top4_project(_as_rows(value[b]), index, weight, out=out[b])
         return out
+
+    def restore_map_for(self, value: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor] | None:
+        """(index [N, 4] int32, weight [N, 4] float32) with which `restore(value)` projects
+        value[0], for a caller that fuses the restore into its next pass; None when restore
+        returns `value` itself, raises, or value holds more than one batch element (then
+        call `restore`)."""
+        if value.shape[0] != 1:
+            return None
+        if self.preserve_queries and value.shape[1] == self.original_tokens:
+            return None
+        if self.query_keep is not None:
+            _check_value(value)
+            return self._restore_map(True)
+        if self.preserve_queries:
+            return None
+        _check_value(value)
+        return self._restore_map(False)
 
     def restore(self, value: torch.Tensor) -> torch.Tensor:
         """Broadcast physical outputs and bilinearly recover source outputs."""

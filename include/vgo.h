@@ -404,6 +404,30 @@ int vgo_residual_layer_norm(const float* x, int64_t x_row_stride, const void* br
                             int64_t norm_f32_row_stride, void* unit_out, int64_t unit_row_stride,
                             float unit_eps, void* stream);
 
+/*
+ * The same row pass with the branch row restored from a merge plan's output
+ * in the pass itself (the restored rows never go to memory):
+ *   branch[r,:] = sum_{c<4} weight[r,c] * table[index[r,c],:]
+ * rounded as vgo_top4_project rounds it (weight and each product in the table
+ * dtype, fp32 sum in corner order, result in the table dtype; zero weights
+ * skip their row; an out-of-range index with a non-zero weight gives a NaN
+ * row), then s = x + gamma * branch and LN(s) as in vgo_residual_layer_norm.
+ * table: [table_rows, dim] rows of table_dtype (bf16, f16 or fp32) with
+ * table_row_stride; index int32 [rows, 4] and weight fp32 [rows, 4], contiguous
+ * and 16-byte aligned (the plan's restore map, vgo_restore_map).  x_out and
+ * norm_out as above (at least one).  Replaces the plan restore
+ * (vggt_omega/models/token_merging.py:387-414, 193-196) together with the
+ * LayerScale, residual add and norm2 that follow it in forward_compacted
+ * (layers/block.py:219-226, layers/attention.py:303).
+ */
+int vgo_restore_residual_layer_norm(const float* x, int64_t x_row_stride, const void* table,
+                                    int64_t table_row_stride, int64_t table_rows, int table_dtype,
+                                    const int32_t* index, const float* weight, const float* gamma,
+                                    const float* ln_weight, const float* ln_bias, float eps,
+                                    int64_t rows, int64_t dim, float* x_out,
+                                    int64_t x_out_row_stride, void* norm_out,
+                                    int64_t norm_row_stride, int norm_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -21,6 +21,7 @@ OPS = {
     "top4_project": "vgo::top4_project(Tensor table, Tensor index, Tensor weight) -> Tensor",
     "attention_into": None, "attention_pair_into": None, "top4_project_into": None,
     "compact_into": None, "compact_multi_into": None, "qkv_epilogue": None, "residual_layer_norm": None,
+    "restore_residual_layer_norm": None,
 }
 
 
@@ -56,6 +57,11 @@ def test_fake_implementations_describe_outputs():
             x, x.bfloat16(), None, None, None, 1e-5, True, True, torch.bfloat16, False, 1e-12)
         assert total.shape == x.shape and norm.dtype == torch.bfloat16 and norm32.numel() == 0
         assert unit.shape == x.shape
+        s, n = torch.ops.vgo.restore_residual_layer_norm(
+            x, torch.empty(4, 256, dtype=torch.bfloat16, device="cuda"),
+            torch.empty(10, 4, dtype=torch.int32, device="cuda"), torch.empty(10, 4, device="cuda"),
+            None, None, None, 1e-5, torch.bfloat16)
+        assert s.shape == x.shape and s.dtype == torch.float32 and n.dtype == torch.bfloat16
 
 
 @pytest.mark.gpu

@@ -11,6 +11,10 @@
 * SelfAttentionBlock.forward and forward_compacted with the fused rows match
   the reference op sequence (torch LayerNorm, LayerScale, add, autocast casts)
   within the bf16 bar.
+* The restore variant (vgo_restore_residual_layer_norm) equals the plan's
+  top-4 projection followed by the plain row pass bit for bit (one-hot and
+  four-way weights, zero weights, out-of-range ids giving NaN rows, three table
+  dtypes), and forward_compacted through it equals the unfused restore + rows.
 """
 from __future__ import annotations
 
@@ -156,6 +160,83 @@ def test_block_forward_compacted_fused_rows_match_reference(vgo, device):
         _reference_rows(block)
         ref = block.forward_compacted(x, plan, normalized=block.norm1(x))
     assert_close(fused.cpu(), ref.cpu(), torch.bfloat16, what="forward_compacted")
+
+
+def _restore_inputs(n, m, dim, table_dtype, mode, seed):
+    g = torch.Generator().manual_seed(seed)
+    table = (torch.randn(m, dim, generator=g) * 1.5).to(table_dtype)
+    index = torch.randint(0, m, (n, 4), generator=g, dtype=torch.int32)
+    if mode == "one_hot":
+        weight = torch.zeros(n, 4)
+        weight[:, 0] = 1.0
+    else:
+        weight = torch.rand(n, 4, generator=g)
+        weight[torch.rand(n, 4, generator=g) < 0.3] = 0.0      # skipped corners
+        weight[::7] = 0.0                                      # rows with no parent at all
+        weight = weight / weight.sum(1, keepdim=True).clamp_min(1e-6)
+        index[3, 2], weight[3, 2] = m + 5, 0.25                # out of range, used: NaN row
+        index[5, 1], weight[5, 1] = -2, 0.0                    # out of range, unused: ignored
+    return table, index, weight
+
+
+@pytest.mark.parametrize("n,m,dim,table_dtype,norm_dtype,mode", [
+    (1029, 517, 1024, torch.bfloat16, torch.bfloat16, "one_hot"),
+    (1029, 517, 1024, torch.bfloat16, torch.bfloat16, "four"),
+    (333, 1000, 260, torch.float16, torch.float16, "four"),
+    (77, 40, 2048, torch.float32, torch.bfloat16, "four"),
+    (5, 3, 1536, torch.bfloat16, torch.float16, "one_hot"),
+])
+def test_restore_residual_layer_norm_equals_projection_then_rows(kern, device, n, m, dim, table_dtype,
+                                                                  norm_dtype, mode):
+    print(f"[rows] restore+residual+LN n={n} m={m} dim={dim} {table_dtype} {mode}", flush=True)
+    proj = import_package("projection")
+    table, index, weight = _restore_inputs(n, m, dim, table_dtype, mode, n + m + dim)
+    x, _, gamma, w, b = _inputs(n, dim, torch.float32, n * 3 + dim)
+    x, gamma, w, b = x.to(device), gamma.to(device), w.to(device), b.to(device)
+    table, index, weight = table.to(device), index.to(device), weight.to(device)
+    for g_, aff in ((gamma, (w, b, 1e-5)), (None, (None, None, 1e-6))):
+        restored = proj.top4_project(table, index, weight)
+        ref_s, ref_n, _ = kern.residual_layer_norm(x, restored, g_, aff, norm_dtype=norm_dtype)
+        s, nrm = kern.restore_residual_layer_norm(x, table, index, weight, g_, aff, norm_dtype=norm_dtype)
+        torch.testing.assert_close(s, ref_s, rtol=0, atol=0, equal_nan=True)
+        torch.testing.assert_close(nrm, ref_n, rtol=0, atol=0, equal_nan=True)
+    if mode == "four":
+        assert torch.isnan(s[3]).all() and not torch.isnan(s[5]).any()
+
+
+def test_restore_residual_layer_norm_rejects_bad_arguments(kern, device):
+    print("[rows] restore+residual argument checks", flush=True)
+    x = torch.zeros(8, 64, device=device)
+    table = torch.zeros(4, 64, device=device, dtype=torch.bfloat16)
+    index = torch.zeros(8, 4, device=device, dtype=torch.int32)
+    weight = torch.zeros(8, 4, device=device)
+    with pytest.raises(ValueError):
+        kern.restore_residual_layer_norm(x, table, index[:7], weight[:7], None, (None, None, 1e-5))
+    with pytest.raises(ValueError):
+        kern.restore_residual_layer_norm(x, table[:, :32], index, weight, None, (None, None, 1e-5))
+    with pytest.raises(ValueError):
+        kern.restore_residual_layer_norm(x, table, index.long(), weight, None, (None, None, 1e-5))
+
+
+@pytest.mark.parametrize("planner", ["fastvggt", "sparse_convex"])
+def test_block_forward_compacted_fused_restore_equals_unfused(vgo, device, planner):
+    """forward_compacted restores inside the first row pass; the result equals the plan's
+    restore followed by the plain fused rows, bit for bit."""
+    print(f"[rows] forward_compacted fused restore ({planner})", flush=True)
+    block = _block(vgo, device, 17)
+    x = structured_tokens(18, 4, (16, 16), 5, 256).to(device)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        normalized, attn_input = block.norm1_for_plan(x)
+        if planner == "fastvggt":
+            plan = vgo.build_fastvggt_plan(normalized, merge_ratio=0.5, protect_ratio=0.0,
+                                           mass_bias=True, **KW)
+        else:
+            plan = vgo.build_sparse_convex_plan(normalized, threshold=0.9, **KW)
+        y = block.attn._forward_merged(attn_input, None, None, plan)
+        assert plan.restore_map_for(y) is not None
+        unfused = block._fused_tail(x, plan.restore(y))
+        fused = block.forward_compacted(x, plan, normalized=attn_input)
+    assert torch.equal(fused, unfused)
 
 
 def test_tuned_gemm_table_loads_and_matches_default(vgo, device):
