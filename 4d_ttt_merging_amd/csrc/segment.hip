@@ -274,6 +274,30 @@ __device__ __forceinline__ void v16_load(const T* p, float* v) {
   }
 }
 
+// 16 values of T as loaded (not yet widened), so the next member's row can be
+// in flight while the current one is normalised.
+template <typename T>
+struct V16Raw {
+  typename V16<T>::half h[V16<T>::kLoads];
+};
+
+template <typename T>
+__device__ __forceinline__ void v16_load_raw(const T* p, V16Raw<T>& r) {
+  typedef typename V16<T>::half V;
+  constexpr int kPer = 16 / V16<T>::kLoads;
+#pragma unroll
+  for (int i = 0; i < V16<T>::kLoads; ++i) r.h[i] = *reinterpret_cast<const V*>(p + i * kPer);
+}
+
+template <typename T>
+__device__ __forceinline__ void v16_widen(const V16Raw<T>& r, float* v) {
+  constexpr int kPer = 16 / V16<T>::kLoads;
+#pragma unroll
+  for (int i = 0; i < V16<T>::kLoads; ++i)
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) v[i * kPer + j] = to_f32(r.h[i][j]);
+}
+
 template <typename T>
 __device__ __forceinline__ void v16_store(T* p, const float* v) {
   typedef typename V16<T>::half V;
@@ -307,13 +331,26 @@ __global__ __launch_bounds__(256) void compact16_kernel(
     const float* __restrict__ weights, int n_weights, const float* __restrict__ norm, int rows,
     int dim, float ln_eps, CompactOuts<TO, G> o) {
   const int lane = threadIdx.x & 63;
-  const int k = blockIdx.x * 4 + (threadIdx.x >> 6);
+  // Wave-uniform row: its index loads (offsets, items, row ids) go through the
+  // scalar cache and are counted apart from the member rows' vector loads.
+  const int k = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int d0 = (lane * 16) & 63;  // the same in every 1024-channel chunk
+  // Several outputs: their 64-channel LayerNorm parameters are staged in LDS
+  // once per work-group (reads from LDS do not wait on the rows in flight).
+  __shared__ float ln_lds[G > 1 ? G : 1][2][64];
+  if (G > 1) {
+    for (int e = threadIdx.x; e < G * 128; e += blockDim.x) {
+      const int g = e >> 7, h = (e >> 6) & 1, j = e & 63;
+      const float* src = h ? o.ln_b[g] : o.ln_w[g];
+      ln_lds[g][h][j] = src ? src[j] : 0.0f;
+    }
+    __syncthreads();
+  }
   if (k >= rows) return;
   const int64_t b = base_rows ? base_rows[k] : -1;
   const float nk = norm ? norm[k] : 1.0f;
-  const int d0 = (lane * 16) & 63;  // the same in every 1024-channel chunk
   // One output: this lane's 16 LayerNorm parameters stay in registers across
-  // the members.  Several outputs read theirs from the (cached) vectors.
+  // the members.
   float lw[16], lb[16];
   if (G == 1 && o.ln_w[0]) {
 #pragma unroll
@@ -327,54 +364,120 @@ __global__ __launch_bounds__(256) void compact16_kernel(
     if (G == 1)
       head_layer_norm(v, lw, lb, ln_eps);
     else
-      head_layer_norm(v, o.ln_w[g] + d0, o.ln_b[g] + d0, ln_eps);
+      head_layer_norm(v, &ln_lds[g][0][d0], &ln_lds[g][1][d0], ln_eps);
   };
   for (int c0 = 0; c0 < dim; c0 += 1024) {
     const int c = c0 + lane * 16;
-    const bool active = c < dim;  // whole 4-lane head groups are active together (dim % 64 == 0)
-    const int64_t xoff = static_cast<int64_t>(c >> 6) * xhs + (c & 63);
+    // Whole 4-lane head groups are active together (dim % 64 == 0).  Lanes past
+    // the row read its first channels instead and store nothing, so every load
+    // below is under a wave-uniform condition only.
+    const bool active = c < dim;
+    const int cl = active ? c : 0;
+    const int64_t xoff = static_cast<int64_t>(cl >> 6) * xhs + (cl & 63);
     float acc[G][16], v[G][16];
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
       for (int j = 0; j < 16; ++j) acc[g][j] = 0.0f;
-    if (active && b >= 0 && b < x_rows) {
+    if (b >= 0 && b < x_rows) {
 #pragma unroll
       for (int g = 0; g < G; ++g) v16_load(x + b * xts + o.x_off[g] + xoff, acc[g]);
 #pragma unroll
       for (int g = 0; g < G; ++g) layer_norm(g, acc[g]);
     }
-    for (int sgi = 0; sgi < segs_per_row; ++sgi) {
-      const int sb = offsets[k * segs_per_row + sgi], se = offsets[k * segs_per_row + sgi + 1];
-      if (sb >= se) continue;
+    // The row's members over all its segments (segment t holds items[ob[t]] ..
+    // items[ob[t + 1] - 1]) as one stream, software-pipelined: while member q
+    // is normalised and pooled, member q + 1's row is in flight, member q + 2's
+    // row id and member q + 3's item are being fetched, so a row costs a couple
+    // of round trips rather than one chain per member.  The sums keep the
+    // reference's order: seg over a segment's members, then acc += seg for
+    // every non-empty segment.
+    const int32_t* ob = offsets + static_cast<int64_t>(k) * segs_per_row;
+    // Segment ends ob[1..4] up front (plans have one or four segments per row);
+    // further ones are read when reached.
+    const int o1 = ob[1];
+    const int o2 = segs_per_row >= 2 ? ob[2] : 0;
+    const int o3 = segs_per_row >= 3 ? ob[3] : 0;
+    const int o4 = segs_per_row >= 4 ? ob[4] : 0;
+    auto seg_end = [&](int t1) -> int {  // ob[t1], 1 <= t1 <= segs_per_row
+      return t1 == 1 ? o1 : t1 == 2 ? o2 : t1 == 3 ? o3 : t1 == 4 ? o4 : ob[t1];
+    };
+    int q = ob[0];
+    const int q_end = seg_end(segs_per_row);
+    if (q < q_end) {
+      int t = 0;
+      int t_end = o1;
+      while (t_end <= q && t + 1 < segs_per_row) t_end = seg_end(++t + 1);
+      auto row_of = [&](uint32_t p) -> int64_t {
+        const int64_t i = static_cast<int64_t>(p >> item_shift);
+        return item_rows ? item_rows[i] : i;
+      };
+      auto weight_of = [&](uint32_t p) -> float {
+        return weights ? (static_cast<int>(p) < n_weights ? weights[p] : 0.0f) : 1.0f;
+      };
+      auto usable = [&](int64_t row) { return row >= 0 && row < x_rows; };
+      const uint32_t p0 = items[q];
+      uint32_t p1 = q + 1 < q_end ? items[q + 1] : 0u;
+      uint32_t p2 = q + 2 < q_end ? items[q + 2] : 0u;
+      const int64_t row0 = row_of(p0);
+      int64_t row1 = q + 1 < q_end ? row_of(p1) : -1;
+      // Two row buffers used in turn (an unrolled pair of steps), so no
+      // register copy has to wait for a row still in flight.
+      V16Raw<TI> ra[G], rb[G];
+      bool ok_a = usable(row0), ok_b = false;
+      float w_a = weight_of(p0), w_b = 0.0f;
+      if (ok_a) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) v16_load_raw(x + row0 * xts + o.x_off[g] + xoff, ra[g]);
+      }
       float seg[G][16];
 #pragma unroll
       for (int g = 0; g < G; ++g)
 #pragma unroll
         for (int j = 0; j < 16; ++j) seg[g][j] = 0.0f;
-      // The next member's id is requested before this member's row, so the
-      // two loads overlap instead of forming a chain of round trips.
-      uint32_t p_next = items[sb];
-      for (int q = sb; q < se; ++q) {
-        const uint32_t p = p_next;
-        if (q + 1 < se) p_next = items[q + 1];
-        const int64_t i = static_cast<int64_t>(p >> item_shift);
-        const int64_t row = item_rows ? item_rows[i] : i;
-        const float w = weights ? (static_cast<int>(p) < n_weights ? weights[p] : 0.0f) : 1.0f;
-        if (row < 0 || row >= x_rows || !active) continue;
+      // One member: request member q + 1's row into `nxt` (and member q + 2's
+      // row id, member q + 3's item), then pool member q from `cur`.
+      auto step = [&](V16Raw<TI> (&cur)[G], bool ok_c, float w_c, V16Raw<TI> (&nxt)[G], bool& ok_n,
+                      float& w_n) {
+        ok_n = q + 1 < q_end && usable(row1);
+        w_n = q + 1 < q_end ? weight_of(p1) : 0.0f;
+        if (ok_n) {
 #pragma unroll
-        for (int g = 0; g < G; ++g) v16_load(x + row * xts + o.x_off[g] + xoff, v[g]);
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          layer_norm(g, v[g]);
-#pragma unroll
-          for (int j = 0; j < 16; ++j) seg[g][j] = seg[g][j] + v[g][j] * w;
+          for (int g = 0; g < G; ++g) v16_load_raw(x + row1 * xts + o.x_off[g] + xoff, nxt[g]);
         }
+        const int64_t row2 = q + 2 < q_end ? row_of(p2) : -1;
+        const uint32_t p3 = q + 3 < q_end ? items[q + 3] : 0u;
+        if (ok_c) {
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            v16_widen(cur[g], v[g]);
+            layer_norm(g, v[g]);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) seg[g][j] = seg[g][j] + v[g][j] * w_c;
+          }
+        }
+        if (q + 1 == t_end) {
+#pragma unroll
+          for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+              acc[g][j] = acc[g][j] + seg[g][j];
+              seg[g][j] = 0.0f;
+            }
+          // Empty segments that follow add nothing.
+          while (t + 1 < segs_per_row && t_end <= q + 1) t_end = seg_end(++t + 1);
+        }
+        p1 = p2;
+        p2 = p3;
+        row1 = row2;
+        ++q;
+      };
+      while (true) {
+        step(ra, ok_a, w_a, rb, ok_b, w_b);
+        if (q >= q_end) break;
+        step(rb, ok_b, w_b, ra, ok_a, w_a);
+        if (q >= q_end) break;
       }
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) acc[g][j] = acc[g][j] + seg[g][j];
     }
     if (active) {
 #pragma unroll
@@ -496,7 +599,8 @@ extern "C" int vgo_segment_mass(const int32_t* offsets, int64_t segs_per_row, co
                                 float* mass, float* log_mass, void* stream) {
   VGO_REQUIRE(rows >= 0 && segs_per_row >= 1, "segment_mass: bad size");
   if (rows == 0) return VGO_OK;
-  VGO_REQUIRE(offsets && items && mass, "segment_mass: null pointer");
+  // items may be NULL when every segment is empty (a plan with no merged sources).
+  VGO_REQUIRE(offsets && mass, "segment_mass: null pointer");
   hipLaunchKernelGGL(segment_mass_kernel, dim3(static_cast<unsigned>((rows + 255) / 256)), dim3(256), 0,
                      as_stream(stream), offsets, static_cast<int>(segs_per_row), items, weights,
                      static_cast<int>(n_weights), static_cast<int>(rows), start, mass, log_mass);

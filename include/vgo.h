@@ -258,7 +258,8 @@ int vgo_csr_build(const uint32_t* keys, int64_t n_items, int64_t n_buckets, void
  * counts items); log_mass (nullable) = log(mass).  With start = 1 and one
  * segment per corner this is `deterministic_weighted_normalizer`
  * (vggt_omega/models/token_merging.py:40-59) and the sparse-convex mass
- * (vggt_omega/models/sparse_convex.py:2448-2450, 2468).
+ * (vggt_omega/models/sparse_convex.py:2448-2450, 2468).  items may be NULL
+ * when every segment is empty (a plan without merged sources).
  */
 int vgo_segment_mass(const int32_t* offsets, int64_t segs_per_row, const uint32_t* items,
                      const float* weights, int64_t n_weights, int64_t rows, float start,

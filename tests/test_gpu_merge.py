@@ -409,6 +409,22 @@ def test_sparse_convex_plan_vs_oracle_and_reference(vgo, device, fx):
     assert abs(md["merge_ratio"] - 186 / 1044) < 1e-9
 
 
+def test_sparse_convex_plan_without_merges(vgo, device):
+    """Unstructured tokens: no source passes the fit threshold, so the plan keeps every
+    token (as the oracle does), its mass is 1 and compaction / restore are copies."""
+    print("[merge] sparse-convex plan with no merges", flush=True)
+    tokens = torch.randn(1, 4 * 261, 256, generator=torch.Generator().manual_seed(3))
+    o = om.sparse_convex_plan(tokens, threshold=0.9, **KW)
+    assert o["source_original"].numel() == 0
+    plan = vgo.build_sparse_convex_plan(tokens.to(device), threshold=0.9, **KW)
+    assert torch.equal(plan.keep[0].cpu(), o["keep"]) and plan.source_original.numel() == 0
+    assert plan.kept_tokens == plan.original_tokens == 1044
+    assert torch.equal(plan.normalizer.reshape(-1).cpu(), torch.ones(1044))
+    x = tokens.to(device)
+    assert torch.equal(plan.compact(x), x)
+    assert torch.equal(plan.restore(x), x)
+
+
 # ---------------------------------------------------------- attention layer ----
 @pytest.mark.parametrize("tag,preserve", [("attn_qkv", False), ("attn_kv", True)])
 def test_self_attention_layer_vs_reference(vgo, device, fx, tag, preserve):
