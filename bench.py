@@ -7,7 +7,8 @@ inter-frame blocks (19 merged global, 5 register), dim 1024, 16 heads, MLP
 patches + 5 special tokens = 32,928 tokens).  Before every global block the
 FastVGGT bipartite planner merges at ratio 0.5 (protect_ratio 0, integer
 cluster masses as log-mass attention bias), attention runs on the compacted
-tokens, and the top-4 projection restores all tokens.  Patch tokens are a
+tokens, and the plan's top-4 restore (fused into the block's next residual row
+pass) brings all tokens back.  Patch tokens are a
 seeded N(0,1) cache (the DINOv3 encoder is not part of this path).
 
 One JSON line: value = frames/s of the aggregator forward (whole job, one
@@ -454,10 +455,17 @@ def c2_projection(vgo, device, steps):
         sec = event_time(lambda: vgo.top4_project(table, index, weight, out=result), steps, 3)
         compulsory = n * d * size + m * d * size + 32 * n
         name = "bf16" if dtype == torch.bfloat16 else "fp32"
+        # the reference's restore op sequence in torch on the same GPU
+        # (token_merging.py:408-413: gather [N,4,D], multiply by the weights in the
+        # value dtype, sum over the four)
+        idx64 = index.long()
+        torch_sec = event_time(lambda: (table[idx64] * weight.to(dtype)[..., None]).sum(1), 3, 1)
         out[name] = {"ms": sec * 1e3, "gbs_compulsory": compulsory / sec / 1e9,
                      "frac": compulsory / sec / 1e9 / PEAK_HBM_GBS,
-                     "gbs_logical": (compulsory + 4 * n * d * size) / sec / 1e9}
-        del table, result
+                     "gbs_logical": (compulsory + 4 * n * d * size) / sec / 1e9,
+                     "torch_ms": torch_sec * 1e3}
+        del table, result, idx64
+        torch.cuda.empty_cache()
     return out
 
 
@@ -495,6 +503,13 @@ def _median_seconds(fn, warmup: int = 2, runs: int = 5) -> float:
         fn()
         times.append(time.perf_counter() - t0)
     return statistics.median(times)
+
+
+def _median_reported(fn, warmup: int = 2, runs: int = 5) -> float:
+    """The same for a sampled measurement that returns its own (scaled) seconds first."""
+    for _ in range(warmup):
+        fn()
+    return statistics.median(fn()[0] for _ in range(runs))
 
 
 class _CpuBlocks:
@@ -574,6 +589,8 @@ def cpu_baseline(model) -> dict:
     * C2: the top-4 projection of 131,072 of the 1,048,576 rows (fp32, full
       65,536-row table) with the reference's restore op sequence (gather, multiply,
       sum), scaled x8.
+    * C5: the attention of one head and 2,048 of the 205,800 queries over the
+      52,968 merged keys, scaled to 16 heads and every query.
     """
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
@@ -583,10 +600,10 @@ def cpu_baseline(model) -> dict:
     x32 = torch.randn(FRAMES * tpf, DIM, generator=g)
     x16 = x32[:16 * tpf].contiguous()
     x4 = x32[:4 * tpf].contiguous()
-    c4_global = _median_seconds(lambda: blocks.global_block(x32, FRAMES, 1024))
+    c4_global = _median_reported(lambda: blocks.global_block(x32, FRAMES, 1024))
     c4_frame = _median_seconds(lambda: blocks.frame_block(x4, 4)) * (FRAMES / 4)
     pair = c4_frame + c4_global
-    c3 = _median_seconds(lambda: blocks.global_block(x16, 16, 1024))
+    c3 = _median_reported(lambda: blocks.global_block(x16, 16, 1024))
     index, weight = c2_inputs(1 << 20, 65536)
     table = torch.randn(65536, DIM, generator=g)
     rows = 131072
@@ -594,6 +611,15 @@ def cpu_baseline(model) -> dict:
     # the reference's restore op sequence (token_merging.py:405-413) on the host cores
     c2 = _median_seconds(lambda: (table[idx] * wts[..., None]).sum(1)) * ((1 << 20) / rows)
     c2_bytes = (1 << 20) * DIM * 4 + 65536 * DIM * 4 + 32 * (1 << 20)
+    # C5 attention: one head, 2,048 of the 205,800 queries over the 52,968 merged keys
+    # (the oracle's fp32 attention), scaled to 16 heads and every query.
+    from oracle import attention as oa
+    c5_q, c5_n, c5_k = 2048, 200 * (SPECIALS + 1024), 52968
+    qh = torch.randn(1, 1, c5_q, 64, generator=g) * 0.125
+    kh = torch.randn(1, 1, c5_k, 64, generator=g) * 0.125
+    vh = torch.randn(1, 1, c5_k, 64, generator=g)
+    bias = torch.randint(1, 15, (c5_k,), generator=g).float().log()
+    c5 = _median_seconds(lambda: oa.mass_bias_attention(qh, kh, vh, bias)) * HEADS * c5_n / c5_q
     cpu = "unknown"
     try:
         for line in open("/proc/cpuinfo"):
@@ -612,7 +638,9 @@ def cpu_baseline(model) -> dict:
             "c4_global_block_s": round(c4_global, 4),
             "c3_block_ms": round(c3 * 1e3, 2),
             "c2_fp32_ms": round(c2 * 1e3, 2), "c2_fp32_gbs": round(c2_bytes / c2 / 1e9, 2),
-            "c2_sample": "131,072 of 1,048,576 rows (x8), fp32, gather-multiply-sum"}
+            "c2_sample": "131,072 of 1,048,576 rows (x8), fp32, gather-multiply-sum",
+            "c5_attention_s": round(c5, 2),
+            "c5_sample": "1 of 16 heads x 2,048 of 205,800 queries over 52,968 keys, fp32, scaled"}
 
 
 # ----------------------------------------------------- counter workloads ----
