@@ -42,8 +42,8 @@ struct Vec16<f16_t> {
 template <typename T, int R, int CH>
 __global__ __launch_bounds__(kWaves * 64) void top4_project_kernel(
     const T* __restrict__ table, int64_t table_stride, const int32_t* __restrict__ index,
-    const float* __restrict__ weight, T* __restrict__ out, int64_t out_stride, int64_t n_rows,
-    int64_t table_rows, int dim) {
+    const float* __restrict__ weight, const int32_t* __restrict__ order, T* __restrict__ out,
+    int64_t out_stride, int64_t n_rows, int64_t table_rows, int dim) {
   typedef typename Vec16<T>::type V;
   constexpr int VN = Vec16<T>::n;
   const int lane = lane_id();
@@ -56,13 +56,26 @@ __global__ __launch_bounds__(kWaves * 64) void top4_project_kernel(
     float wq[R][4];
     bool use[R][4];
     bool bad[R];
+    // Output row of each work position: the position itself, or order[position]
+    // (positions whose order entry is out of range produce nothing).
+    int64_t orow[R];
 #pragma unroll
     for (int rr = 0; rr < R; ++rr) {
-      const int64_t row = r0 + rr;
+      const int64_t pos = r0 + rr;
+      int64_t row = pos < n_rows ? pos : -1;
+      if (order && row >= 0) {
+        const int32_t o = order[pos];
+        row = o >= 0 && o < n_rows ? o : -1;
+      }
+      orow[rr] = row;
+    }
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr) {
+      const int64_t row = orow[rr];
       bad[rr] = false;
       i32x4 id4 = {0, 0, 0, 0};
       f32x4 w4 = {0.0f, 0.0f, 0.0f, 0.0f};
-      if (row < n_rows) {
+      if (row >= 0) {
         id4 = *reinterpret_cast<const i32x4*>(index + 4 * row);
         w4 = *reinterpret_cast<const f32x4*>(weight + 4 * row);
       }
@@ -96,9 +109,9 @@ __global__ __launch_bounds__(kWaves * 64) void top4_project_kernel(
       }
 #pragma unroll
       for (int rr = 0; rr < R; ++rr) {
-        const int64_t row = r0 + rr;
-        if (row >= n_rows) continue;
-        T* orow = out + row * out_stride;
+        const int64_t row = orow[rr];
+        if (row < 0) continue;
+        T* o_row = out + row * out_stride;
 #pragma unroll
         for (int ch = 0; ch < CH; ++ch) {
           const int e = base + (ch * 64 + lane) * VN;
@@ -117,7 +130,7 @@ __global__ __launch_bounds__(kWaves * 64) void top4_project_kernel(
           V o;
 #pragma unroll
           for (int j = 0; j < VN; ++j) o[j] = from_f32<T>(bad[rr] ? __builtin_nanf("") : acc[j]);
-          __builtin_nontemporal_store(o, reinterpret_cast<V*>(orow + e));
+          __builtin_nontemporal_store(o, reinterpret_cast<V*>(o_row + e));
         }
       }
     }
@@ -128,11 +141,13 @@ __global__ __launch_bounds__(kWaves * 64) void top4_project_kernel(
 template <typename T>
 __global__ __launch_bounds__(256) void top4_project_scalar_kernel(
     const T* __restrict__ table, int64_t table_stride, const int32_t* __restrict__ index,
-    const float* __restrict__ weight, T* __restrict__ out, int64_t out_stride, int64_t n_rows,
-    int64_t table_rows, int dim) {
-  const int64_t row = blockIdx.y;
+    const float* __restrict__ weight, const int32_t* __restrict__ order, T* __restrict__ out,
+    int64_t out_stride, int64_t n_rows, int64_t pos0, int64_t table_rows, int dim) {
+  const int64_t pos = pos0 + blockIdx.y;
   const int e = blockIdx.x * 256 + threadIdx.x;
-  if (row >= n_rows || e >= dim) return;
+  if (pos >= n_rows || e >= dim) return;
+  const int64_t row = order ? order[pos] : pos;
+  if (row < 0 || row >= n_rows) return;
   float acc = 0.0f;
   bool bad = false;
   for (int c = 0; c < 4; ++c) {
@@ -151,11 +166,11 @@ __global__ __launch_bounds__(256) void top4_project_scalar_kernel(
 
 template <typename T, int R, int CH>
 void launch_vec(const T* tb, int64_t table_stride, const int32_t* index, const float* weight,
-                T* ob, int64_t out_stride, int64_t n_rows, int64_t table_rows, int dim,
-                int64_t blocks, hipStream_t stream) {
+                const int32_t* order, T* ob, int64_t out_stride, int64_t n_rows, int64_t table_rows,
+                int dim, int64_t blocks, hipStream_t stream) {
   hipLaunchKernelGGL((top4_project_kernel<T, R, CH>), dim3(static_cast<unsigned>(blocks)),
-                     dim3(kWaves * 64), 0, stream, tb, table_stride, index, weight, ob, out_stride,
-                     n_rows, table_rows, dim);
+                     dim3(kWaves * 64), 0, stream, tb, table_stride, index, weight, order, ob,
+                     out_stride, n_rows, table_rows, dim);
 }
 
 // Work-groups resident per CU for the persistent launch (MI355X: 256 CUs).
@@ -175,8 +190,8 @@ int device_cus() {
 
 template <typename T>
 int launch_project(const void* table, int64_t table_stride, const int32_t* index,
-                   const float* weight, void* out, int64_t out_stride, int64_t n_rows,
-                   int64_t table_rows, int64_t dim, hipStream_t stream) {
+                   const float* weight, const int32_t* order, void* out, int64_t out_stride,
+                   int64_t n_rows, int64_t table_rows, int64_t dim, hipStream_t stream) {
   const T* tb = static_cast<const T*>(table);
   T* ob = static_cast<T*>(out);
   constexpr int VN = Vec16<T>::n;
@@ -193,13 +208,13 @@ int launch_project(const void* table, int64_t table_stride, const int32_t* index
       return need < cap ? need : cap;
     };
     if (row_chunks >= 4) {
-      launch_vec<T, 2, 4>(tb, table_stride, index, weight, ob, out_stride, n_rows, table_rows, d,
+      launch_vec<T, 2, 4>(tb, table_stride, index, weight, order, ob, out_stride, n_rows, table_rows, d,
                           blocks_for(2), stream);
     } else if (row_chunks >= 2) {
-      launch_vec<T, 4, 2>(tb, table_stride, index, weight, ob, out_stride, n_rows, table_rows, d,
+      launch_vec<T, 4, 2>(tb, table_stride, index, weight, order, ob, out_stride, n_rows, table_rows, d,
                           blocks_for(4), stream);
     } else {
-      launch_vec<T, 8, 1>(tb, table_stride, index, weight, ob, out_stride, n_rows, table_rows, d,
+      launch_vec<T, 8, 1>(tb, table_stride, index, weight, order, ob, out_stride, n_rows, table_rows, d,
                           blocks_for(8), stream);
     }
   } else {
@@ -209,8 +224,8 @@ int launch_project(const void* table, int64_t table_stride, const int32_t* index
       const int64_t nr = (n_rows - r0) < 65535 ? (n_rows - r0) : 65535;
       grid.y = static_cast<unsigned>(nr);
       hipLaunchKernelGGL((top4_project_scalar_kernel<T>), grid, dim3(256), 0, stream, tb,
-                         table_stride, index + 4 * r0, weight + 4 * r0, ob + r0 * out_stride,
-                         out_stride, nr, table_rows, static_cast<int>(dim));
+                         table_stride, index, weight, order, ob, out_stride, n_rows, r0, table_rows,
+                         static_cast<int>(dim));
     }
   }
   return check_launch("top4_project");
@@ -219,10 +234,10 @@ int launch_project(const void* table, int64_t table_stride, const int32_t* index
 }  // namespace
 }  // namespace vgo
 
-extern "C" int vgo_top4_project(const void* table, int64_t table_row_stride, const int32_t* index,
-                                const float* weight, void* out, int64_t out_row_stride,
-                                int64_t n_rows, int64_t table_rows, int64_t dim, int dtype,
-                                void* stream) {
+namespace {
+int project_entry(const void* table, int64_t table_row_stride, const int32_t* index,
+                  const float* weight, const int32_t* order, void* out, int64_t out_row_stride,
+                  int64_t n_rows, int64_t table_rows, int64_t dim, int dtype, void* stream) {
   using namespace vgo;
   VGO_REQUIRE(n_rows >= 0 && table_rows >= 0 && dim >= 0, "top4_project: negative size");
   if (n_rows == 0 || dim == 0) return VGO_OK;
@@ -235,15 +250,35 @@ extern "C" int vgo_top4_project(const void* table, int64_t table_row_stride, con
   hipStream_t s = as_stream(stream);
   switch (dtype) {
     case VGO_F32:
-      return launch_project<float>(table, table_row_stride, index, weight, out, out_row_stride,
+      return launch_project<float>(table, table_row_stride, index, weight, order, out, out_row_stride,
                                    n_rows, table_rows, dim, s);
     case VGO_BF16:
-      return launch_project<bf16_t>(table, table_row_stride, index, weight, out, out_row_stride,
+      return launch_project<bf16_t>(table, table_row_stride, index, weight, order, out, out_row_stride,
                                     n_rows, table_rows, dim, s);
     case VGO_F16:
-      return launch_project<f16_t>(table, table_row_stride, index, weight, out, out_row_stride,
+      return launch_project<f16_t>(table, table_row_stride, index, weight, order, out, out_row_stride,
                                    n_rows, table_rows, dim, s);
     default:
       return fail(VGO_EINVAL, "top4_project: unknown dtype");
   }
+}
+}  // namespace
+
+extern "C" int vgo_top4_project(const void* table, int64_t table_row_stride, const int32_t* index,
+                                const float* weight, void* out, int64_t out_row_stride,
+                                int64_t n_rows, int64_t table_rows, int64_t dim, int dtype,
+                                void* stream) {
+  return project_entry(table, table_row_stride, index, weight, nullptr, out, out_row_stride, n_rows,
+                       table_rows, dim, dtype, stream);
+}
+
+extern "C" int vgo_top4_project_ordered(const void* table, int64_t table_row_stride,
+                                        const int32_t* index, const float* weight,
+                                        const int32_t* order, void* out, int64_t out_row_stride,
+                                        int64_t n_rows, int64_t table_rows, int64_t dim, int dtype,
+                                        void* stream) {
+  using namespace vgo;
+  VGO_REQUIRE(order || n_rows == 0, "top4_project_ordered: null order");
+  return project_entry(table, table_row_stride, index, weight, order, out, out_row_stride, n_rows,
+                       table_rows, dim, dtype, stream);
 }

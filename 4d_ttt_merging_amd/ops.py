@@ -8,8 +8,9 @@ dispatcher, `torch.compile` and fake-tensor tracing see them as single ops:
   inputs; `vgo::attention_into` / `vgo::attention_pair_into` write into given
   (strided) outputs, the pair form also running the dense special-query pass of
   vggt_omega/models/layers/attention.py:406-422 in the same launch;
-* `vgo::top4_project(table, index, weight) -> Tensor` and `vgo::top4_project_into`
-  -- the plans' restore (token_merging.py:387-414, 193-196);
+* `vgo::top4_project(table, index, weight) -> Tensor`, `vgo::top4_project_into` and
+  `vgo::top4_project_ordered_into` -- the plans' restore (token_merging.py:387-414,
+  193-196);
 * `vgo::compact_into`, `vgo::compact_multi_into` -- Q/K/V compaction
   (token_merging.py:343-385, 176-191) with the q/k LayerNorm fused;
 * `vgo::qkv_epilogue` -- the packed projection split into head-major q/k/v with
@@ -101,6 +102,18 @@ def top4_project_into(table: Tensor, index: Tensor, weight: Tensor, out: Tensor)
 
 @top4_project_into.register_fake
 def _(table, index, weight, out):
+    return None
+
+
+@torch.library.custom_op("vgo::top4_project_ordered_into", mutates_args={"out"}, device_types="cuda")
+def top4_project_ordered_into(table: Tensor, index: Tensor, weight: Tensor, order: Tensor,
+                              out: Tensor) -> None:
+    """top4_project_into with the rows computed in `order` (same result)."""
+    _proj._top4_project_impl(table, index, weight, out=out, order=order)
+
+
+@top4_project_ordered_into.register_fake
+def _(table, index, weight, order, out):
     return None
 
 

@@ -10,23 +10,41 @@ from __future__ import annotations
 
 import torch
 
-from . import _lib
+from . import _kernels, _lib
 
 
 def top4_project(table: torch.Tensor, index: torch.Tensor, weight: torch.Tensor, *,
-                 out: torch.Tensor | None = None) -> torch.Tensor:
+                 out: torch.Tensor | None = None, order: torch.Tensor | None = None) -> torch.Tensor:
     """Gather four rows of `table` [M, D] per output row and take their weighted sum
     (torch.ops.vgo.top4_project, or top4_project_into with `out`); see
-    `_top4_project_impl`."""
-    _lib.require_gpu(table, index, weight, out)
+    `_top4_project_impl`.  `order` (int32 [N], e.g. from `locality_order`) only sets
+    the order the rows are computed in; the result is the same."""
+    _lib.require_gpu(table, index, weight, out, order)
+    if order is not None:
+        if out is None:
+            out = torch.empty((index.shape[0], table.shape[1]), device=table.device, dtype=table.dtype)
+        torch.ops.vgo.top4_project_ordered_into(table, index, weight, order, out)
+        return out
     if out is None:
         return torch.ops.vgo.top4_project(table, index, weight)
     torch.ops.vgo.top4_project_into(table, index, weight, out)
     return out
 
 
+def locality_order(index: torch.Tensor, table_rows: int) -> torch.Tensor:
+    """Output rows grouped by their first parent (stable, int32 [N]): computed in this
+    order, the rows that share a parent run together and that parent's repeated
+    gathers hit the L2 cache.  Reusable for every restore with the same index."""
+    _lib.require_gpu(index)
+    if index.ndim != 2 or index.shape[1] != 4 or index.dtype != torch.int32:
+        raise ValueError("locality_order requires int32 index [N, 4]")
+    order, _ = _kernels.csr_build(index[:, 0].contiguous(), int(table_rows))
+    return order.view(torch.int32)
+
+
 def _top4_project_impl(table: torch.Tensor, index: torch.Tensor, weight: torch.Tensor, *,
-                       out: torch.Tensor | None = None) -> torch.Tensor:
+                       out: torch.Tensor | None = None,
+                       order: torch.Tensor | None = None) -> torch.Tensor:
     """Gather four rows of `table` [M, D] per output row and take their weighted sum.
 
     index: [N, 4] int32, weight: [N, 4] float32 (both contiguous).  Zero weights
@@ -48,10 +66,19 @@ def _top4_project_impl(table: torch.Tensor, index: torch.Tensor, weight: torch.T
         out = torch.empty((n_rows, dim), device=table.device, dtype=table.dtype)
     elif out.shape != (n_rows, dim) or out.dtype != table.dtype or out.stride(-1) != 1:
         raise ValueError("top4_project output must be [N, D] of the table dtype")
-    status = lib.vgo_top4_project(
-        table.data_ptr(), table.stride(0), index.data_ptr(), weight.data_ptr(), out.data_ptr(),
-        out.stride(0), n_rows, table.shape[0], dim, _lib.dtype_code(table.dtype),
-        _lib.stream_of(table),
-    )
+    if order is not None:
+        if order.shape != (n_rows,) or order.dtype != torch.int32:
+            raise ValueError("top4_project order must be int32 [N]")
+        order = order.contiguous()
+        status = lib.vgo_top4_project_ordered(
+            table.data_ptr(), table.stride(0), index.data_ptr(), weight.data_ptr(), order.data_ptr(),
+            out.data_ptr(), out.stride(0), n_rows, table.shape[0], dim, _lib.dtype_code(table.dtype),
+            _lib.stream_of(table))
+    else:
+        status = lib.vgo_top4_project(
+            table.data_ptr(), table.stride(0), index.data_ptr(), weight.data_ptr(), out.data_ptr(),
+            out.stride(0), n_rows, table.shape[0], dim, _lib.dtype_code(table.dtype),
+            _lib.stream_of(table),
+        )
     _lib.check(status)
     return out

@@ -447,12 +447,19 @@ def c2_projection(vgo, device, steps):
     n, m, d = 1 << 20, 65536, 1024
     index, weight = c2_inputs(n, m)
     index, weight = index.to(device), weight.to(device)
+    proj = importlib.import_module("4d_ttt_merging_amd.projection")
+    # Rows grouped by first parent: that parent's repeated gathers hit L2 (the
+    # order depends only on the index, so a plan computes it once).
+    order = proj.locality_order(index, m)
+    sort_sec = event_time(lambda: proj.locality_order(index, m), 5, 1)
     gt = torch.Generator(device=device).manual_seed(2)
-    out = {}
+    out = {"locality_order_ms": sort_sec * 1e3}
     for dtype, size in ((torch.bfloat16, 2), (torch.float32, 4)):
         table = torch.randn(m, d, device=device, generator=gt).to(dtype)
         result = torch.empty(n, d, device=device, dtype=dtype)
         sec = event_time(lambda: vgo.top4_project(table, index, weight, out=result), steps, 3)
+        ordered_sec = event_time(lambda: proj.top4_project(table, index, weight, out=result, order=order),
+                                 steps, 3)
         compulsory = n * d * size + m * d * size + 32 * n
         name = "bf16" if dtype == torch.bfloat16 else "fp32"
         # the reference's restore op sequence in torch on the same GPU
@@ -463,6 +470,8 @@ def c2_projection(vgo, device, steps):
         out[name] = {"ms": sec * 1e3, "gbs_compulsory": compulsory / sec / 1e9,
                      "frac": compulsory / sec / 1e9 / PEAK_HBM_GBS,
                      "gbs_logical": (compulsory + 4 * n * d * size) / sec / 1e9,
+                     "ordered_ms": ordered_sec * 1e3,
+                     "ordered_frac": compulsory / ordered_sec / 1e9 / PEAK_HBM_GBS,
                      "torch_ms": torch_sec * 1e3}
         del table, result, idx64
         torch.cuda.empty_cache()

@@ -157,6 +157,20 @@ int vgo_top4_project(const void* table, int64_t table_row_stride, const int32_t*
                      const float* weight, void* out, int64_t out_row_stride, int64_t n_rows,
                      int64_t table_rows, int64_t dim, int dtype, void* stream);
 
+/*
+ * vgo_top4_project with the output rows taken in a given order: work position i
+ * computes output row order[i] (order is int32 [n_rows], normally a permutation
+ * of 0..n_rows-1; entries outside that range compute nothing).  Each output row
+ * is computed exactly as by vgo_top4_project, so any order gives the same
+ * result.  An order that groups rows by a shared parent (the stable sort of
+ * index[:, 0] that vgo_csr_build gives) lets the repeated gathers of that parent
+ * hit the L2 cache.  Same restore as vgo_top4_project (token_merging.py:387-414).
+ */
+int vgo_top4_project_ordered(const void* table, int64_t table_row_stride, const int32_t* index,
+                             const float* weight, const int32_t* order, void* out,
+                             int64_t out_row_stride, int64_t n_rows, int64_t table_rows,
+                             int64_t dim, int dtype, void* stream);
+
 
 /*
  * Row gather + L2 normalisation: out[r] = x[rows[r]] / max(||x[rows[r]]||, eps),

@@ -21,7 +21,7 @@ OPS = {
     "top4_project": "vgo::top4_project(Tensor table, Tensor index, Tensor weight) -> Tensor",
     "attention_into": None, "attention_pair_into": None, "top4_project_into": None,
     "compact_into": None, "compact_multi_into": None, "qkv_epilogue": None, "residual_layer_norm": None,
-    "restore_residual_layer_norm": None,
+    "restore_residual_layer_norm": None, "top4_project_ordered_into": None,
 }
 
 

@@ -69,3 +69,32 @@ def test_strided_table_and_output(vgo, device):
     ref = oracle.top4_project(table, index, weight)
     assert torch.equal(view.cpu(), ref)
     assert (out[:, :128] == 7).all() and (out[:, 640:] == 7).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("n,m,d", [(4099, 700, 1024), (1044, 522, 1000), (257, 16, 23)])
+def test_ordered_projection_equals_plain(dtype, device, n, m, d):
+    """Rows computed in the locality order (grouped by first parent) or any other
+    order give the plain projection bit for bit; order entries outside [0, N)
+    compute nothing."""
+    print(f"[project] ordered dtype={dtype} n={n} m={m} d={d}", flush=True)
+    from tests.conftest import import_package
+    proj = import_package("projection")
+    table, index, weight = _case(n * 3 + m + d, n, m, d, dtype)
+    table, index, weight = table.to(device), index.to(device), weight.to(device)
+    plain = proj.top4_project(table, index, weight)
+    order = proj.locality_order(index, m)
+    assert order.dtype == torch.int32 and torch.equal(order.sort().values.cpu(), torch.arange(n, dtype=torch.int32))
+    first = index[:, 0].long()[order.long()].cpu()
+    assert bool((first[1:] >= first[:-1]).all()), "locality order must group rows by first parent"
+    assert torch.equal(proj.top4_project(table, index, weight, order=order), plain)
+    shuffled = torch.randperm(n, generator=torch.Generator().manual_seed(n)).int().to(device)
+    assert torch.equal(proj.top4_project(table, index, weight, order=shuffled), plain)
+    partial = shuffled.clone()
+    partial[: n // 2] = -1
+    out = torch.full_like(plain, 7.0)
+    proj.top4_project(table, index, weight, out=out, order=partial)
+    done = torch.zeros(n, dtype=torch.bool)
+    done[partial[n // 2:].long().cpu()] = True
+    assert torch.equal(out[done.to(device)], plain[done.to(device)])
+    assert bool((out[~done.to(device)] == 7.0).all())
