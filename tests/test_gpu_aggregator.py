@@ -293,3 +293,34 @@ def test_aggregator_sparse_convex_replayed_plans(vgo, manifest, afx, device, tag
     print(f"[aggregator] sparse-convex replay {tag} autocast={autocast} rel err {err:.2e}", flush=True)
     stats = model.sparse_convex_last_plan_stats
     assert [s["kept_tokens"] for s in stats] == [s["kept_tokens"] for s in manifest[f"{tag}_stats"]]
+
+
+@pytest.mark.gpu
+def test_aggregator_fastvggt_forward_replays_from_a_hip_graph(manifest, device):
+    """The FastVGGT forward (bf16 autocast, mass bias) has no host synchronisation, so it
+    captures into one HIP graph; three replays, with eager forwards between them, each give
+    the eager output bit for bit."""
+    print("[aggregator] FastVGGT forward in a HIP graph", flush=True)
+    model, images = _model(manifest, device)
+    _configure(model, "fv")
+    model.set_fastvggt(True, merge_ratio=0.5, protect_ratio=0.0, mass_bias=True)
+
+    def step():
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16, cache_enabled=False):
+            return [o for o in model(images)[0] if o is not None]
+
+    eager = [o.clone() for o in step()]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static = step()
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, b) for a, b in zip(static, eager))
+        step()
+        torch.cuda.synchronize()
