@@ -35,8 +35,11 @@ __device__ __forceinline__ uint32_t bf16_bits(float x) {
   return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b));
 }
 
-// Monotone map of bf16 bit patterns to unsigned order; -0 is folded onto +0.
+// Monotone map of bf16 bit patterns to unsigned order; -0 is folded onto +0
+// and every NaN, whatever its sign (inf * 0 gives a negative one), onto the
+// top, above +inf, as torch's descending sort ranks it.
 __device__ __forceinline__ uint32_t ord16(uint32_t b) {
+  if ((b & 0x7FFFu) > 0x7F80u) return 0xFFFFu;
   if (b == 0x8000u) b = 0;
   return (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
 }
@@ -47,6 +50,20 @@ __host__ __device__ __forceinline__ uint32_t unord16(uint32_t o) {
 // fp32 value of x rounded to bf16 (round to nearest even, as the conversion).
 __device__ __forceinline__ float bf16_round(float x) {
   return __builtin_bit_cast(float, bf16_bits(x) << 16);
+}
+
+// Smallest fp32 x whose bf16 rounding equals t (a bf16 value held in fp32, not
+// NaN).  Rounding is to nearest even, so the midpoint below t belongs to t when
+// t's last bf16 mantissa bit is 0.  Both zeros share the interval of -0 and +0;
+// -inf is its own bound.  Rounding is monotone, so among values that are at
+// most m, x rounds to bf16(m) exactly when x >= bf16_lower_bound(bf16(m)).
+__device__ __forceinline__ float bf16_lower_bound(float t) {
+  if (t == -__builtin_inff()) return t;
+  const uint32_t b = __builtin_bit_cast(uint32_t, t);
+  const uint32_t mag = b & 0x7FFFFFFFu;
+  const uint32_t lsb = (mag >> 16) & 1u;
+  if ((b >> 31) == 0u && mag != 0u) return __builtin_bit_cast(float, mag - 0x8000u + lsb);
+  return __builtin_bit_cast(float, 0x80000000u | (mag + 0x8000u - lsb));
 }
 
 __device__ __forceinline__ uint64_t make_key(float score, int j) {
@@ -531,23 +548,71 @@ __global__ __launch_bounds__(kRWaves * 64, 1) void sim_topk_ring_kernel(
         // A lane's rows jl + pos rise with pos, a compile-time constant per
         // element, so the tile's winner is tracked by pos and jl added once.
         // Rows past d_end exist only in a part's last, partial tile.
-        const int lim = d0 + kRTile <= d_end ? kRTile : d_end - jl;
+        //
+        // Full tiles without a NaN take two cheap passes per source: the fp32
+        // maximum m of the lane's 64 scores (NaN-propagating 3-input max), then
+        // the first position whose score is at least the lower bound of
+        // bf16(m)'s rounding interval -- the first score that rounds to the
+        // tile's bf16 maximum -- by one compare and one select per score, where
+        // the per-score loop below rounds and compares every score.
+        const bool full = d0 + kRTile <= d_end;
+        bool fast = false;
+        float mx[2];
+        if (full) {
 #pragma unroll
-        for (int sb = 0; sb < 2; ++sb) {
-          float tv = top_v[sb];
-          int tp = -1;
+          for (int sb = 0; sb < 2; ++sb) {
+            float part[4];
 #pragma unroll
-          for (int db = 0; db < 4; ++db)
+            for (int db = 0; db < 4; ++db) {
+              float m = acc[db][sb][0];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int pos = 32 * db + 8 * (r >> 2) + (r & 3);
-              const float v = bf16_round(acc[db][sb][r]);
-              const bool take = (pos < lim) & ((v > tv) | ((v != v) & (tv == tv)));
-              tv = take ? v : tv;
-              tp = take ? pos : tp;
+              for (int r = 1; r < 16; r += 2)
+                m = __builtin_elementwise_maximum(__builtin_elementwise_maximum(m, acc[db][sb][r]),
+                                                  r + 1 < 16 ? acc[db][sb][r + 1] : acc[db][sb][r]);
+              part[db] = m;
             }
-          top_j[sb] = tp >= 0 ? jl + tp : top_j[sb];
-          top_v[sb] = tv;
+            mx[sb] = __builtin_elementwise_maximum(__builtin_elementwise_maximum(part[0], part[1]),
+                                                   __builtin_elementwise_maximum(part[2], part[3]));
+          }
+          fast = __ballot((mx[0] != mx[0]) | (mx[1] != mx[1])) == 0;
+        }
+        if (fast) {
+#pragma unroll
+          for (int sb = 0; sb < 2; ++sb) {
+            const float t = bf16_round(mx[sb]);
+            const float lo = bf16_lower_bound(t);
+            int tp = 0;  // some score reaches lo: the maximum itself
+#pragma unroll
+            for (int db = 3; db >= 0; --db)
+#pragma unroll
+              for (int r = 15; r >= 0; --r)
+                tp = acc[db][sb][r] >= lo ? 32 * db + 8 * (r >> 2) + (r & 3) : tp;
+            // Strictly greater: an equal maximum of an earlier tile keeps its
+            // lower row, and a NaN kept from an earlier tile stays.
+            if (t > top_v[sb]) {
+              top_v[sb] = t;
+              top_j[sb] = jl + tp;
+            }
+          }
+        } else {
+          const int lim = full ? kRTile : d_end - jl;
+#pragma unroll
+          for (int sb = 0; sb < 2; ++sb) {
+            float tv = top_v[sb];
+            int tp = -1;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) {
+                const int pos = 32 * db + 8 * (r >> 2) + (r & 3);
+                const float v = bf16_round(acc[db][sb][r]);
+                const bool take = (pos < lim) & ((v > tv) | ((v != v) & (tv == tv)));
+                tv = take ? v : tv;
+                tp = take ? pos : tp;
+              }
+            top_j[sb] = tp >= 0 ? jl + tp : top_j[sb];
+            top_v[sb] = tv;
+          }
         }
       } else {
 #pragma unroll

@@ -96,6 +96,53 @@ def test_similarity_selection_is_exact_on_kernel_scores(kern, device, topk, ns, 
     assert torch.equal(values.cpu(), ref_v)
 
 
+@pytest.mark.parametrize("dim", [64, 72])
+@pytest.mark.parametrize("topk", [1, 4])
+@pytest.mark.parametrize("nd", [768, 1000])
+def test_similarity_topk_on_crafted_rounding_ties(kern, device, nd, topk, dim):
+    """With dim 64, full 256-row dictionary tiles take the two-pass top-1 epilogue (the
+    fp32 maximum, then the first score at or above the lower bound of its bf16 rounding
+    interval); dim 72 takes the 128-row kernel.  The dictionary puts scores exactly on
+    bf16 midpoints (ties to even, up and down), a quarter ulp either side of them and on
+    bf16 values, so several fp32 scores at several positions round to each row's maximum;
+    source rows negate them, zero them, and one row (in another wave, which then takes the
+    per-score path) makes inf scores and a NaN (inf * 0, whose sign bit the hardware sets)
+    that must rank above +inf after the dictionary parts are merged.  All products and
+    sums are exact in fp32, so the kernel's scores equal the exact ones and the selection
+    must be the lowest indices of the bf16 maxima."""
+    print(f"[similarity] crafted rounding ties nd={nd} topk={topk} dim={dim}", flush=True)
+    g = torch.Generator().manual_seed(nd)
+    half = 2.0 ** -9
+    k = torch.randint(-2, 3, (nd,), generator=g).float()
+    c = torch.tensor([-1.0, -0.5, 0.0, 0.5, 1.0])[torch.randint(0, 5, (nd,), generator=g)]
+    dst = torch.zeros(nd, dim)
+    dst[:, 0] = 0.75 + k * 2.0 ** -8
+    dst[:, 1] = c
+    dst[7, 0], dst[7, 1] = 0.0, 1.0  # inf * 0: a NaN score for the overflow row
+    kinds = [(1.0, half), (-1.0, -half), (0.0, 0.0), (1.0, -half), (0.5, half), (-0.5, half)]
+    src = torch.zeros(128, dim)
+    for i in range(128):
+        src[i, :2] = torch.tensor(kinds[i % len(kinds)])
+    src[100, :2] = torch.tensor([float("inf"), 0.0])
+    src_b, dst_b = src.bfloat16(), dst.bfloat16()
+    assert torch.equal(src_b.float(), src) and torch.equal(dst_b.float(), dst)
+    scores = torch.full((128, nd), float("nan"), dtype=torch.bfloat16, device=device)
+    values, index = kern.similarity_topk(src_b.to(device), dst_b.to(device), topk, scores=scores)
+    ks = scores.float().cpu()
+    exact = om.bf16_scores(src_b, dst_b)
+    assert torch.equal(ks.isnan(), exact.isnan()) and torch.equal(ks.nan_to_num(), exact.nan_to_num())
+    ref_v, ref_i = om.topk_lowest_index(ks, topk)
+    assert ref_i[100, 0] == 7  # the NaN ranks first
+    assert torch.equal(index.cpu(), ref_i)
+    assert torch.equal(values.cpu().isnan(), ref_v.isnan())
+    assert torch.equal(values.cpu().nan_to_num(), ref_v.nan_to_num())
+    # the data really tie: rows whose maximum several positions reach, with different fp32 scores
+    fp32 = src_b.double() @ dst_b.double().T
+    row = 0
+    at_max = ks[row] == ks[row].max()
+    assert int(at_max.sum()) > 1 and fp32[row][at_max].unique().numel() > 1
+
+
 def test_similarity_ranges_rows_and_device_count(kern, device):
     g = torch.Generator().manual_seed(3)
     src = F.normalize(torch.randn(500, 256, generator=g), dim=-1).bfloat16()
