@@ -341,8 +341,14 @@ __global__ __launch_bounds__(256, 2) void sim_topk_kernel(
 // through a 5-stage ring (all 160 KB of the CU's LDS), up to four chunks
 // ahead.  A step's first k-step operands are read from LDS during the
 // previous step, its second k-step's during its first k-step's MFMAs, so the
-// LDS reads (96 KB per step and CU, near the LDS bandwidth) overlap the
-// MFMAs instead of preceding them.  LDS rows are 64 B; their four 16-byte chunks are
+// LDS reads (96 KB per step and CU) overlap the MFMAs instead of preceding
+// them.  The CU's DMA path moves about 25 B per clock, a little slower than
+// the MFMAs consume a step, and a DMA issue stalls its wave while that path
+// is backed up; so the first k-step's MFMAs run before the step's barrier
+// and the DMAs are issued between the second k-step's MFMAs, which keeps the
+// matrix cores fed through barrier skew and issue stalls (with every wave
+// issuing its DMAs right after the barrier, the transfer and the MFMAs
+// mostly took turns).  LDS rows are 64 B; their four 16-byte chunks are
 // XOR-permuted by sw4(row) = (row >> 2) & 3, so the operand reads (16 rows at
 // one logical chunk per quarter-wave) are conflict-free.  Requires
 // dim % 32 == 0.  Invalid source row ids read row 0 through the DMA and score
@@ -430,22 +436,29 @@ __global__ __launch_bounds__(kRWaves * 64, 1) void sim_topk_ring_kernel(
   // vmcnt waits below count on -- with fewer in flight, "at most N
   // outstanding" would no longer mean that the oldest step has landed.
   int iss_step = 0, iss_dt = 0, iss_kc = 0, iss_stage = 0;
-  auto issue_next = [&]() {
-    if (iss_dt != cur_dt) set_dtile(iss_dt);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int blk = (32 * wave + 16 * j) * kRKc;
-      lds_dma16_addr(dict_p[j] + iss_kc, lds_offset(a_lds + iss_stage * kRTileElems + blk));
-      lds_dma16_addr(src_p[j] + iss_kc, lds_offset(b_lds + iss_stage * kRTileElems + blk));
-    }
-    iss_stage = iss_stage == kRStages - 1 ? 0 : iss_stage + 1;
-    if (++iss_step < n_steps) {
-      iss_kc += kRKc;
-      if (iss_kc == dim) {
-        iss_kc = 0;
-        ++iss_dt;
+  // DMA q (0..3) of the next step: block q >> 1 of the dictionary (q even) or
+  // source (q odd) operand; the last one moves on to the following step.
+  auto issue_one = [&](int q) {
+    if (q == 0 && iss_dt != cur_dt) set_dtile(iss_dt);
+    const int blk = (32 * wave + 16 * (q >> 1)) * kRKc;
+    if ((q & 1) == 0)
+      lds_dma16_addr(dict_p[q >> 1] + iss_kc, lds_offset(a_lds + iss_stage * kRTileElems + blk));
+    else
+      lds_dma16_addr(src_p[q >> 1] + iss_kc, lds_offset(b_lds + iss_stage * kRTileElems + blk));
+    if (q == 3) {
+      iss_stage = iss_stage == kRStages - 1 ? 0 : iss_stage + 1;
+      if (++iss_step < n_steps) {
+        iss_kc += kRKc;
+        if (iss_kc == dim) {
+          iss_kc = 0;
+          ++iss_dt;
+        }
       }
     }
+  };
+  auto issue_next = [&]() {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) issue_one(q);
   };
   // Operand read offsets (elements) within a 32-row block: logical chunk 2t+hh
   // of row l32; sw4 of rows 32*x + l32 + base depends on l32 only.
@@ -497,24 +510,74 @@ __global__ __launch_bounds__(kRWaves * 64, 1) void sim_topk_ring_kernel(
   }
   int dt = 0, kcs = 0, stage = 0;
   for (int step = 0; step < n_steps; ++step) {
+    const int next = stage == kRStages - 1 ? 0 : stage + 1;
+    // Before the barrier: k-step 0's MFMAs (operands read in the previous
+    // step) and the reads of k-step 1's operands, whose stage landed before
+    // the previous barrier.  A wave arriving at the barrier leaves MFMAs in
+    // the pipe, and the other wave of its SIMD keeps issuing them, so barrier
+    // skew does not idle the matrix cores.
+    if (K == 1) {
+      // The compiler interleaves the reads with the MFMAs.
+      read_half(stage, 1, a1, b1);
+      mma_half(a0, b0);
+    } else {
+      // One read after each MFMA (the top-4 epilogue leaves the compiler
+      // fewer registers to hoist the reads with).
+      const bf16_t* al = a_lds + stage * kRTileElems + wd * 128 * kRKc;
+      const bf16_t* bl = b_lds + stage * kRTileElems + ws * 64 * kRKc;
+#pragma unroll
+      for (int x = 0; x < 4; ++x)
+#pragma unroll
+        for (int y = 0; y < 2; ++y) {
+          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[x], b0[y], acc[x][y], 0, 0, 0);
+          const int q = 2 * x + y;
+          if (q < 4) a1[q] = *reinterpret_cast<const bf16x8*>(al + q * 32 * kRKc + off[1]);
+          else if (q < 6) b1[q - 4] = *reinterpret_cast<const bf16x8*>(bl + (q - 4) * 32 * kRKc + off[1]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
     // After this barrier step + 1 has landed for every wave and every wave
-    // has finished step - 1, whose stage the next DMA refills.  A wave's
+    // has finished step - 1, whose stage the DMAs below refill.  A wave's
     // reads of a stage are consumed by its MFMAs before its next barrier, so
     // the barrier need not wait for LDS reads in flight.
     wait_vmem<(kRAhead - 2) * kRDmaPerStep>();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    issue_next();
-    const int next = stage == kRStages - 1 ? 0 : stage + 1;
-    read_half(stage, 1, a1, b1);
-    __builtin_amdgcn_sched_barrier(0);
-    mma_half(a0, b0);
-    __builtin_amdgcn_sched_barrier(0);
-    // Unconditional: after the last step this reads a stage nobody uses,
-    // and a branch here would make the wait below cover these reads too.
-    read_half(next, 0, a0, b0);
-    __builtin_amdgcn_sched_barrier(0);
-    mma_half(a1, b1);
+    // k-step 1's MFMAs with step + 4's four DMAs issued between them: a DMA
+    // issue can stall the wave while the CU's DMA queue is full, and the
+    // MFMAs issued before it keep the pipe busy meanwhile.  The reads of the
+    // next step's k-step 0 operands are unconditional: after the last step
+    // they read a stage nobody uses, and a branch here would make the wait
+    // above cover them too.
+    if (K == 1) {
+      read_half(next, 0, a0, b0);
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+#pragma unroll
+        for (int y = 0; y < 2; ++y)
+          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[x], b1[y], acc[x][y], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        issue_one(x);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+      const bf16_t* al = a_lds + next * kRTileElems + wd * 128 * kRKc;
+      const bf16_t* bl = b_lds + next * kRTileElems + ws * 64 * kRKc;
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+#pragma unroll
+        for (int y = 0; y < 2; ++y) {
+          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[x], b1[y], acc[x][y], 0, 0, 0);
+          const int q = 2 * x + y;
+          if (q < 4) a0[q] = *reinterpret_cast<const bf16x8*>(al + q * 32 * kRKc + off[0]);
+          else if (q < 6) b0[q - 4] = *reinterpret_cast<const bf16x8*>(bl + (q - 4) * 32 * kRKc + off[0]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        issue_one(x);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
     stage = next;
     if (kcs == n_chunks - 1) {
       if (!all_src_ok) {
