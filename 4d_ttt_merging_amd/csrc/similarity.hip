@@ -71,6 +71,28 @@ __device__ __forceinline__ uint64_t make_key(float score, int j) {
          static_cast<uint64_t>(0xFFFFFFFFu - static_cast<uint32_t>(j));
 }
 
+// Key of a score at position pos (< 0x10000) of a lane's dictionary tile, for
+// a score that is not NaN: ord16 of its bf16 rounding t in the high half (t
+// with the sign bit set for t >= 0, which also folds -0 onto +0; t with its
+// upper 16 bits inverted for t < 0) and 0xFFFF - pos in the low half.
+__device__ __forceinline__ uint32_t tile_key(float score, int pos) {
+  const float t = bf16_round(score);
+  const uint32_t k = __builtin_bit_cast(uint32_t, t) | (0x80000000u | (0xFFFFu - static_cast<uint32_t>(pos)));
+  return t < 0.0f ? k ^ 0xFFFF0000u : k;
+}
+// The make_key() key of a tile key whose lane's tile starts at row j0.
+__device__ __forceinline__ uint64_t tile_key_to_key(uint32_t k, int j0) {
+  const uint32_t j = static_cast<uint32_t>(j0) + (0xFFFFu - (k & 0xFFFFu));
+  return (static_cast<uint64_t>(k >> 16) << 32) | static_cast<uint64_t>(0xFFFFFFFFu - j);
+}
+// Median of three unsigned integers (v_med3_u32; the compiler forms it from
+// min/max only in some cases).
+__device__ __forceinline__ uint32_t med3_u32(uint32_t a, uint32_t b, uint32_t c) {
+  uint32_t d;
+  asm("v_med3_u32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+}
+
 template <int K>
 struct TopK {
   uint64_t k[K];
@@ -678,15 +700,59 @@ __global__ __launch_bounds__(kRWaves * 64, 1) void sim_topk_ring_kernel(
           }
         }
       } else {
+        // Full tiles without a NaN in the wave: a tile-local top-4 of 32-bit
+        // keys per source, merged into the running list once.  tile_key()
+        // puts ord16 of the bf16 score in the high half and 0xFFFF - position
+        // in the low half, so a larger key is a larger score or, for equal
+        // scores, the lower dictionary row; a sorted list takes a key with one
+        // max and three medians.  Other tiles take the per-score inserts.
+        const bool full = d0 + kRTile <= d_end;
+        bool fast = false;
+        if (full) {
+          float m = acc[0][0][0];
 #pragma unroll
-        for (int sb = 0; sb < 2; ++sb)
+          for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
-          for (int db = 0; db < 4; ++db)
+            for (int db = 0; db < 4; ++db)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int jj = jl + 32 * db + 8 * (r >> 2) + (r & 3);
-              if (jj < d_end) best[sb].insert(make_key(acc[db][sb][r], jj));
-            }
+              for (int r = 0; r < 16; r += 2)
+                m = __builtin_elementwise_maximum(__builtin_elementwise_maximum(m, acc[db][sb][r]),
+                                                  acc[db][sb][r + 1]);
+          fast = __ballot(m != m) == 0;
+        }
+        if (fast) {
+#pragma unroll
+          for (int sb = 0; sb < 2; ++sb) {
+            uint32_t l0 = 0, l1 = 0, l2 = 0, l3 = 0;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) {
+                const uint32_t key = tile_key(acc[db][sb][r], 32 * db + 8 * (r >> 2) + (r & 3));
+                const uint32_t n1 = med3_u32(l0, l1, key);
+                const uint32_t n2 = med3_u32(l1, l2, key);
+                l3 = med3_u32(l2, l3, key);
+                l0 = max(l0, key);
+                l1 = n1;
+                l2 = n2;
+              }
+            // 64 keys went in, so all four slots hold scores.
+            best[sb].insert(tile_key_to_key(l0, jl));
+            best[sb].insert(tile_key_to_key(l1, jl));
+            best[sb].insert(tile_key_to_key(l2, jl));
+            best[sb].insert(tile_key_to_key(l3, jl));
+          }
+        } else {
+#pragma unroll
+          for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) {
+                const int jj = jl + 32 * db + 8 * (r >> 2) + (r & 3);
+                if (jj < d_end) best[sb].insert(make_key(acc[db][sb][r], jj));
+              }
+        }
       }
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb)
