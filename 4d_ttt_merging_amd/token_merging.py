@@ -508,15 +508,19 @@ def build_fastvggt_plan(
     if total != frames * tokens_per_frame or patch_token_start + math.prod(patch_hw) != tokens_per_frame:
         raise ValueError("Invalid Omega FastVGGT frame/patch/special-token layout")
     device = tokens.device
-    identity = torch.arange(total, device=device).expand(batch, -1)
-    if frames == 1 or merge_ratio == 0:
+
+    def identity_plan():
+        identity = torch.arange(total, device=device).expand(batch, -1)
         return TokenPlan(identity, identity, total)
+
+    if frames == 1 or merge_ratio == 0:
+        return identity_plan()
     sources, destinations = _fastvggt_layout(
         total, frames, tokens_per_frame, patch_token_start, tuple(patch_hw), float(protect_ratio),
         int(seed), device)
     removed = min(int(total * merge_ratio), sources.numel())
     if removed == 0:
-        return TokenPlan(identity, identity, total)
+        return identity_plan()
     if not tokens.is_cuda:
         raise RuntimeError("vgo kernels run on the GPU only; got a CPU tensor")
 
@@ -553,8 +557,10 @@ def build_fastvggt_plan(
     if mass_bias:
         if batch != 1:
             raise ValueError("mass-bias FastVGGT plans support batch size one")
-        csr, _ = plan._cluster_csr(0)
-        _, log_mass = _kernels.segment_mass(csr.offsets, 1, csr.order, None, plan.kept_tokens,
-                                            0.0, want_log=True)
+        # One mass pass gives the cluster counts _cluster_csr caches and their logs.
+        order, offsets = _kernels.csr_build(inverse[0], plan.kept_tokens)
+        counts, log_mass = _kernels.segment_mass(offsets, 1, order, None, plan.kept_tokens, 0.0,
+                                                 want_log=True)
+        plan._derived[("csr", 0)] = (_Csr(order, offsets), counts, None)
         plan.key_log_mass = log_mass.view(1, -1)
     return plan
