@@ -323,6 +323,44 @@ struct CompactOuts {
   int64_t ots[G], ohs[G];
 };
 
+// acc[g][j] = acc[g][j] / n, correctly rounded as the division (n is the
+// row's normalizer, the same in every lane).  n == 1 leaves acc as it is.
+// Otherwise, when every value of the wave lies in [2^-100, FLT_MAX], each takes
+// three operations instead of a division: with r = RN(1/n), q = RN(a*r) and
+// the exact residual e = fma(-q, n, a), fma(e, r, q) is the correctly rounded
+// a/n (Markstein's theorem: r within half an ulp of 1/n, q within one ulp of
+// a/n, e exact).  The range keeps e clear of the subnormals, where the
+// residual can round; zeros, subnormals, infinities and NaNs take the division.
+template <int G>
+__device__ __forceinline__ void divide_by_normalizer(float (&acc)[G][16], float n) {
+  if (n == 1.0f) return;
+  float lo = __builtin_inff(), hi = 0.0f;
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      lo = fminf(lo, fabsf(acc[g][j]));
+      hi = __builtin_elementwise_maximum(hi, fabsf(acc[g][j]));  // a NaN propagates
+    }
+  const bool in_range = lo >= 0x1p-100f && hi <= 3.40282347e+38f;
+  if (__ballot(!in_range) == 0) {
+    const float r = 1.0f / n;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const float a = acc[g][j];
+        const float q = a * r;
+        acc[g][j] = fmaf(fmaf(-q, n, a), r, q);
+      }
+  } else {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[g][j] = acc[g][j] / n;
+  }
+}
+
 template <typename TI, typename TO, int G>
 __global__ __launch_bounds__(256) void compact16_kernel(
     const TI* __restrict__ x, int64_t xts, int64_t xhs, int64_t x_rows,
@@ -480,13 +518,11 @@ __global__ __launch_bounds__(256) void compact16_kernel(
       }
     }
     if (active) {
+      divide_by_normalizer<G>(acc, nk);
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) acc[g][j] = acc[g][j] / nk;
+      for (int g = 0; g < G; ++g)
         v16_store(o.out[g] + static_cast<int64_t>(k) * o.ots[g] + static_cast<int64_t>(c >> 6) * o.ohs[g] + (c & 63),
                   acc[g]);
-      }
     }
   }
 }
