@@ -168,14 +168,14 @@ __device__ __forceinline__ void head_layer_norm(float* v, const float* w, const 
   float q = 0.0f;
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
-    const float d = v[j] - mean;
-    q = fmaf(d, d, q);
+    v[j] = v[j] - mean;  // kept centred for the scaling below
+    q = fmaf(v[j], v[j], q);
   }
   q += quad_xor<1>(q);
   q += quad_xor<2>(q);
   const float rstd = 1.0f / sqrtf(q / 64.0f + eps);
 #pragma unroll
-  for (int j = 0; j < 16; ++j) v[j] = (v[j] - mean) * rstd * w[j] + b[j];
+  for (int j = 0; j < 16; ++j) v[j] = fmaf(v[j] * rstd, w[j], b[j]);
 }
 
 // ------------------------------------------------------------ LDS DMA ----
