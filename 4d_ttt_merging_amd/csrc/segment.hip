@@ -490,8 +490,13 @@ __global__ __launch_bounds__(256) void compact16_kernel(
           for (int g = 0; g < G; ++g) {
             v16_widen(cur[g], v[g]);
             layer_norm(g, v[g]);
+            if (weights) {
 #pragma unroll
-            for (int j = 0; j < 16; ++j) seg[g][j] = seg[g][j] + v[g][j] * w_c;
+              for (int j = 0; j < 16; ++j) seg[g][j] = seg[g][j] + v[g][j] * w_c;
+            } else {  // w_c == 1
+#pragma unroll
+              for (int j = 0; j < 16; ++j) seg[g][j] = seg[g][j] + v[g][j];
+            }
           }
         }
         if (q + 1 == t_end) {

@@ -173,7 +173,9 @@ __device__ __forceinline__ void head_layer_norm(float* v, const float* w, const 
   }
   q += quad_xor<1>(q);
   q += quad_xor<2>(q);
-  const float rstd = 1.0f / sqrtf(q / 64.0f + eps);
+  // v_rsq_f32 (about 1 ulp; var + eps >= eps > 0 is a normal number), as the
+  // reference's GPU LayerNorm takes rsqrt rather than a rounded 1 / sqrt.
+  const float rstd = __builtin_amdgcn_rsqf(q / 64.0f + eps);
 #pragma unroll
   for (int j = 0; j < 16; ++j) v[j] = fmaf(v[j] * rstd, w[j], b[j]);
 }
