@@ -24,21 +24,18 @@ constexpr int kSortRounds = 8;
 constexpr int kBlockItems = kSortThreads * kSortRounds;  // 2048 items per block
 constexpr int kSortWaves = kSortThreads / 64;
 
-__global__ __launch_bounds__(kSortThreads) void clamp_keys_kernel(const uint32_t* __restrict__ in,
-                                                                  uint32_t* __restrict__ keys,
-                                                                  uint32_t* __restrict__ vals,
-                                                                  int n, uint32_t limit) {
-  const int i = blockIdx.x * kSortThreads + threadIdx.x;
-  if (i >= n) return;
-  const uint32_t k = in[i];
-  keys[i] = k < limit ? k : limit;  // out-of-range keys sort past the last bucket
-  vals[i] = static_cast<uint32_t>(i);
+// The first pass reads the caller's keys with `limit` = n_buckets: a key at or
+// past it (a negative id too) sorts past the last bucket.  Later passes read
+// clamped keys (limit 0: as they are).
+__device__ __forceinline__ uint32_t sort_key(const uint32_t* keys, int i, uint32_t limit) {
+  const uint32_t k = keys[i];
+  return limit != 0u && k > limit ? limit : k;
 }
 
 __global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(const uint32_t* __restrict__ keys,
                                                                   int n, int shift,
                                                                   uint32_t* __restrict__ hist,
-                                                                  int nblocks) {
+                                                                  int nblocks, uint32_t limit) {
   __shared__ uint32_t h[256];
   const int tid = threadIdx.x;
   h[tid] = 0;
@@ -47,7 +44,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(const uint32_t
 #pragma unroll
   for (int r = 0; r < kSortRounds; ++r) {
     const int i = base + r * kSortThreads + tid;
-    if (i < n) atomicAdd(&h[(keys[i] >> shift) & 0xFF], 1u);
+    if (i < n) atomicAdd(&h[(sort_key(keys, i, limit) >> shift) & 0xFF], 1u);
   }
   __syncthreads();
   hist[tid * nblocks + blockIdx.x] = h[tid];
@@ -87,10 +84,11 @@ __global__ __launch_bounds__(1024) void exclusive_scan_kernel(uint32_t* __restri
   }
 }
 
+// vals_in == nullptr (the first pass): the values are the item indices.
 __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
     uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out, int n, int shift,
-    const uint32_t* __restrict__ hist_scan, int nblocks) {
+    const uint32_t* __restrict__ hist_scan, int nblocks, uint32_t limit) {
   __shared__ uint32_t base[256];
   __shared__ uint32_t running[256];
   __shared__ uint32_t wcnt[kSortWaves][256];
@@ -106,8 +104,8 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     const bool valid = i < n;
     uint32_t key = 0, val = 0, d = 0;
     if (valid) {
-      key = keys_in[i];
-      val = vals_in[i];
+      key = sort_key(keys_in, i, limit);
+      val = vals_in ? vals_in[i] : static_cast<uint32_t>(i);
       d = (key >> shift) & 0xFF;
     }
     uint64_t same = __ballot(valid);
@@ -617,17 +615,19 @@ extern "C" int vgo_csr_build(const uint32_t* keys, int64_t n_items, int64_t n_bu
   // Value buffers ping-pong between va and `order` so the last pass lands in `order`.
   uint32_t* vbuf[2] = {va, order};
   uint32_t* kbuf[2] = {ka, kb};
-  int cur = passes % 2 == 0 ? 1 : 0;  // buffer index holding the input of pass 0
-  // vals start in vbuf[cur]; after `passes` flips they end in vbuf[(cur + passes) % 2] == order.
-  hipLaunchKernelGGL(clamp_keys_kernel, dim3((n + kSortThreads - 1) / kSortThreads), dim3(kSortThreads), 0,
-                     s, keys, kbuf[cur], vbuf[cur], n, static_cast<uint32_t>(nb));
+  int cur = passes % 2 == 0 ? 1 : 0;  // pass p writes buffer (cur + p + 1) % 2
+  // Pass 0 reads the caller's keys (clamped as it reads them) and the item
+  // indices; after `passes` flips the values end in vbuf[(cur + passes) % 2] == order.
   for (int p = 0; p < passes; ++p) {
     const int shift = 8 * p;
-    hipLaunchKernelGGL(radix_hist_kernel, dim3(nblocks), dim3(kSortThreads), 0, s, kbuf[cur], n,
-                       shift, hist, nblocks);
+    const uint32_t* kin = p == 0 ? keys : kbuf[cur];
+    const uint32_t* vin = p == 0 ? nullptr : vbuf[cur];
+    const uint32_t limit = p == 0 ? static_cast<uint32_t>(nb) : 0u;
+    hipLaunchKernelGGL(radix_hist_kernel, dim3(nblocks), dim3(kSortThreads), 0, s, kin, n, shift, hist,
+                       nblocks, limit);
     hipLaunchKernelGGL(exclusive_scan_kernel, dim3(1), dim3(1024), 0, s, hist, 256 * nblocks);
-    hipLaunchKernelGGL(radix_scatter_kernel, dim3(nblocks), dim3(kSortThreads), 0, s, kbuf[cur],
-                       vbuf[cur], kbuf[1 - cur], vbuf[1 - cur], n, shift, hist, nblocks);
+    hipLaunchKernelGGL(radix_scatter_kernel, dim3(nblocks), dim3(kSortThreads), 0, s, kin, vin,
+                       kbuf[1 - cur], vbuf[1 - cur], n, shift, hist, nblocks, limit);
     cur = 1 - cur;
   }
   hipLaunchKernelGGL(bucket_offsets_kernel, dim3((n + 255) / 256), dim3(256), 0, s, kbuf[cur], n,
