@@ -323,12 +323,14 @@ struct CompactOuts {
 
 // acc[g][j] = acc[g][j] / n, correctly rounded as the division (n is the
 // row's normalizer, the same in every lane).  n == 1 leaves acc as it is.
-// Otherwise, when every value of the wave lies in [2^-100, FLT_MAX], each takes
-// three operations instead of a division: with r = RN(1/n), q = RN(a*r) and
-// the exact residual e = fma(-q, n, a), fma(e, r, q) is the correctly rounded
-// a/n (Markstein's theorem: r within half an ulp of 1/n, q within one ulp of
-// a/n, e exact).  The range keeps e clear of the subnormals, where the
-// residual can round; zeros, subnormals, infinities and NaNs take the division.
+// Otherwise, when 1 <= n <= 2^16 (cluster counts and masses) and every value of
+// the wave lies in [2^-100, FLT_MAX], each takes three operations instead of a
+// division: with r = RN(1/n), q = RN(a*r) and the exact residual
+// e = fma(-q, n, a), fma(e, r, q) is the correctly rounded a/n (Markstein's
+// theorem: r within half an ulp of 1/n, q within one ulp of a/n, e exact).
+// These ranges keep q finite and q and e clear of the subnormals, where the
+// residual can round; anything else (zeros, subnormals, infinities, NaNs, other
+// normalizers) takes the division.
 template <int G>
 __device__ __forceinline__ void divide_by_normalizer(float (&acc)[G][16], float n) {
   if (n == 1.0f) return;
@@ -340,7 +342,7 @@ __device__ __forceinline__ void divide_by_normalizer(float (&acc)[G][16], float 
       lo = fminf(lo, fabsf(acc[g][j]));
       hi = __builtin_elementwise_maximum(hi, fabsf(acc[g][j]));  // a NaN propagates
     }
-  const bool in_range = lo >= 0x1p-100f && hi <= 3.40282347e+38f;
+  const bool in_range = lo >= 0x1p-100f && hi <= 3.40282347e+38f && n >= 1.0f && n <= 65536.0f;
   if (__ballot(!in_range) == 0) {
     const float r = 1.0f / n;
 #pragma unroll

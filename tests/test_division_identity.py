@@ -1,10 +1,11 @@
 """The compaction divides a row's pooled values by its normalizer n without a
 division per value: with r = RN(1/n), q = RN(a*r), e = fma(-q, n, a) (exact) and
 q' = fma(e, r, q), q' is the correctly rounded a/n (Markstein's theorem), which the
-kernel uses for every value in [2^-100, FLT_MAX] (csrc/segment.hip,
-divide_by_normalizer).  Checked here in exact rational arithmetic with one rounding
-per operation, for integer counts and fractional masses >= 1, random values, values
-next to exact quotients, sparse mantissas and the ends of that range."""
+kernel uses for every value in [2^-100, FLT_MAX] and normalizers in [1, 2^16]
+(csrc/segment.hip, divide_by_normalizer).  Checked here in exact rational arithmetic
+with one rounding per operation, for integer counts and fractional masses in
+[1, 2^16], random values, values next to exact quotients, sparse mantissas and the
+ends of that range."""
 import random
 from fractions import Fraction
 
@@ -39,8 +40,9 @@ def corrected_quotient(a: np.float32, n: np.float32) -> np.float32:
 
 def test_markstein_corrected_quotient_is_the_rounded_division():
     rng = random.Random(11)
-    divisors = [np.float32(b) for b in (1, 2, 3, 5, 7, 9, 11, 13, 27, 31, 63)]
+    divisors = [np.float32(b) for b in (1, 2, 3, 5, 7, 9, 11, 13, 27, 31, 63, 1023, 65535, 65536)]
     divisors += [np.float32(1 + rng.random() * 20) for _ in range(8)]
+    divisors += [np.float32(rng.uniform(1, 65536)) for _ in range(4)]
     checked = 0
     for n in divisors:
         fn = Fraction(float(n))

@@ -396,6 +396,29 @@ def test_weighted_plan_compact_restore_bit_exact(vgo, device, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_weighted_plan_compact_edge_normalizers(vgo, device, dtype):
+    """Normalizers outside the counts-and-masses range [1, 2^16] and rows of
+    tiny values take the plain division; the result is still the oracle's."""
+    print(f"[edge normalizers] dtype={dtype}", flush=True)
+    keep, src, parent, w = _random_weighted_plan(13, 2000, 600, 1400)
+    mass = om.deterministic_weighted_normalizer(parent[None], w[None], 600).clone()
+    edges = [0.25, 1e-20, 1e20, 70000.3, 65536.0, 65535.5, float("inf"), 0.75, 1.0, 3.0]
+    for i, e in enumerate(edges):
+        mass[0, 7 * i] = e
+    plan = vgo.WeightedBilinearTokenPlan(
+        keep=keep[None].to(device), source_original=src[None].to(device),
+        source_parent_compact=parent[None].to(device), source_pool_weights=w[None].to(device),
+        source_restore_weights=w[None].to(device), original_tokens=2000,
+        normalizer=mass.to(device))
+    # scales: in range; straddling 2^-100; results down in the subnormals
+    for scale in (1.0, 1e-28, 1e-37):
+        value = (seeded_values(14, (1, 2000, 1024), torch.float32) * scale).to(dtype)
+        out = plan.compact(value.to(device))
+        ref = om.weighted_compact(keep, src, parent, w, mass[0], value[0])
+        assert torch.equal(out[0].cpu(), ref), scale
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_token_plan_compact_restore_bit_exact(vgo, device, fx, dtype):
     inv = torch.from_numpy(fx["fv50_inverse"])
     keep = torch.from_numpy(fx["fv50_keep"])
