@@ -23,8 +23,10 @@
 //    softmax offset ride in the MFMA too: a fifth k-step multiplies the
 //    key-side column pair (hi, lo) = log2(e)*log m split into two input-dtype
 //    values (exact to ~2^-17) and a column of ones with the query-side
-//    (1, 1, -mref).  The reference rounds log(m) to the input dtype first
-//    (mass_bias_attention.py:109); so do we.
+//    (1, 1, -mref).  It has three terms, so it runs as one 8-deep
+//    v_mfma_f32_32x32x8, which takes the matrix pipe for less time than a
+//    16-deep one (same accumulator layout, same sums).  The reference rounds
+//    log(m) to the input dtype first (mass_bias_attention.py:109); so do we.
 //  * Lazy online softmax: P = 2^S straight from the accumulator while no
 //    logit exceeds the reference max mref by more than 8 (checked through the
 //    per-lane sums); only then, and on a segment's first tile, are the tile's
@@ -66,6 +68,12 @@ struct Mma<bf16_t> {
   static __device__ __forceinline__ f32x16 mma(op8 a, op8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
+  // 8-deep product (lanes 0-31 hold k-slots 0-3, lanes 32-63 slots 4-7).
+  static __device__ __forceinline__ f32x16 mma8(op4 a, op4 b, f32x16 c) {
+    typedef short s4 __attribute__((ext_vector_type(4)));
+    return __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(__builtin_bit_cast(s4, a), __builtin_bit_cast(s4, b), c,
+                                                     0, 0, 0);
+  }
 };
 template <>
 struct Mma<f16_t> {
@@ -74,6 +82,9 @@ struct Mma<f16_t> {
   typedef f16x4 op4;
   static __device__ __forceinline__ f32x16 mma(op8 a, op8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x16 mma8(op4 a, op4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x8f16(a, b, c, 0, 0, 0);
   }
 };
 
@@ -224,21 +235,22 @@ struct WaveAttn {
     }
   }
 
-  // The bias k-step.  A (keys; lanes 0-31 hold k-slots 0-7 of key l32, lanes
-  // 32-63 slots 8-15): {bias_hi, bias_lo, 1, 0, ...}, the key's log2(e)*bias
-  // split into two T values.  B (queries): {1, 1, -offset, 0, ...}.
+  // The bias k-step (8 deep).  A (keys; lanes 0-31 hold k-slots 0-3 of key
+  // l32, lanes 32-63 slots 4-7): {bias_hi, bias_lo, 1, 0}, the key's
+  // log2(e)*bias split into two T values, and zeros.  B (queries):
+  // {1, 1, -offset, 0}, and zeros.
   __device__ __forceinline__ uint32_t neg_bits(float offset) const {
     return __builtin_bit_cast(uint16_t, static_cast<T>(-offset)) & low_lanes;
   }
   // Built where it is used (it is needed once per tile) rather than held.
-  __device__ __forceinline__ op8 offset_b(uint32_t neg) const {
-    const i32x4 w = {static_cast<int>((one_bits | (one_bits << 16)) & low_lanes), static_cast<int>(neg), 0, 0};
-    return __builtin_bit_cast(op8, w);
+  __device__ __forceinline__ op4 offset_b(uint32_t neg) const {
+    const i32x2 w = {static_cast<int>((one_bits | (one_bits << 16)) & low_lanes), static_cast<int>(neg)};
+    return __builtin_bit_cast(op4, w);
   }
-  __device__ __forceinline__ op8 bias_a(const T* bl, int sub) const {
+  __device__ __forceinline__ op4 bias_a(const T* bl, int sub) const {
     const uint32_t bw = *reinterpret_cast<const uint32_t*>(bl + boff[sub]);
-    const i32x4 w = {static_cast<int>(bw), static_cast<int>(one_bits & low_lanes), 0, 0};
-    return __builtin_bit_cast(op8, w);
+    const i32x2 w = {static_cast<int>(bw), static_cast<int>(one_bits & low_lanes)};
+    return __builtin_bit_cast(op4, w);
   }
   // A operand of rows 32*half.. of a K or V^T tile, k-chunk pair t.
   __device__ __forceinline__ op8 tile_op(const T* tl, int half, int t) const {
@@ -249,7 +261,7 @@ struct WaveAttn {
   // the reads overlap each other rather than each MFMA waiting for its own).
   struct KOps {
     op8 k[2][4];  // K rows 32*sub.., k-chunk pair t
-    op8 b[2];     // bias k-step A operands
+    op4 b[2];     // bias k-step A operands
   };
   struct VOps {
     op8 v[4][2];  // V^T rows (dims) 32*dt.., key chunk pair t
@@ -280,7 +292,7 @@ struct WaveAttn {
 #pragma unroll
         for (int qb = 0; qb < kQB; ++qb) s[qb][sub] = Mma<T>::mma(ops.k[sub][t], qreg[qb][t], s[qb][sub]);
 #pragma unroll
-      for (int qb = 0; qb < kQB; ++qb) s[qb][sub] = Mma<T>::mma(ops.b[sub], offset_b(qneg[qb]), s[qb][sub]);
+      for (int qb = 0; qb < kQB; ++qb) s[qb][sub] = Mma<T>::mma8(ops.b[sub], offset_b(qneg[qb]), s[qb][sub]);
     }
   }
   __device__ __forceinline__ void scores(const T* kl, const T* bl, f32x16 (&s)[kQB][2]) const {
@@ -322,7 +334,7 @@ struct WaveAttn {
     f32x16 x = {};
 #pragma unroll
     for (int t = 0; t < 4; ++t) x = Mma<T>::mma(tile_op(kl, sub, t), qreg[qb][t], x);
-    return Mma<T>::mma(bias_a(bl, sub), offset_b(0u), x);
+    return Mma<T>::mma8(bias_a(bl, sub), offset_b(0u), x);
   }
 
   // Lazy online softmax of one tile's scores.  P = 2^S directly while every
@@ -421,7 +433,7 @@ struct WaveAttn {
     op8 ka[4], kb[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) ka[t] = tile_op(kl, 0, t);
-    const op8 ba = bias_a(bl, 0);
+    const op4 ba = bias_a(bl, 0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 2; t < 4; ++t)
@@ -432,13 +444,13 @@ struct WaveAttn {
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 0; t < 4; ++t) kb[t] = tile_op(kl, 1, t);
-    const op8 bb = bias_a(bl, 1);
+    const op4 bb = bias_a(bl, 1);
 #pragma unroll
     for (int qb = 0; qb < kQB; ++qb) {
       s[qb][0] = f32x16{};
 #pragma unroll
       for (int t = 0; t < 4; ++t) s[qb][0] = Mma<T>::mma(ka[t], qreg[qb][t], s[qb][0]);
-      s[qb][0] = Mma<T>::mma(ba, offset_b(qneg[qb]), s[qb][0]);
+      s[qb][0] = Mma<T>::mma8(ba, offset_b(qneg[qb]), s[qb][0]);
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -446,7 +458,7 @@ struct WaveAttn {
       s[qb][1] = f32x16{};
 #pragma unroll
       for (int t = 0; t < 4; ++t) s[qb][1] = Mma<T>::mma(kb[t], qreg[qb][t], s[qb][1]);
-      s[qb][1] = Mma<T>::mma(bb, offset_b(qneg[qb]), s[qb][1]);
+      s[qb][1] = Mma<T>::mma8(bb, offset_b(qneg[qb]), s[qb][1]);
     }
   }
 
