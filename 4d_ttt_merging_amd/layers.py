@@ -56,7 +56,50 @@ def rope_apply(x: Tensor, sin: Tensor, cos: Tensor) -> Tensor:
     return (x * cos) + (rope_rotate_half(x) * sin)
 
 
-class LinearKMaskedBias(nn.Linear):
+class Linear(nn.Linear):
+    """nn.Linear whose autocast inference casts its parameters once.
+
+    Under CUDA bf16/f16 autocast, F.linear casts the fp32 weight and bias to the
+    autocast dtype on every call (a copy kernel each).  When no gradient is
+    recorded, the cast copies are kept and reused until a parameter changes
+    (its version counter or its storage), so the GEMM gets the operands that
+    autocast would give it and the result is the same.  Writes that bypass the
+    version counter (through `.data`) must be followed by `clear_cast_cache()`."""
+
+    def clear_cast_cache(self) -> None:
+        self.__dict__.pop("_cast_cache", None)
+
+    def _bias(self) -> Tensor | None:
+        return self.bias
+
+    def _cast_sources(self) -> tuple:
+        return (self.weight, self.bias)
+
+    def _cast_params(self, dtype: torch.dtype):
+        try:
+            key = (dtype,) + tuple(None if t is None else (t.data_ptr(), t._version)
+                                   for t in self._cast_sources())
+        except RuntimeError:  # inference tensors keep no version counter
+            return None
+        cache = self.__dict__.get("_cast_cache")
+        if cache is None or cache[0] != key:
+            bias = self._bias()
+            cache = (key, self.weight.to(dtype), None if bias is None else bias.to(dtype))
+            self.__dict__["_cast_cache"] = cache
+        return cache[1], cache[2]
+
+    def forward(self, input: Tensor) -> Tensor:
+        dtype = _autocast_dtype()
+        # A traced graph (torch.compile) keeps autocast's casts as graph nodes.
+        if (dtype is not None and not torch.is_grad_enabled() and self.weight.is_cuda
+                and not torch.compiler.is_compiling()):
+            cast = self._cast_params(dtype)
+            if cast is not None:
+                return F.linear(input, *cast)
+        return F.linear(input, self.weight, self._bias())
+
+
+class LinearKMaskedBias(Linear):
     """qkv projection whose K third of the bias is masked to zero (attention.py:195-207)."""
 
     def __init__(self, *args, **kwargs):
@@ -68,9 +111,11 @@ class LinearKMaskedBias(nn.Linear):
             bias_mask[o // 3: 2 * o // 3].fill_(0)
             self.register_buffer("bias_mask", bias_mask)
 
-    def forward(self, input: Tensor) -> Tensor:
-        masked_bias = self.bias * self.bias_mask.to(self.bias.dtype) if self.bias is not None else None
-        return F.linear(input, self.weight, masked_bias)
+    def _bias(self) -> Tensor | None:
+        return self.bias * self.bias_mask.to(self.bias.dtype) if self.bias is not None else None
+
+    def _cast_sources(self) -> tuple:
+        return (self.weight, self.bias, getattr(self, "bias_mask", None))
 
 
 class LayerScale(nn.Module):
@@ -96,9 +141,9 @@ class Mlp(nn.Module):
         super().__init__()
         out_features = out_features or in_features
         hidden_features = hidden_features or in_features
-        self.fc1 = nn.Linear(in_features, hidden_features, bias=bias, device=device)
+        self.fc1 = Linear(in_features, hidden_features, bias=bias, device=device)
         self.act = act_layer()
-        self.fc2 = nn.Linear(hidden_features, out_features, bias=bias, device=device)
+        self.fc2 = Linear(hidden_features, out_features, bias=bias, device=device)
         self.drop = nn.Dropout(drop)
 
     def forward(self, x: Tensor) -> Tensor:
@@ -120,10 +165,10 @@ class SelfAttention(nn.Module):
         else:
             self.q_norm = None
             self.k_norm = None
-        linear_class = LinearKMaskedBias if mask_k_bias else nn.Linear
+        linear_class = LinearKMaskedBias if mask_k_bias else Linear
         self.qkv = linear_class(dim, dim * 3, bias=qkv_bias, device=device)
         self.attn_drop = nn.Dropout(attn_drop)
-        self.proj = nn.Linear(dim, dim, bias=proj_bias, device=device)
+        self.proj = Linear(dim, dim, bias=proj_bias, device=device)
         self.proj_drop = nn.Dropout(proj_drop)
 
     def apply_rope(self, q: Tensor, k: Tensor, rope) -> tuple[Tensor, Tensor]:
