@@ -244,8 +244,11 @@ def restore_map(total: int, *, device: torch.device, keep: torch.Tensor | None =
                 inverse: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """Dense [total, 4] (int32 index, fp32 weight) rows consumed by top4_project."""
     lib = _lib.load()
-    index_out = torch.zeros((total, 4), device=device, dtype=torch.int32)
-    weight_out = torch.zeros((total, 4), device=device, dtype=torch.float32)
+    # With `inverse` the kernel writes every row; otherwise rows outside keep and
+    # source stay zero (zero weights, as the reference's `new_zeros` output).
+    alloc = torch.empty if inverse is not None else torch.zeros
+    index_out = alloc((total, 4), device=device, dtype=torch.int32)
+    weight_out = alloc((total, 4), device=device, dtype=torch.float32)
     n_keep = 0 if keep is None else keep.numel()
     n_source = 0 if source is None else source.numel()
     status = lib.vgo_restore_map(
