@@ -63,6 +63,18 @@ def test_linear_cast_cache_equals_autocast(layers, device, dtype, masked):
         # fp32 (no autocast) runs the parameters as they are
         assert torch.equal(lin(x), F.linear(x, lin.weight, lin.bias * lin.bias_mask if masked else lin.bias))
 
+    # copies made under inference_mode serve no_grad calls, and the other way round
+    lin.clear_cast_cache()
+    with torch.inference_mode(), torch.autocast("cuda", dtype=dtype):
+        inf = lin(x)
+    with torch.no_grad(), torch.autocast("cuda", dtype=dtype):
+        assert torch.equal(lin(x), inf)
+    lin.clear_cast_cache()
+    with torch.no_grad(), torch.autocast("cuda", dtype=dtype):
+        ng = lin(x)
+    with torch.inference_mode(), torch.autocast("cuda", dtype=dtype):
+        assert torch.equal(lin(x), ng)
+
     lin.clear_cast_cache()
     with torch.autocast("cuda", dtype=dtype):
         out = lin(x)  # autograd on: no cached copies
