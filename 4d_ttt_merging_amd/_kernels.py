@@ -355,12 +355,14 @@ def _residual_layer_norm_impl(x: torch.Tensor, branch: torch.Tensor | None = Non
 
 
 def _restore_residual_layer_norm_impl(x: torch.Tensor, table: torch.Tensor, index: torch.Tensor,
-                                      weight: torch.Tensor, gamma: torch.Tensor | None,
+                                      weight: torch.Tensor | None, gamma: torch.Tensor | None,
                                       norm: tuple[torch.Tensor | None, torch.Tensor | None, float],
                                       norm_dtype: torch.dtype):
     """One pass over fp32 rows x [N, dim] with the branch restored from `table` on the fly:
     branch = top4_project(table, index, weight) (same rounding), s = x + gamma * branch,
-    n = LayerNorm(s) in `norm_dtype`.  Returns (s, n)."""
+    n = LayerNorm(s) in `norm_dtype`.  With weight None, index is a one-hot int32 [N]
+    map (a token plan's inverse): branch = table[index] (zero rows for index < 0).
+    Returns (s, n)."""
     lib = _lib.load()
     _lib.require_gpu(x, table, index, weight, gamma)
     if x.dtype != torch.float32:
@@ -370,13 +372,17 @@ def _restore_residual_layer_norm_impl(x: torch.Tensor, table: torch.Tensor, inde
     n = rows.shape[0]
     if table.ndim != 2 or table.shape[1] != dim:
         raise ValueError(f"restore_residual_layer_norm: table {tuple(table.shape)} must be [M, {dim}]")
-    if index.shape != (n, 4) or weight.shape != (n, 4):
+    if weight is None:
+        if index.shape != (n,):
+            raise ValueError("restore_residual_layer_norm: a one-hot index must be [rows]")
+    elif index.shape != (n, 4) or weight.shape != (n, 4):
         raise ValueError("restore_residual_layer_norm: index and weight must be [rows, 4]")
-    if index.dtype != torch.int32 or weight.dtype != torch.float32:
+    if index.dtype != torch.int32 or (weight is not None and weight.dtype != torch.float32):
         raise ValueError("restore_residual_layer_norm: int32 indices and float32 weights")
     if norm_dtype not in (torch.bfloat16, torch.float16):
         raise ValueError("restore_residual_layer_norm: norm_dtype must be bfloat16 or float16")
-    index, weight = index.contiguous(), weight.contiguous()
+    index = index.contiguous()
+    weight = None if weight is None else weight.contiguous()
     if table.stride(-1) != 1:
         table = table.contiguous()
     w, b, eps = norm
@@ -388,7 +394,7 @@ def _restore_residual_layer_norm_impl(x: torch.Tensor, table: torch.Tensor, inde
     normed = torch.empty(x.shape, device=x.device, dtype=norm_dtype)
     status = lib.vgo_restore_residual_layer_norm(
         rows.data_ptr(), rows.stride(0), table.data_ptr(), table.stride(0), table.shape[0],
-        _lib.dtype_code(table.dtype), index.data_ptr(), weight.data_ptr(), _c(gamma), _c(w), _c(b),
+        _lib.dtype_code(table.dtype), index.data_ptr(), _c(weight), _c(gamma), _c(w), _c(b),
         float(eps), n, dim, total.data_ptr(), dim, normed.data_ptr(), dim,
         _lib.dtype_code(norm_dtype), _lib.stream_of(x))
     _lib.check(status)
@@ -457,7 +463,7 @@ def residual_layer_norm(x: torch.Tensor, branch: torch.Tensor | None = None,
 
 
 def restore_residual_layer_norm(x: torch.Tensor, table: torch.Tensor, index: torch.Tensor,
-                                weight: torch.Tensor, gamma: torch.Tensor | None,
+                                weight: torch.Tensor | None, gamma: torch.Tensor | None,
                                 norm: tuple[torch.Tensor | None, torch.Tensor | None, float], *,
                                 norm_dtype: torch.dtype = torch.bfloat16):
     """The residual-row pass with the plan restore fused in

@@ -31,7 +31,10 @@
 // (token_merging.py:387-414, 193-196: weight and each product in the value type,
 // fp32 sum, result in the value type), so the restored rows never go to memory:
 // the row's (index, weight) is loaded first, the table rows of its non-zero
-// weights next, under the loads of x and the parameter vectors.
+// weights next, under the loads of x and the parameter vectors.  A token plan
+// restores by a one-hot map, branch[r,:] = table[index[r],:] (its `inverse`,
+// token_merging.py:193-196); with weight == NULL, index is that [rows] array
+// and the pass reads 4 bytes of map per row instead of 32.
 #include "vgo_common.h"
 
 namespace vgo {
@@ -76,7 +79,10 @@ struct RowArgs {
   int64_t table_rows;
 };
 
-template <int kChunks, bool kBranch, bool kGather, typename TB, typename TN>
+// kGather: 0 no restore; 1 restore by a [rows, 4] (index, weight) map; 2 restore
+// by a one-hot [rows] index (a token plan's inverse): the map row (k, 1, 0, 0, 0)
+// for k >= 0, a zero row for k < 0, with the same rounding.
+template <int kChunks, bool kBranch, int kGather, typename TB, typename TN>
 __global__ __launch_bounds__(256) void residual_ln_kernel(RowArgs a) {
   const int lane = lane_id();
   const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 +
@@ -84,11 +90,15 @@ __global__ __launch_bounds__(256) void residual_ln_kernel(RowArgs a) {
   if (r >= a.rows) return;
   // The restore map of the row goes out before everything else: only the
   // table loads wait for it.
+  constexpr int kCorners = kGather == 2 ? 1 : 4;
   i32x4 id4 = {0, 0, 0, 0};
   f32x4 w4 = {0.0f, 0.0f, 0.0f, 0.0f};
-  if constexpr (kGather) {
+  if constexpr (kGather == 1) {
     id4 = *reinterpret_cast<const i32x4*>(a.r_index + 4 * r);
     w4 = *reinterpret_cast<const f32x4*>(a.r_weight + 4 * r);
+  } else if constexpr (kGather == 2) {
+    id4[0] = a.r_index[r];
+    w4[0] = id4[0] >= 0 ? 1.0f : 0.0f;
   }
   const int chunks = a.dim >> 2;
   // Every load is unconditional, so one wait covers them all: a lane's chunk
@@ -133,7 +143,7 @@ __global__ __launch_bounds__(256) void residual_ln_kernel(RowArgs a) {
       bool use[4];
       bool bad = false;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
+      for (int c = 0; c < kCorners; ++c) {
         use[c] = w4[c] != 0.0f;
         if (use[c] && static_cast<uint32_t>(id4[c]) >= static_cast<uint64_t>(a.table_rows)) {
           bad = true;
@@ -149,7 +159,7 @@ __global__ __launch_bounds__(256) void residual_ln_kernel(RowArgs a) {
 #pragma unroll
       for (int i = 0; i < kChunks; ++i) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
+      for (int c = 0; c < kCorners; ++c) {
         if (!use[c]) continue;
         const float wq = weight_as_value<TB>(w4[c]);
 #pragma unroll
@@ -230,7 +240,7 @@ __global__ __launch_bounds__(256) void residual_ln_kernel(RowArgs a) {
     if (live[i]) store4(uo + off[i], v[i] / denom);
 }
 
-template <bool kBranch, typename TB, typename TN, bool kGather = false>
+template <bool kBranch, typename TB, typename TN, int kGather = 0>
 int launch_rows(const RowArgs& a, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>((a.rows + 3) / 4));
   if (a.dim <= 4 * 64 * 4)
@@ -251,14 +261,18 @@ int dispatch_branch(const RowArgs& a, int branch_dtype, hipStream_t s) {
   }
 }
 
-template <typename TN>
+template <typename TN, int kGather>
 int dispatch_restore(const RowArgs& a, int table_dtype, hipStream_t s) {
   switch (table_dtype) {
-    case VGO_BF16: return launch_rows<true, bf16_t, TN, true>(a, s);
-    case VGO_F16: return launch_rows<true, f16_t, TN, true>(a, s);
-    case VGO_F32: return launch_rows<true, float, TN, true>(a, s);
+    case VGO_BF16: return launch_rows<true, bf16_t, TN, kGather>(a, s);
+    case VGO_F16: return launch_rows<true, f16_t, TN, kGather>(a, s);
+    case VGO_F32: return launch_rows<true, float, TN, kGather>(a, s);
     default: return fail(VGO_EINVAL, "restore_residual_layer_norm: unsupported table dtype");
   }
+}
+template <typename TN>
+int dispatch_restore(const RowArgs& a, int table_dtype, hipStream_t s) {
+  return a.r_weight ? dispatch_restore<TN, 1>(a, table_dtype, s) : dispatch_restore<TN, 2>(a, table_dtype, s);
 }
 
 size_t dtype_bytes(int dtype) { return dtype == VGO_F32 ? 4 : 2; }
@@ -319,7 +333,7 @@ extern "C" int vgo_restore_residual_layer_norm(
   using namespace vgo;
   VGO_REQUIRE(rows >= 0 && dim >= 0 && table_rows >= 0, "restore_residual_layer_norm: negative size");
   if (rows == 0 || dim == 0) return VGO_OK;
-  VGO_REQUIRE(x && table && index && weight, "restore_residual_layer_norm: null input");
+  VGO_REQUIRE(x && table && index, "restore_residual_layer_norm: null input");
   VGO_REQUIRE(x_out || norm_out, "restore_residual_layer_norm: no output");
   VGO_REQUIRE(dim % 4 == 0 && dim <= 4 * 64 * kRowChunks,
               "restore_residual_layer_norm: dim must be a multiple of 4 and at most 2048");
@@ -335,8 +349,8 @@ extern "C" int vgo_restore_residual_layer_norm(
   VGO_REQUIRE(vec_ok(x, x_row_stride, 4) && vec_ok(x_out, x_out_row_stride, 4) &&
                   vec_ok(table, table_row_stride, dtype_bytes(table_dtype)) &&
                   vec_ok(norm_out, norm_row_stride, 2) && vec_ok(gamma, 0, 4) &&
-                  vec_ok(ln_weight, 0, 4) && vec_ok(ln_bias, 0, 4) && vec_ok(index, 0, 4) &&
-                  vec_ok(weight, 0, 4),
+                  vec_ok(ln_weight, 0, 4) && vec_ok(ln_bias, 0, 4) &&
+                  (weight ? vec_ok(index, 0, 4) : aligned(index, 4)) && vec_ok(weight, 0, 4),
               "restore_residual_layer_norm: pointers must be 4-element aligned and row strides multiples of 4");
   VGO_REQUIRE(!x_out || x_out == x || x_out_row_stride != 0,
               "restore_residual_layer_norm: zero x_out row stride");

@@ -215,12 +215,13 @@ def _(x, branch, gamma, ln_weight, ln_bias, eps, has_norm, write_sum, norm_dtype
 
 
 @torch.library.custom_op("vgo::restore_residual_layer_norm", mutates_args=(), device_types="cuda")
-def restore_residual_layer_norm(x: Tensor, table: Tensor, index: Tensor, weight: Tensor,
+def restore_residual_layer_norm(x: Tensor, table: Tensor, index: Tensor, weight: Optional[Tensor],
                                 gamma: Optional[Tensor], ln_weight: Optional[Tensor],
                                 ln_bias: Optional[Tensor], eps: float,
                                 norm_dtype: torch.dtype) -> List[Tensor]:
     """[x + gamma * restore(table), LN of that in norm_dtype] with restore = the top-4
-    projection of `table` by (index, weight), never written to memory."""
+    projection of `table` by (index, weight) -- or, without weight, the one-hot gather
+    table[index] -- never written to memory."""
     return list(_kernels._restore_residual_layer_norm_impl(x, table, index, weight, gamma,
                                                            (ln_weight, ln_bias, eps), norm_dtype))
 

@@ -127,10 +127,17 @@ class TokenPlan:
         return self.kept_tokens / self.original_tokens
 
     # Derived device structures, built once per batch element on first use.
+    def _inverse32(self, b: int) -> torch.Tensor:
+        """inverse[b] as int32: the CSR keys and the one-hot restore map."""
+        key = ("inverse32", b)
+        if key not in self._derived:
+            self._derived[key] = self.inverse[b].to(torch.int32).contiguous()
+        return self._derived[key]
+
     def _cluster_csr(self, b: int) -> tuple[_Csr, torch.Tensor]:
         key = ("csr", b)
         if key not in self._derived:
-            order, offsets = _kernels.csr_build(self.inverse[b], self.kept_tokens)
+            order, offsets = _kernels.csr_build(self._inverse32(b), self.kept_tokens)
             contribution = None if self.pool_mask is None else self.pool_mask[b].to(torch.float32)
             counts, _ = _kernels.segment_mass(offsets, 1, order, contribution, self.kept_tokens,
                                               0.0, want_log=False)
@@ -154,14 +161,15 @@ class TokenPlan:
         """Members per compact token (float32 [K]) in batch element b."""
         return self._cluster_csr(b)[1]
 
-    def restore_map_for(self, value: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor] | None:
-        """(index [N, 4] int32, weight [N, 4] float32) with which `restore(value)` projects
-        value[0], for a caller that fuses the restore into its next pass; None when restore
-        returns `value` itself or value holds more than one batch element."""
+    def restore_map_for(self, value: torch.Tensor) -> tuple[torch.Tensor, None] | None:
+        """(index [N] int32, None): the one-hot map with which `restore(value)` gathers
+        value[0] (row t = value[0, inverse[t]]), for a caller that fuses the restore into
+        its next pass; None when restore returns `value` itself or value holds more than
+        one batch element."""
         if self.kept_tokens == self.original_tokens or value.shape[0] != 1:
             return None
         _check_value(value)
-        return self._restore_map(0)
+        return self._inverse32(0), None
 
     def compact(self, value: torch.Tensor, *, merge: bool = True) -> torch.Tensor:
         if self.kept_tokens == self.original_tokens:
@@ -558,7 +566,7 @@ def build_fastvggt_plan(
         if batch != 1:
             raise ValueError("mass-bias FastVGGT plans support batch size one")
         # One mass pass gives the cluster counts _cluster_csr caches and their logs.
-        order, offsets = _kernels.csr_build(inverse[0], plan.kept_tokens)
+        order, offsets = _kernels.csr_build(plan._inverse32(0), plan.kept_tokens)
         counts, log_mass = _kernels.segment_mass(offsets, 1, order, None, plan.kept_tokens, 0.0,
                                                  want_log=True)
         plan._derived[("csr", 0)] = (_Csr(order, offsets), counts, None)

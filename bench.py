@@ -888,8 +888,9 @@ def main() -> int:
     n_tok = FRAMES * (SPECIALS + 1024)
     # The label spans the row pass that restores the merged rows in place of a
     # branch row: x read and the new stream row written in fp32, norm2's bf16 rows
-    # written, the merged table read once, 32 B of restore map per row.
-    restore_bytes = n_tok * DIM * (4 + 4 + 2) + kept * DIM * 2 + 32 * n_tok
+    # written, the merged table read once, the one-hot restore map (the plan's
+    # int32 inverse) read once: 4 B per row.
+    restore_bytes = n_tok * DIM * (4 + 4 + 2) + kept * DIM * 2 + 4 * n_tok
     result["global_restore"] = {"fused_with": "residual add + norm2 (vgo_restore_residual_layer_norm)",
                                 "ms": round(restore_ms, 4), "bytes": restore_bytes,
                                 "gbs": round(restore_bytes / (restore_ms / 1e3) / 1e9, 1),

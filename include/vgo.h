@@ -429,7 +429,10 @@ int vgo_residual_layer_norm(const float* x, int64_t x_row_stride, const void* br
  * row), then s = x + gamma * branch and LN(s) as in vgo_residual_layer_norm.
  * table: [table_rows, dim] rows of table_dtype (bf16, f16 or fp32) with
  * table_row_stride; index int32 [rows, 4] and weight fp32 [rows, 4], contiguous
- * and 16-byte aligned (the plan's restore map, vgo_restore_map).  x_out and
+ * and 16-byte aligned (the plan's restore map, vgo_restore_map).  With weight
+ * == NULL the map is one-hot: index is int32 [rows] (4-byte aligned) and
+ * branch[r,:] = table[index[r],:] as the map row (index[r] x 4, (1, 0, 0, 0))
+ * gives it, a zero row for index[r] < 0 -- a token plan's inverse.  x_out and
  * norm_out as above (at least one).  Replaces the plan restore
  * (vggt_omega/models/token_merging.py:387-414, 193-196) together with the
  * LayerScale, residual add and norm2 that follow it in forward_compacted

@@ -204,6 +204,32 @@ def test_restore_residual_layer_norm_equals_projection_then_rows(kern, device, n
         assert torch.isnan(s[3]).all() and not torch.isnan(s[5]).any()
 
 
+@pytest.mark.parametrize("table_dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_restore_residual_layer_norm_one_hot_index_equals_map(kern, device, table_dtype):
+    """weight None: index is a one-hot [rows] map (a token plan's inverse); equal bit for
+    bit to the map rows (k x 4, (1, 0, 0, 0)), with zero rows for k < 0 and NaN rows for
+    k past the table."""
+    print(f"[rows] one-hot restore {table_dtype}", flush=True)
+    n, m, dim = 333, 120, 1024
+    g = torch.Generator().manual_seed(21)
+    table = (torch.randn(m, dim, generator=g) * 2).to(table_dtype).to(device)
+    inv = torch.randint(0, m, (n,), generator=g, dtype=torch.int32)
+    inv[7], inv[8], inv[40] = -1, m, m + 1000
+    x, _, gamma, w, b = _inputs(n, dim, torch.float32, 22)
+    x, gamma, w, b = x.to(device), gamma.to(device), w.to(device), b.to(device)
+    index4 = inv.view(-1, 1).expand(n, 4).contiguous().to(device)
+    weight4 = torch.zeros(n, 4)
+    weight4[:, 0] = (inv >= 0).float()
+    weight4 = weight4.to(device)
+    for g_, aff in ((gamma, (w, b, 1e-5)), (None, (None, None, 1e-6))):
+        ref_s, ref_n = kern.restore_residual_layer_norm(x, table, index4, weight4, g_, aff)
+        s, nrm = kern.restore_residual_layer_norm(x, table, inv.to(device), None, g_, aff)
+        torch.testing.assert_close(s, ref_s, rtol=0, atol=0, equal_nan=True)
+        torch.testing.assert_close(nrm, ref_n, rtol=0, atol=0, equal_nan=True)
+    assert torch.isnan(s[8]).all() and torch.isnan(s[40]).all() and not torch.isnan(s[7]).any()
+    assert torch.equal(s[7], x[7])  # a zero branch row
+
+
 def test_restore_residual_layer_norm_rejects_bad_arguments(kern, device):
     print("[rows] restore+residual argument checks", flush=True)
     x = torch.zeros(8, 64, device=device)
@@ -216,6 +242,10 @@ def test_restore_residual_layer_norm_rejects_bad_arguments(kern, device):
         kern.restore_residual_layer_norm(x, table[:, :32], index, weight, None, (None, None, 1e-5))
     with pytest.raises(ValueError):
         kern.restore_residual_layer_norm(x, table, index.long(), weight, None, (None, None, 1e-5))
+    with pytest.raises(ValueError):  # a one-hot map is [rows]
+        kern.restore_residual_layer_norm(x, table, index, None, None, (None, None, 1e-5))
+    with pytest.raises(ValueError):
+        kern.restore_residual_layer_norm(x, table, index[:, 0].long(), None, None, (None, None, 1e-5))
 
 
 @pytest.mark.parametrize("planner", ["fastvggt", "sparse_convex"])
