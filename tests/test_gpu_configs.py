@@ -29,7 +29,7 @@ from oracle import merging as om
 from oracle import projection as oproj
 from tests._tol import assert_close
 from tests.conftest import import_package
-from tests.test_gpu_merge import score_tolerance, ulp_bf16
+from tests.test_gpu_merge import score_tolerance
 
 pytestmark = pytest.mark.gpu
 
