@@ -321,8 +321,18 @@ struct CompactOuts {
   int64_t ots[G], ohs[G];
 };
 
-// acc[g][j] = acc[g][j] / n, correctly rounded as the division (n is the
-// row's normalizer, the same in every lane).  n == 1 leaves acc as it is.
+// One output of a launch, as a wave sees it.
+template <typename TO>
+struct CompactOut {
+  int64_t x_off;
+  const float* ln_w;
+  const float* ln_b;
+  TO* out;
+  int64_t ots, ohs;
+};
+
+// acc[j] = acc[j] / n, correctly rounded as the division (n is the row's
+// normalizer, the same in every lane).  n == 1 leaves acc as it is.
 // Otherwise, when 1 <= n <= 2^16 (cluster counts and masses) and every value of
 // the wave lies in [2^-100, FLT_MAX], each takes three operations instead of a
 // division: with r = RN(1/n), q = RN(a*r) and the exact residual
@@ -331,78 +341,48 @@ struct CompactOuts {
 // These ranges keep q finite and q and e clear of the subnormals, where the
 // residual can round; anything else (zeros, subnormals, infinities, NaNs, other
 // normalizers) takes the division.
-template <int G>
-__device__ __forceinline__ void divide_by_normalizer(float (&acc)[G][16], float n) {
+__device__ __forceinline__ void divide_by_normalizer(float (&acc)[16], float n) {
   if (n == 1.0f) return;
   float lo = __builtin_inff(), hi = 0.0f;
 #pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      lo = fminf(lo, fabsf(acc[g][j]));
-      hi = __builtin_elementwise_maximum(hi, fabsf(acc[g][j]));  // a NaN propagates
-    }
+  for (int j = 0; j < 16; ++j) {
+    lo = fminf(lo, fabsf(acc[j]));
+    hi = __builtin_elementwise_maximum(hi, fabsf(acc[j]));  // a NaN propagates
+  }
   const bool in_range = lo >= 0x1p-100f && hi <= 3.40282347e+38f && n >= 1.0f && n <= 65536.0f;
   if (__ballot(!in_range) == 0) {
     const float r = 1.0f / n;
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const float a = acc[g][j];
-        const float q = a * r;
-        acc[g][j] = fmaf(fmaf(-q, n, a), r, q);
-      }
+    for (int j = 0; j < 16; ++j) {
+      const float a = acc[j];
+      const float q = a * r;
+      acc[j] = fmaf(fmaf(-q, n, a), r, q);
+    }
   } else {
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) acc[g][j] = acc[g][j] / n;
+    for (int j = 0; j < 16; ++j) acc[j] = acc[j] / n;
   }
 }
 
-template <typename TI, typename TO, int G>
-__global__ __launch_bounds__(256) void compact16_kernel(
+// Compact row k of one output: (f(x[base_rows[k]]) + sum over the row's segments
+// of the segment's sum of weights[p] * f(x[row of p])) / norm[k], f = the
+// output's per-head LayerNorm (parameters staged in LDS: ln_w / ln_b) or the
+// identity.  kFold (one segment per row, no base row): the segment's sum is the
+// row's sum, so members add into acc directly -- acc starts at +0 as a segment
+// sum does, and a sum that starts at +0 is never -0, so 0 + seg would equal seg.
+template <typename TI, typename TO, bool kFold>
+__device__ __forceinline__ void compact16_row(
     const TI* __restrict__ x, int64_t xts, int64_t xhs, int64_t x_rows,
     const int64_t* __restrict__ base_rows, const int32_t* __restrict__ offsets, int segs_per_row,
     const uint32_t* __restrict__ items, int item_shift, const int64_t* __restrict__ item_rows,
-    const float* __restrict__ weights, int n_weights, const float* __restrict__ norm, int rows,
-    int dim, float ln_eps, CompactOuts<TO, G> o) {
+    const float* __restrict__ weights, int n_weights, const float* __restrict__ norm, int k,
+    int dim, float ln_eps, const CompactOut<TO>& o, const float* ln_w, const float* ln_b) {
   const int lane = threadIdx.x & 63;
-  // Wave-uniform row: its index loads (offsets, items, row ids) go through the
-  // scalar cache and are counted apart from the member rows' vector loads.
-  const int k = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int d0 = (lane * 16) & 63;  // the same in every 1024-channel chunk
-  // Several outputs: their 64-channel LayerNorm parameters are staged in LDS
-  // once per work-group (reads from LDS do not wait on the rows in flight).
-  __shared__ float ln_lds[G > 1 ? G : 1][2][64];
-  if (G > 1) {
-    for (int e = threadIdx.x; e < G * 128; e += blockDim.x) {
-      const int g = e >> 7, h = (e >> 6) & 1, j = e & 63;
-      const float* src = h ? o.ln_b[g] : o.ln_w[g];
-      ln_lds[g][h][j] = src ? src[j] : 0.0f;
-    }
-    __syncthreads();
-  }
-  if (k >= rows) return;
   const int64_t b = base_rows ? base_rows[k] : -1;
   const float nk = norm ? norm[k] : 1.0f;
-  // One output: this lane's 16 LayerNorm parameters stay in registers across
-  // the members.
-  float lw[16], lb[16];
-  if (G == 1 && o.ln_w[0]) {
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      lw[j] = o.ln_w[0][d0 + j];
-      lb[j] = o.ln_b[0][d0 + j];
-    }
-  }
-  auto layer_norm = [&](int g, float* v) {
-    if (!o.ln_w[g]) return;
-    if (G == 1)
-      head_layer_norm(v, lw, lb, ln_eps);
-    else
-      head_layer_norm(v, &ln_lds[g][0][d0], &ln_lds[g][1][d0], ln_eps);
+  auto layer_norm = [&](float* v) {
+    if (o.ln_w) head_layer_norm(v, ln_w + d0, ln_b + d0, ln_eps);
   };
   for (int c0 = 0; c0 < dim; c0 += 1024) {
     const int c = c0 + lane * 16;
@@ -411,17 +391,13 @@ __global__ __launch_bounds__(256) void compact16_kernel(
     // below is under a wave-uniform condition only.
     const bool active = c < dim;
     const int cl = active ? c : 0;
-    const int64_t xoff = static_cast<int64_t>(cl >> 6) * xhs + (cl & 63);
-    float acc[G][16], v[G][16];
+    const int64_t xoff = static_cast<int64_t>(cl >> 6) * xhs + (cl & 63) + o.x_off;
+    float acc[16], v[16];
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) acc[g][j] = 0.0f;
+    for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
     if (b >= 0 && b < x_rows) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) v16_load(x + b * xts + o.x_off[g] + xoff, acc[g]);
-#pragma unroll
-      for (int g = 0; g < G; ++g) layer_norm(g, acc[g]);
+      v16_load(x + b * xts + xoff, acc);
+      layer_norm(acc);
     }
     // The row's members over all its segments (segment t holds items[ob[t]] ..
     // items[ob[t + 1] - 1]) as one stream, software-pipelined: while member q
@@ -461,52 +437,41 @@ __global__ __launch_bounds__(256) void compact16_kernel(
       int64_t row1 = q + 1 < q_end ? row_of(p1) : -1;
       // Two row buffers used in turn (an unrolled pair of steps), so no
       // register copy has to wait for a row still in flight.
-      V16Raw<TI> ra[G], rb[G];
+      V16Raw<TI> ra, rb;
       bool ok_a = usable(row0), ok_b = false;
       float w_a = weight_of(p0), w_b = 0.0f;
-      if (ok_a) {
+      if (ok_a) v16_load_raw(x + row0 * xts + xoff, ra);
+      float seg_own[kFold ? 1 : 16];
+      float* seg = kFold ? acc : seg_own;
+      if constexpr (!kFold) {
 #pragma unroll
-        for (int g = 0; g < G; ++g) v16_load_raw(x + row0 * xts + o.x_off[g] + xoff, ra[g]);
+        for (int j = 0; j < 16; ++j) seg[j] = 0.0f;
       }
-      float seg[G][16];
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) seg[g][j] = 0.0f;
       // One member: request member q + 1's row into `nxt` (and member q + 2's
       // row id, member q + 3's item), then pool member q from `cur`.
-      auto step = [&](V16Raw<TI> (&cur)[G], bool ok_c, float w_c, V16Raw<TI> (&nxt)[G], bool& ok_n,
-                      float& w_n) {
+      auto step = [&](V16Raw<TI>& cur, bool ok_c, float w_c, V16Raw<TI>& nxt, bool& ok_n, float& w_n) {
         ok_n = q + 1 < q_end && usable(row1);
         w_n = q + 1 < q_end ? weight_of(p1) : 0.0f;
-        if (ok_n) {
-#pragma unroll
-          for (int g = 0; g < G; ++g) v16_load_raw(x + row1 * xts + o.x_off[g] + xoff, nxt[g]);
-        }
+        if (ok_n) v16_load_raw(x + row1 * xts + xoff, nxt);
         const int64_t row2 = q + 2 < q_end ? row_of(p2) : -1;
         const uint32_t p3 = q + 3 < q_end ? items[q + 3] : 0u;
         if (ok_c) {
+          v16_widen(cur, v);
+          layer_norm(v);
+          if (weights) {
 #pragma unroll
-          for (int g = 0; g < G; ++g) {
-            v16_widen(cur[g], v[g]);
-            layer_norm(g, v[g]);
-            if (weights) {
+            for (int j = 0; j < 16; ++j) seg[j] = seg[j] + v[j] * w_c;
+          } else {  // w_c == 1
 #pragma unroll
-              for (int j = 0; j < 16; ++j) seg[g][j] = seg[g][j] + v[g][j] * w_c;
-            } else {  // w_c == 1
-#pragma unroll
-              for (int j = 0; j < 16; ++j) seg[g][j] = seg[g][j] + v[g][j];
-            }
+            for (int j = 0; j < 16; ++j) seg[j] = seg[j] + v[j];
           }
         }
-        if (q + 1 == t_end) {
+        if (!kFold && q + 1 == t_end) {
 #pragma unroll
-          for (int g = 0; g < G; ++g)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-              acc[g][j] = acc[g][j] + seg[g][j];
-              seg[g][j] = 0.0f;
-            }
+          for (int j = 0; j < 16; ++j) {
+            acc[j] = acc[j] + seg[j];
+            seg[j] = 0.0f;
+          }
           // Empty segments that follow add nothing.
           while (t + 1 < segs_per_row && t_end <= q + 1) t_end = seg_end(++t + 1);
         }
@@ -523,13 +488,66 @@ __global__ __launch_bounds__(256) void compact16_kernel(
       }
     }
     if (active) {
-      divide_by_normalizer<G>(acc, nk);
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-        v16_store(o.out[g] + static_cast<int64_t>(k) * o.ots[g] + static_cast<int64_t>(c >> 6) * o.ohs[g] + (c & 63),
-                  acc[g]);
+      divide_by_normalizer(acc, nk);
+      v16_store(o.out + static_cast<int64_t>(k) * o.ots + static_cast<int64_t>(c >> 6) * o.ohs + (c & 63), acc);
     }
   }
+}
+
+// G outputs that share one segment structure, one output per wave: wave w
+// pools output w % G of compact row w / G.  A wave holds one output's sums and
+// row buffers (89-105 VGPRs: five or four waves per SIMD to cover each row's
+// index round trips, where three outputs in one wave took 238, two per SIMD);
+// the index loads repeat per output through the scalar cache.  The outputs'
+// LayerNorm parameters are staged in LDS once per work-group.
+template <typename TI, typename TO, int G, bool kFold>
+__global__ __launch_bounds__(256) void compact16_kernel(
+    const TI* __restrict__ x, int64_t xts, int64_t xhs, int64_t x_rows,
+    const int64_t* __restrict__ base_rows, const int32_t* __restrict__ offsets, int segs_per_row,
+    const uint32_t* __restrict__ items, int item_shift, const int64_t* __restrict__ item_rows,
+    const float* __restrict__ weights, int n_weights, const float* __restrict__ norm, int rows,
+    int dim, float ln_eps, CompactOuts<TO, G> o) {
+  // Wave-uniform row: its index loads (offsets, items, row ids) go through the
+  // scalar cache and are counted apart from the member rows' vector loads.
+  const int w = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int k = w / G;
+  const int gs = w - k * G;
+  __shared__ float ln_lds[G][2][64];
+  for (int e = threadIdx.x; e < G * 128; e += blockDim.x) {
+    const int g = e >> 7, h = (e >> 6) & 1, j = e & 63;
+    const float* src = h ? o.ln_b[g] : o.ln_w[g];
+    ln_lds[g][h][j] = src ? src[j] : 0.0f;
+  }
+  __syncthreads();
+  if (k >= rows) return;
+  // Output gs's fields, selected with compile-time indices (indexing the
+  // kernel-argument arrays at run time would copy them to scratch).
+  CompactOut<TO> o1{o.x_off[0], o.ln_w[0], o.ln_b[0], o.out[0], o.ots[0], o.ohs[0]};
+#pragma unroll
+  for (int g = 1; g < G; ++g)
+    if (gs == g) o1 = CompactOut<TO>{o.x_off[g], o.ln_w[g], o.ln_b[g], o.out[g], o.ots[g], o.ohs[g]};
+  compact16_row<TI, TO, kFold>(x, xts, xhs, x_rows, base_rows, offsets, segs_per_row, items, item_shift,
+                               item_rows, weights, n_weights, norm, k, dim, ln_eps, o1, ln_lds[gs][0],
+                               ln_lds[gs][1]);
+}
+
+// Launch of compact16_kernel for `rows` compact rows of G outputs.
+template <typename TI, typename TO, int G>
+int launch_compact16(const TI* x, int64_t xts, int64_t xhs, int64_t x_rows, const int64_t* base_rows,
+                     const int32_t* offsets, int sp, const uint32_t* items, int item_shift,
+                     const int64_t* item_rows, const float* weights, int nw, const float* normalizer,
+                     int rows, int dim, float ln_eps, const CompactOuts<TO, G>& o, hipStream_t s,
+                     const char* what) {
+  const dim3 grid(static_cast<unsigned>((static_cast<int64_t>(rows) * G + 3) / 4));
+  if (sp == 1 && !base_rows)
+    hipLaunchKernelGGL((compact16_kernel<TI, TO, G, true>), grid, dim3(256), 0, s, x, xts, xhs, x_rows,
+                       base_rows, offsets, sp, items, item_shift, item_rows, weights, nw, normalizer, rows,
+                       dim, ln_eps, o);
+  else
+    hipLaunchKernelGGL((compact16_kernel<TI, TO, G, false>), grid, dim3(256), 0, s, x, xts, xhs, x_rows,
+                       base_rows, offsets, sp, items, item_shift, item_rows, weights, nw, normalizer, rows,
+                       dim, ln_eps, o);
+  return check_launch(what);
 }
 
 // ---------------------------------------------------- restore map ----
@@ -677,11 +695,10 @@ extern "C" int vgo_compact(const void* x, int64_t x_token_stride, int64_t x_head
   {                                                                                                \
     const CompactOuts<TO, 1> o{{0}, {ln_weight}, {ln_bias}, {static_cast<TO*>(out)},               \
                                {out_token_stride}, {out_head_stride}};                            \
-    hipLaunchKernelGGL((compact16_kernel<TI, TO, 1>), grid, dim3(256), 0, s,                        \
-                       static_cast<const TI*>(x), x_token_stride, x_head_stride, x_rows, base_rows, \
-                       offsets, sp, items, item_shift, item_rows, weights, nw, normalizer, r, d,    \
-                       ln_eps, o);                                                                 \
-    return check_launch("compact");                                                                \
+    return launch_compact16<TI, TO, 1>(static_cast<const TI*>(x), x_token_stride, x_head_stride,   \
+                                       x_rows, base_rows, offsets, sp, items, item_shift,          \
+                                       item_rows, weights, nw, normalizer, r, d, ln_eps, o, s,     \
+                                       "compact");                                                 \
   }
     if (in_dtype == VGO_F32 && out_dtype == VGO_F32) { VGO_C16(float, float); }
     if (in_dtype == VGO_BF16 && out_dtype == VGO_BF16) { VGO_C16(bf16_t, bf16_t); }
@@ -755,10 +772,9 @@ int launch_compact_multi(const void* x, int64_t xts, int64_t xhs, int64_t x_rows
     o.ots[g] = ots[g];
     o.ohs[g] = ohs[g];
   }
-  hipLaunchKernelGGL((compact16_kernel<TI, TO, G>), dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0,
-                     s, static_cast<const TI*>(x), xts, xhs, x_rows, base_rows, offsets, sp, items, item_shift,
-                     item_rows, weights, nw, normalizer, rows, dim, ln_eps, o);
-  return check_launch("compact_multi");
+  return launch_compact16<TI, TO, G>(static_cast<const TI*>(x), xts, xhs, x_rows, base_rows, offsets, sp,
+                                     items, item_shift, item_rows, weights, nw, normalizer, rows, dim, ln_eps,
+                                     o, s, "compact_multi");
 }
 
 template <typename T>
