@@ -419,6 +419,29 @@ def test_weighted_plan_compact_edge_normalizers(vgo, device, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_compaction_of_rows_wider_than_1024_channels(vgo, device, dtype):
+    """Rows of 1,536 and 2,048 channels (two 1,024-channel passes per wave): a weighted
+    plan (four segments per row) and a token plan (one segment, no base row) against
+    the oracle, bit for bit."""
+    print(f"[compact] wide rows {dtype}", flush=True)
+    keep, src, parent, w = _random_weighted_plan(15, 1500, 500, 900)
+    mass = om.deterministic_weighted_normalizer(parent[None], w[None], 500)
+    plan = vgo.WeightedBilinearTokenPlan(
+        keep=keep[None].to(device), source_original=src[None].to(device),
+        source_parent_compact=parent[None].to(device), source_pool_weights=w[None].to(device),
+        source_restore_weights=w[None].to(device), original_tokens=1500, normalizer=mass.to(device))
+    value = seeded_values(16, (1, 1500, 2048), dtype)
+    out = plan.compact(value.to(device))
+    assert torch.equal(out[0].cpu(), om.weighted_compact(keep, src, parent, w, mass, value[0]))
+    tokens = structured_tokens(17, 4, (16, 16), 5, 256).to(device)
+    tplan = vgo.build_fastvggt_plan(tokens, merge_ratio=0.5, protect_ratio=0.0, **KW)
+    value = seeded_values(18, (1, tokens.shape[1], 1536), dtype)
+    out = tplan.compact(value.to(device))
+    ref = om.token_plan_compact(tplan.inverse[0].cpu(), tplan.kept_tokens, value[0])
+    assert torch.equal(out[0].cpu(), ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_token_plan_compact_restore_bit_exact(vgo, device, fx, dtype):
     inv = torch.from_numpy(fx["fv50_inverse"])
     keep = torch.from_numpy(fx["fv50_keep"])
