@@ -880,8 +880,10 @@ __global__ __launch_bounds__(kPPWaves * 64, 1) void attn_pp_kernel(PPLaunch<T> L
 // Block b handles tail task b / kMergeSplit (problem 0's tail tasks, then
 // problem 1's tasks), queries (b % kMergeSplit) * kPPQBlock / kMergeSplit
 // onwards; 16 threads per query, 4 dims each.  Partial states are read eight
-// at a time so their loads overlap.
-constexpr int kMergeSplit = 8;
+// at a time so their loads overlap.  32 blocks per task (16 queries each):
+// with 16 tail tasks at C4 that is 512 work-groups, two per CU (8 per task
+// left half the CUs idle: 6 us more per launch).
+constexpr int kMergeSplit = 32;
 template <typename T>
 __global__ __launch_bounds__(256) void attn_merge_kernel(PPLaunch<T> L) {
   const PPSchedule& sc = L.s;
