@@ -418,13 +418,16 @@ __global__ __launch_bounds__(kThreads) void sparse_convex_assemble_kernel(
 //            prefix from the previous histogram; work-group 0 records it)
 //   mark     threshold; keys above it are removed; ties counted per group
 //   ties     the first need_ties ties in source order are removed
-//   kcount   kept tokens per 2048-token group
+//   kcount   kept tokens per 512-token group
 //   compact  compact ids (ascending) and the keep list
 //   inverse  removed sources take their target's compact id
 // Every step is integer work; the result is bit-identical to the one-group
 // kernel.
 constexpr int kAThreads = 256;
-constexpr int kAPer = 8;                     // elements per thread, contiguous
+// Two elements per thread: 512-element groups spread each step over 4x the
+// work-groups of 2048-element ones (47 / 65 at C4 instead of 12 / 17), which took
+// the C4 plan build from 500 to 480 us.
+constexpr int kAPer = 2;                     // elements per thread, contiguous
 constexpr int kAChunk = kAThreads * kAPer;  // elements per work-group
 constexpr int kASel = 4 * 256;               // sel[5][4] follows hist[4][256]
 constexpr int kAGroupsAt = kASel + 20;       // per-group counts follow
