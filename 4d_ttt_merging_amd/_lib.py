@@ -68,6 +68,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "vgo_mass_bias_attn_pair_fwd_ws": (_c_int, [
         ctypes.POINTER(AttnProblem), _c_int, _c_int, _c_p, _c_size, _c_p,
     ]),
+    "vgo_attn_kernel_timing": (_c_int, [_c_int]),
+    "vgo_attn_kernel_timing_read": (_c_int, [
+        ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64),
+    ]),
     "vgo_top4_project": (_c_int, [
         _c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_p,
     ]),

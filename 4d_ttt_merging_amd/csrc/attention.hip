@@ -1210,6 +1210,49 @@ int launch_reg(const Problem& pr, hipStream_t stream) {
   return check_launch("mass_bias_attention");
 }
 
+// Kernel timing (vgo_attn_kernel_timing): while it is on, every attn_pp_kernel
+// launch made outside stream capture on the device it was switched on for is
+// bracketed by a pair of HIP events from a fixed pool, so the kernel's own
+// duration can be read without the V^T pack and the merge around it.
+constexpr int kTimingSlots = 4096;
+struct KernelTiming {
+  std::mutex mutex;
+  bool on = false;
+  int device = -1;
+  int used = 0;
+  int64_t dropped = 0;
+  hipEvent_t start[kTimingSlots] = {};
+  hipEvent_t stop[kTimingSlots] = {};
+};
+KernelTiming& kernel_timing() {
+  static KernelTiming t;
+  return t;
+}
+
+// The event pair for the next launch on `stream`, or false when timing is off,
+// the stream is being captured or belongs to another device, or the pool is full.
+bool timing_slot(hipStream_t stream, hipEvent_t* start, hipEvent_t* stop) {
+  KernelTiming& t = kernel_timing();
+  std::lock_guard<std::mutex> lock(t.mutex);
+  if (!t.on) return false;
+  int dev = -1;
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  if (hipGetDevice(&dev) != hipSuccess || dev != t.device ||
+      hipStreamIsCapturing(stream, &capture) != hipSuccess || capture != hipStreamCaptureStatusNone)
+    return false;
+  if (t.used == kTimingSlots) {
+    ++t.dropped;
+    return false;
+  }
+  const int i = t.used;
+  if (t.start[i] == nullptr && hipEventCreate(&t.start[i]) != hipSuccess) return false;
+  if (t.stop[i] == nullptr && hipEventCreate(&t.stop[i]) != hipSuccess) return false;
+  ++t.used;
+  *start = t.start[i];
+  *stop = t.stop[i];
+  return true;
+}
+
 // Workspace path over one or two problems: pack V^T and the bias of each,
 // then the ping-pong LDS-DMA kernel, then the merge of split tasks.
 template <typename T>
@@ -1245,9 +1288,13 @@ int launch_pp(const Problem* pr, int count, void* workspace, size_t workspace_by
   if (count == 1) L.p[1] = L.p[0];  // never selected: problem 1 has no units
   L.s = plan.s;
   if (plan.s.units > 0) L.s.partial = reinterpret_cast<float*>(base + ws.partial);
+  hipEvent_t t_start = nullptr, t_stop = nullptr;
+  const bool timed = timing_slot(stream, &t_start, &t_stop);
+  if (timed) (void)hipEventRecord(t_start, stream);
   hipLaunchKernelGGL((attn_pp_kernel<T>), dim3(static_cast<unsigned>(plan.s.groups)),
                      dim3(kPPWaves * 64), 0, stream, L);
   int status = check_launch("mass_bias_attention");
+  if (timed) (void)hipEventRecord(t_stop, stream);
   if (status != VGO_OK || plan.s.units == 0) return status;
   const int64_t tail_tasks = plan.s.tail_tasks0 + (count > 1 ? plan.tasks[1] : 0);
   hipLaunchKernelGGL((attn_merge_kernel<T>), dim3(static_cast<unsigned>(tail_tasks * kMergeSplit)),
@@ -1483,4 +1530,49 @@ extern "C" int vgo_mass_bias_attn_pair_fwd_ws(const vgo_attn_problem* problems, 
     head_dims[i] = problems[i].head_dim;
   }
   return attn_run(p, head_dims, count, dtype, workspace, workspace_bytes, true, stream);
+}
+
+extern "C" int vgo_attn_kernel_timing(int enable) {
+  using namespace vgo;
+  KernelTiming& t = kernel_timing();
+  std::lock_guard<std::mutex> lock(t.mutex);
+  if (!enable) {
+    t.on = false;
+    return VGO_OK;
+  }
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0)
+    return fail(VGO_ELAUNCH, "vgo_attn_kernel_timing: no current device");
+  if (t.device >= 0 && t.device != dev && t.used > 0)
+    return fail(VGO_EINVAL, "vgo_attn_kernel_timing: read the launches recorded on device " +
+                                std::to_string(t.device) + " first");
+  if (t.device != dev) {
+    // Events belong to the device they were created on: a new device starts a new pool.
+    for (int i = 0; i < kTimingSlots; ++i) t.start[i] = t.stop[i] = nullptr;
+  }
+  t.device = dev;
+  t.on = true;
+  return VGO_OK;
+}
+
+extern "C" int vgo_attn_kernel_timing_read(double* total_ms, int64_t* launches, int64_t* dropped) {
+  using namespace vgo;
+  VGO_REQUIRE(total_ms && launches, "vgo_attn_kernel_timing_read: null output");
+  KernelTiming& t = kernel_timing();
+  std::lock_guard<std::mutex> lock(t.mutex);
+  double sum = 0.0;
+  for (int i = 0; i < t.used; ++i) {
+    hipError_t err = hipEventSynchronize(t.stop[i]);
+    float ms = 0.0f;
+    if (err == hipSuccess) err = hipEventElapsedTime(&ms, t.start[i], t.stop[i]);
+    if (err != hipSuccess)
+      return fail(VGO_ELAUNCH, std::string("vgo_attn_kernel_timing_read: ") + hipGetErrorString(err));
+    sum += ms;
+  }
+  *total_ms = sum;
+  *launches = t.used;
+  if (dropped) *dropped = t.dropped;
+  t.used = 0;
+  t.dropped = 0;
+  return VGO_OK;
 }

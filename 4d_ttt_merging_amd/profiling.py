@@ -74,3 +74,32 @@ def summary() -> dict[str, tuple[float, int]]:
         entry[0] += begin.elapsed_time(end)
         entry[1] += 1
     return {label: (total, int(calls)) for label, (total, calls) in totals.items()}
+
+
+def attention_kernel_timing(flag: bool = True) -> None:
+    """Switch the library's kernel timing on or off: while on, every launch of the
+    workspace attention kernel on the current device is bracketed by its own HIP
+    event pair (the V^T pack and the split-task merge of the same call are not)."""
+    from . import _lib
+
+    lib = _lib.load()
+    _lib.check(lib.vgo_attn_kernel_timing(1 if flag else 0))
+
+
+def attention_kernel_summary() -> tuple[float, int]:
+    """(total ms, launches) of the attention kernel launches timed since the last
+    call; waits for them, then empties the record."""
+    import ctypes
+
+    from . import _lib
+
+    lib = _lib.load()
+    total = ctypes.c_double(0.0)
+    launches = ctypes.c_int64(0)
+    dropped = ctypes.c_int64(0)
+    _lib.check(lib.vgo_attn_kernel_timing_read(ctypes.byref(total), ctypes.byref(launches),
+                                               ctypes.byref(dropped)))
+    if dropped.value:
+        raise RuntimeError(f"attention kernel timing: {dropped.value} launches were not recorded "
+                           "(more than the library's 4096 event pairs)")
+    return total.value, int(launches.value)

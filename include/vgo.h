@@ -141,6 +141,24 @@ int vgo_mass_bias_attn_pair_fwd_ws(const vgo_attn_problem* problems, int count, 
                                    void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Kernel timing of the workspace attention path.  No counterpart in the
+ * reference, whose profiling timers (vggt_omega/models/layers/attention.py:25-63)
+ * bracket labelled spans of a layer, not single kernels; it serves callers that
+ * measure the attention kernel against its roofline.
+ *
+ * vgo_attn_kernel_timing(1) records a HIP event pair around every
+ * attn_pp_kernel launch that vgo_mass_bias_attn_fwd_ws / _fwd_static /
+ * _pair_fwd_ws make afterwards on the device current at the call, outside
+ * stream capture, up to 4096 launches (later ones are counted in `dropped`);
+ * vgo_attn_kernel_timing(0) stops recording.  vgo_attn_kernel_timing_read
+ * waits for the recorded launches, returns their summed duration in
+ * milliseconds and their count, and empties the record.  The V^T pack and
+ * the merge of split tasks that the same calls launch are not included.
+ */
+int vgo_attn_kernel_timing(int enable);
+int vgo_attn_kernel_timing_read(double* total_ms, int64_t* launches, int64_t* dropped);
+
+/*
  * Top-4 convex projection (unmerge): out[i,:] = sum_c w[i,c] * table[index[i,c],:].
  *
  * Replaces the restore of WeightedBilinearTokenPlan / TokenPlan

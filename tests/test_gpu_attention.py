@@ -226,3 +226,25 @@ def test_pair_launch_empty_problems_and_errors(vgo, device):
         mba._lib.check(lib.vgo_mass_bias_attn_pair_fwd_ws(problems, 2, 1, None, 0, None))
     with pytest.raises(ValueError, match="1 or 2 problems"):
         mba._lib.check(mba._lib.load().vgo_mass_bias_attn_pair_fwd_ws(problems, 3, 1, None, 0, None))
+
+
+def test_kernel_timing_records_each_workspace_launch(vgo, device):
+    """vgo_attn_kernel_timing brackets each attention-kernel launch with an event
+    pair while it is on, records nothing while it is off, and leaves results alone."""
+    prof = __import__("4d_ttt_merging_amd.profiling", fromlist=["profiling"])
+    print("[attn] kernel timing, 1x2x600x3000 bf16", flush=True)
+    q, k, v, mass = _inputs(11, 1, 2, 600, 3000, torch.bfloat16)
+    q, k, v, bias = q.to(device), k.to(device), v.to(device), mass.log().to(device)
+    untimed = vgo.mass_bias_attention(q, k, v, bias)
+    prof.attention_kernel_summary()
+    prof.attention_kernel_timing(True)
+    try:
+        timed = [vgo.mass_bias_attention(q, k, v, bias) for _ in range(3)]
+    finally:
+        prof.attention_kernel_timing(False)
+    total_ms, launches = prof.attention_kernel_summary()
+    assert launches == 3 and total_ms > 0.0
+    for out in timed:
+        assert torch.equal(out, untimed)
+    vgo.mass_bias_attention(q, k, v, bias)
+    assert prof.attention_kernel_summary() == (0.0, 0)
