@@ -435,16 +435,25 @@ struct WaveAttn {
     for (int t = 0; t < 4; ++t) ka[t] = tile_op(kl, 0, t);
     const op4 ba = bias_a(bl, 0);
     __builtin_amdgcn_sched_barrier(0);
+    // The second half's K reads go out between the last two P.V k-steps and
+    // ahead of every score MFMA (left to itself the scheduler sinks them
+    // below the first score MFMAs to reuse ka's registers, four MFMAs before
+    // their use); issuing ka earlier than this, under the V^T reads still in
+    // flight, is slower.
 #pragma unroll
-    for (int t = 2; t < 4; ++t)
+    for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-      for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-        for (int qb = 0; qb < kQB; ++qb) o[qb][dt] = Mma<T>::mma(vops.v[t][dt], p[qb][t], o[qb][dt]);
+      for (int qb = 0; qb < kQB; ++qb) o[qb][dt] = Mma<T>::mma(vops.v[2][dt], p[qb][2], o[qb][dt]);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 0; t < 4; ++t) kb[t] = tile_op(kl, 1, t);
     const op4 bb = bias_a(bl, 1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int qb = 0; qb < kQB; ++qb) o[qb][dt] = Mma<T>::mma(vops.v[3][dt], p[qb][3], o[qb][dt]);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int qb = 0; qb < kQB; ++qb) {
       s[qb][0] = f32x16{};
