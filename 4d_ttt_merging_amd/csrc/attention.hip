@@ -18,17 +18,23 @@
 //    and 16 keys of every 32-key sub-tile: the row max/sum of the online
 //    softmax stay in registers except for one v_permlane32_swap, and the
 //    exponentiated scores are already laid out as the B operand of O^T = V^T P^T.
-//  * Q is scaled by log2(e)/8 as it is loaded (rounded to the input dtype), so
-//    the MFMA yields logits in the exp2 domain.  The per-key bias and the
-//    softmax offset ride in the MFMA too: a fifth k-step multiplies the
-//    key-side column pair (hi, lo) = log2(e)*log m split into two input-dtype
-//    values (exact to ~2^-17) and a column of ones with the query-side
-//    (1, 1, -mref).  It has three terms, so it runs as one 8-deep
-//    v_mfma_f32_32x32x8, which takes the matrix pipe for less time than a
-//    16-deep one (same accumulator layout, same sums).  The reference rounds
-//    log(m) to the input dtype first (mass_bias_attention.py:109); so do we.
-//  * Lazy online softmax: P = 2^S straight from the accumulator while no
-//    logit exceeds the reference max mref by more than 8 (checked through the
+//  * Q is scaled by 1/8 = 1/sqrt(64) as it is loaded, which is exact in the
+//    input dtype, so the MFMA yields the reference's logits q.k/8 from the
+//    inputs as given; log2(e) multiplies them in fp32 before v_exp_f32, as
+//    the reference multiplies its fp32 dot products (mass_bias_attention.py:
+//    56-58).  (Rounding Q*log2(e)/8 to the input dtype instead saves that
+//    multiply but adds a logit error of up to 2^-9 of each product, which
+//    grows with the logit scale: 7e-2 of the output at q, k of 3x unit scale
+//    in bf16.)  Sub-tile 0's multiplies run under sub-tile 1's MFMAs.  The
+//    per-key bias and the softmax offset ride in the MFMA: a fifth k-step
+//    multiplies the key-side column pair (hi, lo) = (log m, 0) with log m in
+//    the input dtype, and a column of ones, with the query-side (1, 1, -mref).
+//    It has three terms, so it runs as one 8-deep v_mfma_f32_32x32x8, which
+//    takes the matrix pipe for less time than a 16-deep one (same accumulator
+//    layout, same sums).  The reference rounds log(m) to the input dtype
+//    first (mass_bias_attention.py:109); so do we.
+//  * Lazy online softmax: P = e^S straight from the accumulator while no
+//    logit exceeds the reference max mref by more than 15 ln 2 (checked through the
 //    per-lane sums); only then, and on a segment's first tile, are the tile's
 //    logits recomputed, mref moved and O / the row sum rescaled.  P is rounded
 //    to the input dtype before P.V (reference :74); the row sum adds the
@@ -128,10 +134,10 @@ struct AttnArgs {
   T* out;
   int heads, nq, nk, n_qblocks, ntiles;
   int64_t qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn, osb, osh, osn;
-  float c;  // log2(e) / 8, folded into Q
+  float c;  // 1/8, folded into Q (exact)
   // LDS-DMA kernel only: V^T packed per (batch*head) as [64][npad] in the MFMA
-  // key order, and per key the pair (hi, lo) = log2(e)*bias split into two T
-  // values ((-inf, 0) past n_key), 2*npad long.
+  // key order, and per key the pair (hi, lo) = (bias, 0) ((-inf, 0) past
+  // n_key), 2*npad long.
   const T* vt;
   const T* bias2;
   int npad;
@@ -178,8 +184,14 @@ __device__ __forceinline__ void zero_bias_tails(T* b_lds, int stages) {
     reinterpret_cast<uint32_t*>(b_lds + (i / (kBN / 2)) * kBiasSlot + kBiasPairs)[i % (kBN / 2)] = 0u;
 }
 // Largest per-lane sum of 32 probabilities the lazy softmax accepts without
-// moving its reference max (bounds every P by 2^8).
-constexpr float kLazyLimit = 256.0f;
+// moving its reference max.  It bounds every P by 2^15, below the largest
+// finite f16 (65,504), so the rounded P operands of either type stay finite;
+// the bound exists only for that.  P's relative rounding error is the same at
+// any magnitude, and a higher bound takes the rescaling path less often when
+// logits spread widely (q, k at 2-3x unit scale: 16-19% faster at C4 than a
+// bound of 2^8; at unit scale and below the path is never taken and the
+// results are the same bit for bit).
+constexpr float kLazyLimit = 32768.0f;
 
 // Per-wave state of the bf16/f16 kernels: 64 queries as two 32-column MFMA
 // blocks -- their scaled Q operands, the online-softmax state and the O^T
@@ -190,7 +202,7 @@ struct WaveAttn {
   typedef typename Mma<T>::op2 op2;
   typedef typename Mma<T>::op4 op4;
 
-  op8 qreg[kQB][4];  // Q' = Q * log2(e)/8, B operands
+  op8 qreg[kQB][4];  // Q' = Q / 8 (exact), B operands
   uint32_t qneg[kQB];  // -mref as a T bit pattern (lanes 0-31; 0 elsewhere)
   // Reference max per query (a T value; -inf until a finite logit is seen);
   // the running sum and O are relative to 2^mref.
@@ -201,8 +213,8 @@ struct WaveAttn {
   uint32_t low_lanes, one_bits;
   int l32, hh;
 
-  // Q' = Q * c rounded to T for the wave's rows qw0.. (rows past n_query read
-  // a valid row; never stored): K Q'^T is then in the exp2 domain.
+  // Q' = Q * c for the wave's rows qw0.. (rows past n_query read a valid row;
+  // never stored); c = 1/8 keeps Q' exact, so K Q'^T holds the logits.
   __device__ __forceinline__ void init(const T* qb_ptr, int64_t qsn, int qw0, int nq, float c) {
     const int lane = threadIdx.x & 63;
     l32 = lane & 31;
@@ -236,8 +248,8 @@ struct WaveAttn {
   }
 
   // The bias k-step (8 deep).  A (keys; lanes 0-31 hold k-slots 0-3 of key
-  // l32, lanes 32-63 slots 4-7): {bias_hi, bias_lo, 1, 0}, the key's
-  // log2(e)*bias split into two T values, and zeros.  B (queries):
+  // l32, lanes 32-63 slots 4-7): {bias_hi, bias_lo, 1, 0}, the key's bias
+  // as a pair of T values (the second 0 for a T bias), and zeros.  B (queries):
   // {1, 1, -offset, 0}, and zeros.
   __device__ __forceinline__ uint32_t neg_bits(float offset) const {
     return __builtin_bit_cast(uint16_t, static_cast<T>(-offset)) & low_lanes;
@@ -281,7 +293,8 @@ struct WaveAttn {
       for (int dt = 0; dt < 2; ++dt) ops.v[t][dt] = tile_op(vl, dt, t);
   }
 
-  // S^T = K Q'^T + log2(e) bias - mref for the tile's two 32-key sub-tiles.
+  // S^T = K Q'^T + bias - mref for the tile's two 32-key sub-tiles, times
+  // log2(e) (the exp2 domain the softmax takes them in).
   __device__ __forceinline__ void scores(const KOps& ops, f32x16 (&s)[kQB][2]) const {
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
@@ -294,6 +307,11 @@ struct WaveAttn {
 #pragma unroll
       for (int qb = 0; qb < kQB; ++qb) s[qb][sub] = Mma<T>::mma8(ops.b[sub], offset_b(qneg[qb]), s[qb][sub]);
     }
+    // Sub-tile 0 leaves in the exp2 domain, as pv_scores leaves it.
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[qb][0][r] *= kLog2e;
   }
   __device__ __forceinline__ void scores(const T* kl, const T* bl, f32x16 (&s)[kQB][2]) const {
     KOps ops;
@@ -302,11 +320,13 @@ struct WaveAttn {
     scores(ops, s);
   }
 
-  // P = exp2(x - shift) for one 32-key sub-tile (x), rounded to T and packed
+  // P = e^(x - shift) = exp2((x - shift) * log2(e)) for one 32-key sub-tile
+  // (x; kScaled: x is already (x - 0) * log2(e)), rounded to T and packed
   // into B operands p[2*sub], p[2*sub+1] of O^T += V^T P^T.  The unrounded
   // values are summed into part[4] (started by sub 0), as the reference sums
   // its fp32 probabilities; the sum uses fp32 adds because dot instructions
   // would share the matrix pipe with the other wave's MFMAs.
+  template <bool kScaled = false>
   __device__ __forceinline__ void exp_pack(const f32x16& x, int sub, float shift, op8 (&p)[4],
                                            float (&part)[4]) const {
 #pragma unroll
@@ -315,8 +335,8 @@ struct WaveAttn {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int r = u * 8 + 2 * j;
-        const float e0 = __builtin_amdgcn_exp2f(x[r] - shift);
-        const float e1 = __builtin_amdgcn_exp2f(x[r + 1] - shift);
+        const float e0 = __builtin_amdgcn_exp2f(kScaled ? x[r] : (x[r] - shift) * kLog2e);
+        const float e1 = __builtin_amdgcn_exp2f(kScaled ? x[r + 1] : (x[r + 1] - shift) * kLog2e);
         part[j] = sub == 0 && u == 0 ? e0 : part[j] + e0;
         part[j] += e1;
         const op2 pr = {static_cast<T>(e0), static_cast<T>(e1)};
@@ -337,9 +357,9 @@ struct WaveAttn {
     return Mma<T>::mma8(bias_a(bl, sub), offset_b(0u), x);
   }
 
-  // Lazy online softmax of one tile's scores.  P = 2^S directly while every
+  // Lazy online softmax of one tile's scores.  P = e^S directly while every
   // lane's sum of its 32 probabilities stays <= kLazyLimit (so no logit
-  // exceeds mref by more than 8): the reference max then need not move.
+  // exceeds mref by more than 15 ln 2): the reference max then need not move.
   // Otherwise (and on a segment's first tile, when mref = -inf makes S
   // non-finite) the tile's logits are recomputed without the offset from K
   // (at kl, bias at bl), mref moves to the T value nearest the running max,
@@ -352,7 +372,7 @@ struct WaveAttn {
 #pragma unroll
     for (int qb = 0; qb < kQB; ++qb) {
       float acc[4];
-      exp_pack(s[qb][0], 0, 0.0f, p[qb], acc);
+      exp_pack<true>(s[qb][0], 0, 0.0f, p[qb], acc);
       exp_pack(s[qb][1], 1, 0.0f, p[qb], acc);
       part[qb] = sum4(acc);
     }
@@ -371,7 +391,7 @@ struct WaveAttn {
         // Rounding is monotone and mref is a T value, so mnew >= mref.
         const float mnew = to_f32(static_cast<T>(fmaxf(mref[qb], half_max(mx))));
         if (__ballot(mnew != mref[qb])) {
-          const float corr = mnew == -__builtin_inff() ? 1.0f : __builtin_amdgcn_exp2f(mref[qb] - mnew);
+          const float corr = mnew == -__builtin_inff() ? 1.0f : __builtin_amdgcn_exp2f((mref[qb] - mnew) * kLog2e);
           lsum[qb] *= corr;
 #pragma unroll
           for (int dt = 0; dt < 2; ++dt)
@@ -468,6 +488,16 @@ struct WaveAttn {
 #pragma unroll
       for (int t = 0; t < 4; ++t) s[qb][1] = Mma<T>::mma(kb[t], qreg[qb][t], s[qb][1]);
       s[qb][1] = Mma<T>::mma8(bb, offset_b(qneg[qb]), s[qb][1]);
+    }
+    // Sub-tile 0's scores into the exp2 domain under sub-tile 1's MFMAs.
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[qb][0][r] *= kLog2e;
+#pragma unroll
+    for (int i = 0; i < 10; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four VALU
     }
   }
 
@@ -582,7 +612,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attn_reg_kernel(AttnArgs<T> a)
       *reinterpret_cast<op2*>(vl + vbase + i * kD + ((vphys ^ i) << 3)) = pr;
     }
     const bool valid = tile * kBN + lane < a.nk;
-    const float bv = valid ? (a.bias ? kLog2e * to_f32(pb) : 0.0f) : -__builtin_inff();
+    const float bv = valid ? (a.bias ? to_f32(pb) : 0.0f) : -__builtin_inff();
     const T hi = static_cast<T>(bv);
     const T lo = static_cast<T>(__builtin_isfinite(bv) ? bv - to_f32(hi) : 0.0f);
     const op2 pair = {hi, lo};
@@ -946,7 +976,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(PPLaunch<T> L) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         if (wb + e <= w1) {
-          const float f = __builtin_amdgcn_exp2f(mv[e] - mmax);
+          const float f = __builtin_amdgcn_exp2f((mv[e] - mmax) * kLog2e);
 #pragma unroll
           for (int q = 0; q < 4; ++q) acc[q] = fmaf(xv[e][q], f, acc[q]);
           l = fmaf(lv[e], f, l);
@@ -1037,7 +1067,7 @@ __global__ __launch_bounds__(64) void attn_f32_kernel(
 // Packs V of every (batch, head) into V^T tiles for the DMA kernel:
 // vt[bh][d][j'] = V[bh][key j][d] with j' = vt_pos(j) inside each 16-key group
 // (the key order of the P operand), zeros past n_key, npad = ntiles * 64
-// columns; and bias2[2j], bias2[2j+1] = hi, lo of log2(e) * bias[j] (0, 0
+// columns; and bias2[2j], bias2[2j+1] = hi, lo of bias[j] (0, 0
 // without a bias) for j < n_key, (-inf, 0) up to npad.  One block per
 // (64-key tile, bh).
 template <typename T>
@@ -1080,7 +1110,7 @@ __global__ __launch_bounds__(256) void vt_pack_kernel(const T* __restrict__ v, i
   }
   if (bh == 0 && tid < kBN) {
     const int j = kt + tid;
-    const float bv = j < nk ? (bias ? kLog2e * to_f32(bias[j]) : 0.0f) : -__builtin_inff();
+    const float bv = j < nk ? (bias ? to_f32(bias[j]) : 0.0f) : -__builtin_inff();
     const T hi = static_cast<T>(bv);
     bias2[2 * j] = hi;
     bias2[2 * j + 1] = static_cast<T>(__builtin_isfinite(bv) ? bv - to_f32(hi) : 0.0f);
@@ -1199,7 +1229,7 @@ AttnArgs<T> make_args(const Problem& pr, int64_t qblock) {
   a.ksb = pr.ks[0], a.ksh = pr.ks[1], a.ksn = pr.ks[2];
   a.vsb = pr.vs[0], a.vsh = pr.vs[1], a.vsn = pr.vs[2];
   a.osb = pr.os[0], a.osh = pr.os[1], a.osn = pr.os[2];
-  a.c = kLog2e / 8.0f;
+  a.c = 0.125f;
   a.vt = nullptr;
   a.bias2 = nullptr;
   a.npad = a.ntiles * kBN;
