@@ -69,8 +69,12 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
         objects = list(pool.map(_compile, sources))
     tmp = LIBRARY.with_suffix(".so.tmp")
+    # Only the C ABI leaves the library: every other symbol (the C++ helpers,
+    # the compiler's per-unit ids) is bound locally by this version script.
+    version_script = BUILD_DIR / "exports.map"
+    version_script.write_text("{\n  global: vgo_*;\n  local: *;\n};\n")
     cmd = [hipcc(), f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC",
-           *map(str, objects), "-o", str(tmp)]
+           f"-Wl,--version-script={version_script}", *map(str, objects), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc link failed:\n{proc.stderr}")

@@ -1460,37 +1460,6 @@ Problem from_c(const vgo_attn_problem& p) {
                  p.q_stride, p.k_stride, p.v_stride, p.o_stride};
 }
 
-// Scratch of vgo_mass_bias_attn_fwd_static: every GPU the library runs on holds
-// one copy until the process ends.  VGO_ATTN_STATIC_SCRATCH_BYTES covers the
-// workspace of every BASELINE configuration on a 256-CU MI355X (C5: 108.5 MB of
-// V^T + 69 MB of partial states).  Host code never passes the array's name to a
-// kernel (on the host it is a stand-in, not a device address); it uses the
-// per-device address from hipGetSymbolAddress below.
-__device__ __align__(256) unsigned char scratch[VGO_ATTN_STATIC_SCRATCH_BYTES];
-
-constexpr int kMaxDevices = 64;
-std::mutex g_scratch_mutex;
-void* g_scratch_ptr[kMaxDevices] = {};
-
-// Device address of the current device's scratch, looked up once per device.
-int static_scratch(void** out) {
-  using namespace vgo;
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
-    return fail(VGO_ELAUNCH, "mass_bias_attention(static): no current device");
-  std::lock_guard<std::mutex> lock(g_scratch_mutex);
-  if (g_scratch_ptr[dev] == nullptr) {
-    void* ptr = nullptr;
-    const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-    if (err != hipSuccess || ptr == nullptr)
-      return fail(VGO_ELAUNCH, std::string("mass_bias_attention(static): hipGetSymbolAddress: ") +
-                                   hipGetErrorString(err));
-    g_scratch_ptr[dev] = ptr;
-  }
-  *out = g_scratch_ptr[dev];
-  return VGO_OK;
-}
-
 }  // namespace
 
 extern "C" int vgo_mass_bias_attn_fwd(const void* q, const void* k, const void* v,
@@ -1586,7 +1555,18 @@ extern "C" int vgo_attn_kernel_timing(int enable) {
     return fail(VGO_EINVAL, "vgo_attn_kernel_timing: read the launches recorded on device " +
                                 std::to_string(t.device) + " first");
   if (t.device != dev) {
-    // Events belong to the device they were created on: a new device starts a new pool.
+    // Events belong to the device they were created on: the old device's pool is
+    // destroyed there, and the new device starts a new one.
+    if (t.device >= 0) {
+      if (hipSetDevice(t.device) == hipSuccess) {
+        for (int i = 0; i < kTimingSlots; ++i) {
+          if (t.start[i]) (void)hipEventDestroy(t.start[i]);
+          if (t.stop[i]) (void)hipEventDestroy(t.stop[i]);
+        }
+      }
+      if (hipSetDevice(dev) != hipSuccess)
+        return fail(VGO_ELAUNCH, "vgo_attn_kernel_timing: cannot return to the current device");
+    }
     for (int i = 0; i < kTimingSlots; ++i) t.start[i] = t.stop[i] = nullptr;
   }
   t.device = dev;

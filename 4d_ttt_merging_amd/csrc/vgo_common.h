@@ -16,6 +16,10 @@ void set_error(const std::string& msg);
 int fail(int status, const std::string& msg);
 int check_launch(const char* what);
 
+// Device address of the current device's static scratch (VGO_ATTN_STATIC_SCRATCH_BYTES,
+// csrc/scratch.hip), looked up once per device.
+int static_scratch(void** out);
+
 #define VGO_REQUIRE(cond, msg)                      \
   do {                                              \
     if (!(cond)) return ::vgo::fail(VGO_EINVAL, msg); \

@@ -64,7 +64,13 @@ class Linear(nn.Linear):
     recorded, the cast copies are kept and reused until a parameter changes
     (its version counter or its storage), so the GEMM gets the operands that
     autocast would give it and the result is the same.  Writes that bypass the
-    version counter (through `.data`) must be followed by `clear_cast_cache()`."""
+    version counter (through `.data`) must be followed by `clear_cast_cache()`.
+
+    The cache is neither used nor built while the current stream is being
+    captured into a graph (a copy made there would only be filled when the
+    graph replays, and a replay must re-cast parameters updated in place
+    since), nor when autocast's own cast cache is switched off
+    (`cache_enabled=False`: every call then casts, as autocast does)."""
 
     def clear_cast_cache(self) -> None:
         self.__dict__.pop("_cast_cache", None)
@@ -92,7 +98,8 @@ class Linear(nn.Linear):
         dtype = _autocast_dtype()
         # A traced graph (torch.compile) keeps autocast's casts as graph nodes.
         if (dtype is not None and not torch.is_grad_enabled() and self.weight.is_cuda
-                and not torch.compiler.is_compiling()):
+                and not torch.compiler.is_compiling() and torch.is_autocast_cache_enabled()
+                and not torch.cuda.is_current_stream_capturing()):
             cast = self._cast_params(dtype)
             if cast is not None:
                 return F.linear(input, *cast)
@@ -519,9 +526,9 @@ class SelfAttentionBlock(nn.Module):
         for ls in (self.ls1, self.ls2):
             if not (type(ls) is nn.Identity or (type(ls) is LayerScale and not ls.inplace)):
                 return False
-        # Row starts must also be 16-byte aligned; the library checks that and raises (a
-        # contiguous [.., dim] tensor of torch's allocator with dim % 4 == 0 always is).
-        return dim % 4 == 0 and dim <= 2048 and x.is_contiguous()
+        # Row starts must be 16-byte aligned (the kernel's vector loads; the library
+        # raises otherwise): a view at an odd storage offset takes the torch path.
+        return dim % 4 == 0 and dim <= 2048 and x.is_contiguous() and x.data_ptr() % 16 == 0
 
     def _norm1_input(self, x: Tensor) -> Tensor:
         return _kernels.residual_layer_norm(x, norm=_ln_args(self.norm1), norm_dtype=_autocast_dtype())[1]

@@ -20,7 +20,10 @@ bypass layer).  The reference Aggregator module is loaded by registering
 `vggt_omega` and `vggt_omega.models` as bare package shells, so the package
 __init__ (the whole VGGT-Omega model) never runs.
 
-Usage:  PYTHONDONTWRITEBYTECODE=1 python tests/golden/make_fixtures.py [c1|agg|all]
+A third file, tests/golden/fixtures_c1w.npz (+ .json), holds the C1 merged layer at its
+stated width (dim 1024, 16 heads): see `wide_layer_fixture`.
+
+Usage:  PYTHONDONTWRITEBYTECODE=1 python tests/golden/make_fixtures.py [c1|agg|c1w|all]
 """
 from __future__ import annotations
 
@@ -288,9 +291,63 @@ def aggregator_fixture() -> None:
     print(f"wrote {len(out)} aggregator arrays")
 
 
+WIDE_DIM, WIDE_HEADS = 1024, 16
+
+
+def wide_layer_fixture() -> None:
+    """BASELINE configs[0] at its stated width: one merged global-attention layer, dim 1024,
+    16 heads of 64, on the C1 tokens (structured_tokens seed 1, the tokens the C1 plans of
+    fixtures_c1.npz were built from), CPU fp32, weights attention_weights(4, 1024).
+
+    Two arms, each the reference's own SelfAttention.forward with a plan its planners build
+    from the same tokens (so the plans are the ones fixtures_c1.npz already holds):
+    * fv  -- FastVGGT ratio 0.5 / protect 0 with integer cluster masses as the key bias:
+             the reference's TokenPlan given key_log_mass = log(bincount(inverse)), which
+             compute_attention reads by getattr (layers/attention.py:384-388) and, on CPU,
+             applies through SDPA with the float mask (:400);
+    * sc  -- the sparse-convex plan (threshold 0.9, Q/K/V compacted, dense special
+             queries), whose key_log_mass is log(normalizer).
+    Stores the two [1044, 1024] outputs in tests/golden/fixtures_c1w.npz (+ .json)."""
+    tm, sc, attn = load_reference()
+    kw = dict(frames=FRAMES, tokens_per_frame=TPF, patch_token_start=SPECIALS, patch_hw=HW)
+    c1 = np.load(HERE / "fixtures_c1.npz")
+    tokens = structured_tokens(1, FRAMES, HW, SPECIALS, WIDE_DIM)
+    manifest: dict[str, object] = {
+        "layout": dict(frames=FRAMES, patch_hw=HW, specials=SPECIALS),
+        "dim": WIDE_DIM, "heads": WIDE_HEADS, "weight_seed": 4, "tokens_seed": 1,
+        "tokens_sha256": sha256(tokens),
+    }
+    out: dict[str, np.ndarray] = {}
+    layer = attn.SelfAttention(WIDE_DIM, num_heads=WIDE_HEADS, qkv_bias=True, mask_k_bias=True,
+                               use_qk_norm=True).eval()
+    layer.load_state_dict(attention_weights(4, WIDE_DIM))
+    with torch.no_grad():
+        fv = tm.build_fastvggt_plan(tokens, merge_ratio=0.5, protect_ratio=0.0, **kw)
+        assert np.array_equal(fv.keep[0].numpy(), c1["fv50_keep"])
+        assert np.array_equal(fv.inverse[0].numpy(), c1["fv50_inverse"])
+        counts = torch.bincount(fv.inverse[0], minlength=fv.kept_tokens).float()
+        fv.key_log_mass = counts.log().view(1, -1)
+        manifest["fv_mass_max"] = float(counts.max())
+        out["fv_out"] = layer(tokens, token_plan=fv)[0].numpy()
+        plan = sc.build_sparse_convex_plan(tokens, threshold=0.90, **kw)
+        for name in ("keep", "source_original", "source_parent_compact", "source_pool_weights"):
+            key = {"keep": "sc_keep", "source_original": "sc_source",
+                   "source_parent_compact": "sc_parent", "source_pool_weights": "sc_weight"}[name]
+            assert np.array_equal(getattr(plan, name)[0].numpy(), c1[key]), name
+        assert plan.dense_special_queries
+        out["sc_out"] = layer(tokens, token_plan=plan)[0].numpy()
+    np.savez_compressed(HERE / "fixtures_c1w.npz", **out)
+    manifest["arrays"] = {k: [list(v.shape), str(v.dtype)] for k, v in out.items()}
+    manifest["arrays_sha256"] = {k: sha256(torch.from_numpy(v)) for k, v in out.items()}
+    (HERE / "fixtures_c1w.json").write_text(json.dumps(manifest, indent=1, default=str) + "\n")
+    print(f"wrote {len(out)} wide-layer arrays")
+
+
 if __name__ == "__main__":
     which = sys.argv[1] if len(sys.argv) > 1 else "all"
     if which in ("c1", "all"):
         main()
     if which in ("agg", "all"):
         aggregator_fixture()
+    if which in ("c1w", "all"):
+        wide_layer_fixture()

@@ -62,7 +62,37 @@ def test_cpu_tensors_are_rejected():
         vgo.mass_bias_attention(q, q, q, torch.zeros(4))
 
 
+def dynamic_exports(path: Path) -> set[str]:
+    """Names of the defined global/weak symbols of default or protected visibility in an
+    ELF64 little-endian shared object's .dynsym (what the dynamic linker resolves)."""
+    import struct
+    data = path.read_bytes()
+    assert data[:4] == b"\x7fELF" and data[4] == 2 and data[5] == 1, "not an ELF64 LE object"
+    shoff, = struct.unpack_from("<Q", data, 0x28)
+    shentsize, shnum = struct.unpack_from("<HH", data, 0x3A)
+    sections = [struct.unpack_from("<IIQQQQIIQQ", data, shoff + i * shentsize) for i in range(shnum)]
+    names = set()
+    for sh_name, sh_type, _, _, offset, size, link, _, _, entsize in sections:
+        if sh_type != 11:  # SHT_DYNSYM
+            continue
+        strtab = sections[link]
+        str_off = strtab[4]
+        for i in range(1, size // entsize):
+            st_name, st_info, st_other, st_shndx, _, _ = struct.unpack_from("<IBBHQQ", data, offset + i * entsize)
+            if st_shndx == 0 or (st_info >> 4) not in (1, 2) or (st_other & 3) in (1, 2):
+                continue  # undefined, local, hidden or internal
+            end = data.index(b"\0", str_off + st_name)
+            names.add(data[str_off + st_name:end].decode())
+    return names
+
+
 def test_library_symbols_are_only_the_c_abi():
-    # The shared object exports the vgo_* C entry points and no C++ kernel API.
-    lib_path = import_package("_lib").LIBRARY_PATH
-    assert Path(lib_path).exists()
+    """The shared object's dynamic symbol table holds the vgo_* C entry points the
+    header declares and nothing else (no C++ helpers, no compiler unit ids)."""
+    lib_path = Path(import_package("_lib").LIBRARY_PATH)
+    exports = dynamic_exports(lib_path)
+    assert set(declared_symbols()) <= exports
+    extra = sorted(name for name in exports if not name.startswith("vgo_"))
+    assert not extra, f"libvgo.so exports non-ABI symbols: {extra[:10]}"
+    undeclared = sorted(exports - set(declared_symbols()))
+    assert not undeclared, f"libvgo.so exports symbols include/vgo.h does not declare: {undeclared}"

@@ -251,16 +251,41 @@ def test_kernel_timing_records_each_workspace_launch(vgo, device):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("std", [2.0, 3.0])
+@pytest.mark.parametrize("std", [1.0, 2.0, 3.0])
 @pytest.mark.parametrize("nk", [1500, 3000])
 def test_wide_logits_match_oracle(vgo, device, dtype, std, nk):
-    """q, k at 2-3x unit scale (logits of tens in the exp2 domain) take the lazy
-    softmax's rescaling path on many tiles; both kernels (1,500 keys: register-
-    staged, 3,000: ping-pong) stay within the tolerance of the oracle."""
+    """q, k at unit scale (the aggregator's operating point: per-head LayerNorm'd
+    q and k) and at 2-3x unit scale (logits of tens in the exp2 domain, which take
+    the lazy softmax's rescaling path on many tiles); both kernels (1,500 keys:
+    register-staged, 3,000: ping-pong) stay within the tolerance of the oracle.
+    The measured error is printed beside the bar."""
     print(f"[attn] wide logits dtype={dtype} std={std} nk={nk}", flush=True)
     q, k, v, mass = _inputs(int(std * 10) + nk, 1, 4, 700, nk, dtype, mass_max=16, std=std)
     out = vgo.mass_bias_attention(q.to(device), k.to(device), v.to(device), mass.log().to(device))
     torch.cuda.synchronize()
     ref = oracle.mass_bias_attention(q, k, v, mass.log())
     assert torch.isfinite(out).all()
-    assert_close(out.cpu(), ref, dtype, what=f"std={std} nk={nk}")
+    err = assert_close(out.cpu(), ref, dtype, what=f"std={std} nk={nk}")
+    print(f"[attn] wide logits dtype={dtype} std={std} nk={nk}: rel err {err:.3e} (bar {RTOL[dtype]:.0e})",
+          flush=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_c4_unit_scale_rows_match_oracle(vgo, device, dtype):
+    """The C4 global attention where the aggregator runs it: 16 heads, 16,464 queries
+    over 16,464 merged keys with integer masses in [1, 8] (a ratio-0.5 FastVGGT plan
+    of 32,928 tokens), q and k at unit scale as the per-head LayerNorm leaves them.
+    Sampled query rows (the first and last included) of every head against the
+    float64 oracle."""
+    print(f"[attn] C4 unit-scale rows dtype={dtype}", flush=True)
+    q, k, v, mass = _inputs(71, 1, 16, 16464, 16464, dtype, mass_max=8, std=1.0)
+    bias = mass.log().to(dtype)
+    qd, kd, vd, bd = q.to(device), k.to(device), v.to(device), bias.to(device)
+    out = vgo.mass_bias_attention(qd, kd, vd, bd)
+    torch.cuda.synchronize()
+    g = torch.Generator().manual_seed(72)
+    rows = torch.cat([torch.randperm(16464, generator=g)[:62], torch.tensor([0, 16463])]).unique()
+    ref = oracle.mass_bias_attention(q[:, :, rows], k, v, bias.float())
+    err = assert_close(out[:, :, rows.to(device)].cpu(), ref, dtype, what=f"C4 unit-scale rows {dtype}")
+    print(f"[attn] C4 unit-scale rows dtype={dtype}: rel err {err:.3e} over {rows.numel()} rows x 16 heads "
+          f"(bar {RTOL[dtype]:.0e})", flush=True)

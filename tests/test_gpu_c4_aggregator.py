@@ -1,0 +1,110 @@
+"""C4 end to end: the 24-block aggregator at S=32 frames of 512x512.
+
+The workload bench.py times (vggt_omega/models/aggregator.py:776-808 with the global
+arm :841-1022, 1215-1216): dim 1024, 16 heads, MLP 4096, 4 register tokens, register
+blocks at (2, 6, 9, 14, 20) so 19 merged global blocks, cached layers (4, 11, 17, 23),
+FastVGGT at ratio 0.5 / protect 0 with the log-cluster-size key bias, bf16 autocast.
+
+Weights are not the 1e-5 LayerScale init the bench uses (under which no block moves
+the residual stream): LayerScale gammas lie in [0.2, 0.6], biases and LayerNorm
+affines are non-trivial (the rule of tests/golden/inputs.py `aggregator_state`,
+drawn on the GPU), so every block's branch shows in the output.
+
+The same model runs through bench.torch_reference_forward, the reference's op
+sequence in plain PyTorch (torch LayerNorm, RoPE and SDPA with a float log-mass
+mask; bmm / scatter_add / gather for the plan's compaction and restore), with this
+build's 19 plans replayed into it so both paths attend over the same clusters.
+This covers what per-block tests do not: the loop's in-place register-row writes,
+the restore folded into the next residual row pass, and the cached concatenation
+after 19 merged blocks.  Each cached output must lie within 2e-2 elementwise (the
+bf16 contract, with the RMS floor of tests/_tol.py) and 5e-3 in relative norm.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import bench
+from tests.conftest import import_package
+
+pytestmark = pytest.mark.gpu
+
+CACHED = (4, 11, 17, 23)
+
+
+def _seed_parameters(model, seed: int = 23) -> None:
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            leaf = name.rsplit(".", 1)[-1]
+            if leaf == "gamma":
+                p.copy_(0.2 + 0.4 * torch.rand(p.shape, generator=g, device=p.device))
+            elif name in ("camera_token", "register_token"):
+                p.copy_(torch.randn(p.shape, generator=g, device=p.device))
+            elif "norm" in name and leaf == "weight":
+                p.copy_(1.0 + 0.1 * torch.randn(p.shape, generator=g, device=p.device))
+            elif leaf == "bias":
+                p.copy_(0.05 * torch.randn(p.shape, generator=g, device=p.device))
+            elif leaf == "weight":
+                p.copy_(torch.randn(p.shape, generator=g, device=p.device) * p.shape[-1] ** -0.5)
+            else:
+                raise KeyError(name)
+
+
+def _errors(actual: torch.Tensor, expected: torch.Tensor) -> tuple[float, float]:
+    """(elementwise error with the RMS floor, relative norm error), on the GPU in float64."""
+    a, e = actual.double(), expected.double()
+    diff = (a - e).abs()
+    rms = e.pow(2).mean().sqrt()
+    elementwise = float((diff / torch.maximum(e.abs(), rms)).max())
+    return elementwise, float(diff.norm() / e.norm())
+
+
+def test_c4_aggregator_forward_vs_torch_restatement(device, monkeypatch):
+    agg = import_package("aggregator")
+    tm = import_package("token_merging")
+    print("[c4] building the 24-block model (dim 1024, S=32)", flush=True)
+    model, images = bench.build_model(agg, device)
+    _seed_parameters(model)
+    model.set_fastvggt(True, merge_ratio=0.5, protect_ratio=0.0, mass_bias=True)
+
+    plans = []
+    builder = agg.build_fastvggt_plan
+
+    def recording(*args, **kwargs):
+        plan = builder(*args, **kwargs)
+        plans.append(plan)
+        return plan
+
+    monkeypatch.setattr(agg, "build_fastvggt_plan", recording)
+    print("[c4] HIP forward", flush=True)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        outputs, start = model(images)
+    torch.cuda.synchronize()
+    assert start == bench.SPECIALS
+    tokens = bench.FRAMES * (bench.SPECIALS + bench.GRID[0] * bench.GRID[1])
+    stats = model.fastvggt_last_plan_stats
+    assert len(stats) == len(plans) == 19
+    assert [s["block_index"] for s in stats] == [i for i in range(24) if i not in (2, 6, 9, 14, 20)]
+    assert all(s["original_tokens"] == tokens and s["kept_tokens"] == tokens // 2 for s in stats)
+    assert [i for i, o in enumerate(outputs) if o is not None] == list(CACHED)
+
+    print("[c4] torch restatement with the 19 plans replayed", flush=True)
+    ref_global = bench.TorchReferenceGlobal(bench.FRAMES, bench.SPECIALS + 1024, bench.SPECIALS,
+                                            bench.GRID, 0.5, tm,
+                                            replay=[(p.keep, p.inverse) for p in plans])
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        reference = bench.torch_reference_forward(model, ref_global, model._input_patch_tokens_cache)
+    torch.cuda.synchronize()
+    assert not ref_global.replay, "the torch path did not consume every plan"
+    failures = []
+    for layer in CACHED:
+        ours, ref = outputs[layer], reference[layer]
+        assert ours.shape == ref.shape == (1, bench.FRAMES, tokens // bench.FRAMES, 2 * bench.DIM)
+        assert torch.isfinite(ours).all()
+        elementwise, norm = _errors(ours, ref)
+        print(f"[c4] cached layer {layer}: elementwise {elementwise:.2e} (bar 2e-2), relative norm "
+              f"{norm:.2e} (bar 5e-3), output rms {float(ref.double().pow(2).mean().sqrt()):.3f}", flush=True)
+        if elementwise > 2e-2 or norm > 5e-3:
+            failures.append(layer)
+    assert not failures, f"cached layers {failures} outside the bf16 tolerance"

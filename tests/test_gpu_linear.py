@@ -79,3 +79,55 @@ def test_linear_cast_cache_equals_autocast(layers, device, dtype, masked):
     with torch.autocast("cuda", dtype=dtype):
         out = lin(x)  # autograd on: no cached copies
     assert "_cast_cache" not in lin.__dict__ and out.requires_grad
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_linear_cast_cache_off_under_capture_and_cache_disabled(layers, device, masked):
+    """A graph captured with no warm-up casts inside the graph (no cached copy is built
+    during capture), an eager call before any replay equals plain autocast, every replay
+    sees an in-place parameter update made after the capture, and with autocast's cast
+    cache switched off no copy is kept."""
+    print(f"[linear cache] graph capture, masked={masked}", flush=True)
+    torch.manual_seed(1)
+    cls = layers.LinearKMaskedBias if masked else layers.Linear
+    lin = cls(256, 512, bias=True, device=device)
+    torch.nn.init.normal_(lin.bias)
+    x = torch.randn(200, 256, device=device)
+
+    def plain():
+        bias = lin.bias * lin.bias_mask if masked else lin.bias
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            return F.linear(x, lin.weight, bias)
+
+    def call():
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            return lin(x)
+
+    # The GEMM library's handle and workspace come from a plain product on a side
+    # stream (torch's capture pattern); the module itself is not called before capture.
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        plain()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static = call()
+    assert "_cast_cache" not in lin.__dict__
+    eager = call()  # before any replay
+    assert torch.equal(eager, plain())
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(static, plain())
+    with torch.no_grad():
+        lin.weight.mul_(0.25)
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(static, plain()) and not torch.equal(static, eager)
+    assert torch.equal(call(), plain())
+
+    lin.clear_cast_cache()
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16, cache_enabled=False):
+        out = lin(x)
+    assert "_cast_cache" not in lin.__dict__
+    assert torch.equal(out, plain())

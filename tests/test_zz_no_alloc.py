@@ -4,7 +4,10 @@ It runs the kernels of vgo_mass_bias_attn_fwd_ws with the library's static
 device scratch in place of a caller's workspace, so its output must equal the
 workspace entry's bit for bit.  Two calls in a row (the second smaller) check
 that the scratch's leftover contents from the first call do not leak into the
-second.  The size limit is checked on the host before any launch.
+second.  The size limit is checked on the host before any launch.  A call
+allocates nothing (torch's allocator and the device's free memory are unchanged
+across it), and the entry captured into a HIP graph replays correctly with other
+calls on the same scratch between the replays.
 """
 from __future__ import annotations
 
@@ -92,3 +95,46 @@ def test_static_entry_rejects_problems_beyond_its_scratch(device):
                                                lib_mod.VGO_BF16, torch.cuda.current_stream().cuda_stream)
     assert status == lib_mod.VGO_EWORKSPACE
     assert "static" in lib_mod.last_error() and "vgo_mass_bias_attn_fwd_ws" in lib_mod.last_error()
+
+
+@pytest.mark.gpu
+def test_static_entry_allocates_nothing_and_replays_from_a_graph(device):
+    """After its first call on a device, a call changes neither torch's allocated bytes
+    nor the device's free memory (hipMemGetInfo); the entry captured into a HIP graph
+    replays three times, with eager calls of another problem on the same scratch
+    between the replays, and every replay equals the workspace entry bit for bit."""
+    lib_mod = import_package("_lib")
+    lib = lib_mod.load()
+    stream = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    q, k, v, b = _problem(30, 3000, 2500, torch.bfloat16, device)
+    ref = _run("ws", q, k, v, b)
+    out = torch.full_like(q, float("nan"))
+    args = _args(lib_mod, q, k, v, b, out)
+    print("[no-alloc] eager call, then the allocation check", flush=True)
+    lib_mod.check(lib.vgo_mass_bias_attn_fwd_static(*args, stream()))
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    out.fill_(float("nan"))
+    torch.cuda.synchronize()
+    allocated, free = torch.cuda.memory_allocated(), torch.cuda.mem_get_info()[0]
+    lib_mod.check(lib.vgo_mass_bias_attn_fwd_static(*args, stream()))
+    torch.cuda.synchronize()
+    assert torch.cuda.memory_allocated() == allocated
+    assert torch.cuda.mem_get_info()[0] == free
+    assert torch.equal(out, ref)
+
+    print("[no-alloc] capture into a HIP graph and replay", flush=True)
+    captured = torch.full_like(q, float("nan"))
+    cargs = _args(lib_mod, q, k, v, b, captured)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        lib_mod.check(lib.vgo_mass_bias_attn_fwd_static(*cargs, stream()))
+    other = _problem(31, 700, 1900, torch.bfloat16, device, bias=False)
+    other_ref = _run("ws", *other)
+    for replay in range(3):
+        captured.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, ref), f"replay {replay} differs from the workspace entry"
+        assert torch.equal(_run("static", *other), other_ref)
+        torch.cuda.synchronize()
