@@ -526,9 +526,12 @@ class SelfAttentionBlock(nn.Module):
         for ls in (self.ls1, self.ls2):
             if not (type(ls) is nn.Identity or (type(ls) is LayerScale and not ls.inplace)):
                 return False
-        # Row starts must be 16-byte aligned (the kernel's vector loads; the library
-        # raises otherwise): a view at an odd storage offset takes the torch path.
-        return dim % 4 == 0 and dim <= 2048 and x.is_contiguous() and x.data_ptr() % 16 == 0
+        # Row starts must be 16-byte aligned (the kernel's vector loads): eagerly, a view
+        # at an odd storage offset takes the torch path.  A traced graph sees neither
+        # pointers nor storage offsets; there the library's own check raises for such a
+        # view (tensors of torch's allocator with dim % 4 == 0 are always aligned).
+        aligned = torch.compiler.is_compiling() or x.data_ptr() % 16 == 0
+        return dim % 4 == 0 and dim <= 2048 and x.is_contiguous() and aligned
 
     def _norm1_input(self, x: Tensor) -> Tensor:
         return _kernels.residual_layer_norm(x, norm=_ln_args(self.norm1), norm_dtype=_autocast_dtype())[1]

@@ -158,9 +158,12 @@ class TorchReferenceGlobal:
         pack = lambda t: self.compact(inverse, kept, t.transpose(1, 2).reshape(B, N, C))  # noqa: E731
         (qc, counts), (kc, _), (vc, _) = pack(q), pack(k), pack(v)
         heads = lambda t: t.reshape(B, kept, HEADS, C // HEADS).transpose(1, 2)  # noqa: E731
-        bias = counts[..., 0].log()[:, None, None, :].to(torch.bfloat16)
-        x = F.scaled_dot_product_attention(heads(qc).bfloat16(), heads(kc).bfloat16(),
-                                           heads(vc).bfloat16(), attn_mask=bias)
+        # Attention in the autocast dtype (the reference's mass_bias_attention casts its
+        # operands and the bias to it), in fp32 without autocast.
+        dtype = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else torch.float32
+        bias = counts[..., 0].log()[:, None, None, :].to(dtype)
+        x = F.scaled_dot_product_attention(heads(qc).to(dtype), heads(kc).to(dtype),
+                                           heads(vc).to(dtype), attn_mask=bias)
         x = attn.proj(x.transpose(1, 2).reshape(B, kept, C))
         restored = x.gather(1, inverse[..., None].expand(-1, -1, C))
         x_attn = tokens + blk.ls1(restored)

@@ -90,7 +90,7 @@ def test_linear_cast_cache_off_under_capture_and_cache_disabled(layers, device, 
     print(f"[linear cache] graph capture, masked={masked}", flush=True)
     torch.manual_seed(1)
     cls = layers.LinearKMaskedBias if masked else layers.Linear
-    lin = cls(256, 512, bias=True, device=device)
+    lin = cls(256, 768, bias=True, device=device)
     torch.nn.init.normal_(lin.bias)
     x = torch.randn(200, 256, device=device)
 
