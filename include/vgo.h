@@ -91,8 +91,9 @@ int vgo_mass_bias_attn_fwd_ws(const void* q, const void* k, const void* v, const
  * the reference; it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  The scratch is a static device array of
- * VGO_ATTN_STATIC_SCRATCH_BYTES that the library holds on every GPU it runs on
- * until the process ends; the first call on a device looks up its address.  A
+ * VGO_ATTN_STATIC_SCRATCH_BYTES in a code object of its own: a GPU holds it from
+ * the first call of this entry on that device (which looks up its address)
+ * until the process ends; processes that never call it do not hold it.  A
  * problem whose workspace (vgo_mass_bias_attn_workspace) exceeds it returns
  * VGO_EWORKSPACE before launching anything.  Calls on one GPU share that
  * array: calls that overlap on one GPU (different streams, or host threads)
