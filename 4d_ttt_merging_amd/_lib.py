@@ -78,6 +78,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "vgo_top4_project_ordered": (_c_int, [
         _c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_p,
     ]),
+    "vgo_top4_gather_probe": (_c_int, [
+        _c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p,
+    ]),
     "vgo_normalize_rows": (_c_int, [
         _c_p, _c_i64, _c_i64, _c_int, _c_p, _c_i64, _c_i64, _c_f32, _c_p, _c_i64, _c_int, _c_p,
     ]),

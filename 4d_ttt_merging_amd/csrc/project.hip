@@ -39,11 +39,16 @@ struct Vec16<f16_t> {
 // Persistent waves: each wave owns R consecutive output rows per step and issues
 // the gathers of all R rows (4 corners x CH 16-byte chunks per lane each) before
 // reducing any of them, so a CU keeps hundreds of KB of gathers in flight.
-template <typename T, int R, int CH>
+//
+// kRowSums (the gather probe, vgo_top4_gather_probe): the same gathers and
+// arithmetic, but each row's output values are summed in fp32 (per lane, then over
+// the wave) and only that sum is written, to row_sums[row]: the kernel's reads
+// without its 2 GB of row writes, for measuring what the fabric gives the reads.
+template <typename T, int R, int CH, bool kRowSums = false>
 __global__ __launch_bounds__(kWaves * 64) void top4_project_kernel(
     const T* __restrict__ table, int64_t table_stride, const int32_t* __restrict__ index,
     const float* __restrict__ weight, const int32_t* __restrict__ order, T* __restrict__ out,
-    int64_t out_stride, int64_t n_rows, int64_t table_rows, int dim) {
+    int64_t out_stride, int64_t n_rows, int64_t table_rows, int dim, float* __restrict__ row_sums = nullptr) {
   typedef typename Vec16<T>::type V;
   constexpr int VN = Vec16<T>::n;
   const int lane = lane_id();
@@ -91,6 +96,9 @@ __global__ __launch_bounds__(kWaves * 64) void top4_project_kernel(
       }
     }
 
+    float lane_sum[R];
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr) lane_sum[rr] = 0.0f;
     for (int base = 0; base < dim; base += CH * 64 * VN) {
       V y[R][4][CH];
 #pragma unroll
@@ -130,8 +138,22 @@ __global__ __launch_bounds__(kWaves * 64) void top4_project_kernel(
           V o;
 #pragma unroll
           for (int j = 0; j < VN; ++j) o[j] = from_f32<T>(bad[rr] ? __builtin_nanf("") : acc[j]);
-          __builtin_nontemporal_store(o, reinterpret_cast<V*>(o_row + e));
+          if constexpr (kRowSums) {
+#pragma unroll
+            for (int j = 0; j < VN; ++j) lane_sum[rr] += to_f32(o[j]);
+          } else {
+            __builtin_nontemporal_store(o, reinterpret_cast<V*>(o_row + e));
+          }
         }
+      }
+    }
+    if constexpr (kRowSums) {
+#pragma unroll
+      for (int rr = 0; rr < R; ++rr) {
+        float v = lane_sum[rr];
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+        if (lane == 0 && orow[rr] >= 0) row_sums[orow[rr]] = v;
       }
     }
   }
@@ -167,10 +189,15 @@ __global__ __launch_bounds__(256) void top4_project_scalar_kernel(
 template <typename T, int R, int CH>
 void launch_vec(const T* tb, int64_t table_stride, const int32_t* index, const float* weight,
                 const int32_t* order, T* ob, int64_t out_stride, int64_t n_rows, int64_t table_rows,
-                int dim, int64_t blocks, hipStream_t stream) {
-  hipLaunchKernelGGL((top4_project_kernel<T, R, CH>), dim3(static_cast<unsigned>(blocks)),
-                     dim3(kWaves * 64), 0, stream, tb, table_stride, index, weight, order, ob,
-                     out_stride, n_rows, table_rows, dim);
+                int dim, int64_t blocks, hipStream_t stream, float* row_sums) {
+  if (row_sums)
+    hipLaunchKernelGGL((top4_project_kernel<T, R, CH, true>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(kWaves * 64), 0, stream, tb, table_stride, index, weight, order, ob,
+                       out_stride, n_rows, table_rows, dim, row_sums);
+  else
+    hipLaunchKernelGGL((top4_project_kernel<T, R, CH>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(kWaves * 64), 0, stream, tb, table_stride, index, weight, order, ob,
+                       out_stride, n_rows, table_rows, dim, nullptr);
 }
 
 // Work-groups resident per CU for the persistent launch (MI355X: 256 CUs).
@@ -191,7 +218,8 @@ int device_cus() {
 template <typename T>
 int launch_project(const void* table, int64_t table_stride, const int32_t* index,
                    const float* weight, const int32_t* order, void* out, int64_t out_stride,
-                   int64_t n_rows, int64_t table_rows, int64_t dim, hipStream_t stream) {
+                   int64_t n_rows, int64_t table_rows, int64_t dim, hipStream_t stream,
+                   float* row_sums = nullptr) {
   const T* tb = static_cast<const T*>(table);
   T* ob = static_cast<T*>(out);
   constexpr int VN = Vec16<T>::n;
@@ -209,15 +237,16 @@ int launch_project(const void* table, int64_t table_stride, const int32_t* index
     };
     if (row_chunks >= 4) {
       launch_vec<T, 2, 4>(tb, table_stride, index, weight, order, ob, out_stride, n_rows, table_rows, d,
-                          blocks_for(2), stream);
+                          blocks_for(2), stream, row_sums);
     } else if (row_chunks >= 2) {
       launch_vec<T, 4, 2>(tb, table_stride, index, weight, order, ob, out_stride, n_rows, table_rows, d,
-                          blocks_for(4), stream);
+                          blocks_for(4), stream, row_sums);
     } else {
       launch_vec<T, 8, 1>(tb, table_stride, index, weight, order, ob, out_stride, n_rows, table_rows, d,
-                          blocks_for(8), stream);
+                          blocks_for(8), stream, row_sums);
     }
   } else {
+    if (row_sums) return fail(VGO_EUNSUPPORTED, "top4_gather_probe: rows must be whole 16-byte chunks");
     dim3 grid(static_cast<unsigned>((dim + 255) / 256), 1, 1);
     // Rows go on grid.y in slabs of 65535 (the y limit).
     for (int64_t r0 = 0; r0 < n_rows; r0 += 65535) {
@@ -270,6 +299,34 @@ extern "C" int vgo_top4_project(const void* table, int64_t table_row_stride, con
                                 void* stream) {
   return project_entry(table, table_row_stride, index, weight, nullptr, out, out_row_stride, n_rows,
                        table_rows, dim, dtype, stream);
+}
+
+extern "C" int vgo_top4_gather_probe(const void* table, int64_t table_row_stride,
+                                     const int32_t* index, const float* weight, float* row_sums,
+                                     int64_t n_rows, int64_t table_rows, int64_t dim, int dtype,
+                                     void* stream) {
+  using namespace vgo;
+  VGO_REQUIRE(n_rows >= 0 && table_rows >= 0 && dim >= 0, "top4_gather_probe: negative size");
+  if (n_rows == 0 || dim == 0) return VGO_OK;
+  VGO_REQUIRE(table && index && weight && row_sums, "top4_gather_probe: null pointer");
+  VGO_REQUIRE(dim <= 0x7fffffff && n_rows <= 0x7fffffff && table_row_stride >= dim,
+              "top4_gather_probe: bad size or stride");
+  VGO_REQUIRE(aligned(index, 16) && aligned(weight, 16),
+              "top4_gather_probe: index/weight must be 16-byte aligned [n,4] arrays");
+  hipStream_t s = as_stream(stream);
+  switch (dtype) {
+    case VGO_F32:
+      return launch_project<float>(table, table_row_stride, index, weight, nullptr, nullptr, dim, n_rows,
+                                   table_rows, dim, s, row_sums);
+    case VGO_BF16:
+      return launch_project<bf16_t>(table, table_row_stride, index, weight, nullptr, nullptr, dim, n_rows,
+                                    table_rows, dim, s, row_sums);
+    case VGO_F16:
+      return launch_project<f16_t>(table, table_row_stride, index, weight, nullptr, nullptr, dim, n_rows,
+                                   table_rows, dim, s, row_sums);
+    default:
+      return fail(VGO_EINVAL, "top4_gather_probe: unknown dtype");
+  }
 }
 
 extern "C" int vgo_top4_project_ordered(const void* table, int64_t table_row_stride,

@@ -42,6 +42,24 @@ def locality_order(index: torch.Tensor, table_rows: int) -> torch.Tensor:
     return order.view(torch.int32)
 
 
+def gather_probe(table: torch.Tensor, index: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """The projection's gathers and arithmetic without its row writes: each output row's
+    values summed in fp32 (float32 [N]).  A measurement probe (vgo_top4_gather_probe):
+    its time is what the memory fabric gives `top4_project`'s random-row reads."""
+    lib = _lib.load()
+    _lib.require_gpu(table, index, weight)
+    if table.ndim != 2 or index.shape != weight.shape or index.ndim != 2 or index.shape[1] != 4:
+        raise ValueError("gather_probe requires table [M,D], index [N,4] and weight [N,4]")
+    if index.dtype != torch.int32 or weight.dtype != torch.float32 or table.stride(-1) != 1:
+        raise ValueError("gather_probe requires int32 indices, float32 weights and unit-stride rows")
+    index, weight = index.contiguous(), weight.contiguous()
+    sums = torch.empty(index.shape[0], device=table.device, dtype=torch.float32)
+    _lib.check(lib.vgo_top4_gather_probe(
+        table.data_ptr(), table.stride(0), index.data_ptr(), weight.data_ptr(), sums.data_ptr(),
+        index.shape[0], table.shape[0], table.shape[1], _lib.dtype_code(table.dtype), _lib.stream_of(table)))
+    return sums
+
+
 def _top4_project_impl(table: torch.Tensor, index: torch.Tensor, weight: torch.Tensor, *,
                        out: torch.Tensor | None = None,
                        order: torch.Tensor | None = None) -> torch.Tensor:

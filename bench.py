@@ -337,8 +337,9 @@ def gather_ceiling(device, steps):
     index_select (independent of this build's kernels): 1,048,576 rows of 2 KB (bf16 x
     1,024) gathered from tables of 4 MB (L2-resident), 32 MB (MALL) and 512 MB (HBM);
     GB/s counts the bytes gathered plus the bytes written.  Beside it: a plain 2 GB
-    device copy, and this build's projection kernel with one-hot weights (one gather
-    per row) on the 512 MB table."""
+    device copy, this build's projection kernel with one-hot weights (one gather per
+    row) on the 512 MB table, and the C2 restore split into a read-only and a
+    write-only stream (`c2_streams`)."""
     vgo = importlib.import_module("4d_ttt_merging_amd")
     n, d = 1 << 20, DIM
     g = torch.Generator(device=device).manual_seed(7)
@@ -359,6 +360,30 @@ def gather_ceiling(device, steps):
     src = torch.empty(n * d, device=device, dtype=torch.bfloat16).fill_(1)
     sec = event_time(lambda: out.view(-1).copy_(src), steps, 2)
     res["copy_2GB_gbs"] = round(2 * n * d * 2 / sec / 1e9, 1)
+    del src
+    # The C2 restore split into its two streams.  Read-only: the gather probe
+    # (vgo_top4_gather_probe) does the projection's four random-row gathers per row
+    # from the 128 MB (MALL-resident) C2 table and its arithmetic, and writes one
+    # float per row.  Write-only: a 2 GiB fill, the size of the C2 output.  Then the
+    # projection itself; its time against the sum of the two says whether the
+    # fabric overlaps its reads with its writes.
+    proj = importlib.import_module("4d_ttt_merging_amd.projection")
+    m = 65536
+    index, weight = c2_inputs(n, m)
+    index, weight = index.to(device), weight.to(device)
+    table = torch.randn(m, d, device=device, generator=g).bfloat16()
+    read_sec = event_time(lambda: proj.gather_probe(table, index, weight), steps, 2)
+    write_sec = event_time(lambda: out.fill_(0.5), steps, 2)
+    proj_sec = event_time(lambda: vgo.top4_project(table, index, weight, out=out), steps, 2)
+    logical = 4 * n * d * 2
+    res["c2_streams"] = {
+        "read_only_probe_ms": round(read_sec * 1e3, 4),
+        "read_only_logical_gbs": round((logical + 32 * n) / read_sec / 1e9, 1),
+        "write_only_2GiB_ms": round(write_sec * 1e3, 4),
+        "write_only_gbs": round(n * d * 2 / write_sec / 1e9, 1),
+        "projection_ms": round(proj_sec * 1e3, 4),
+        "read_plus_write_ms": round((read_sec + write_sec) * 1e3, 4),
+        "projection_over_sum": round(proj_sec / (read_sec + write_sec), 3)}
     return res
 
 

@@ -190,6 +190,18 @@ int vgo_top4_project_ordered(const void* table, int64_t table_row_stride, const 
                              int64_t out_row_stride, int64_t n_rows, int64_t table_rows,
                              int64_t dim, int dtype, void* stream);
 
+/*
+ * Gather probe: vgo_top4_project's gathers and arithmetic with each output row
+ * summed (fp32, over its elements) into row_sums[n_rows] instead of being
+ * written, i.e. the projection's reads without its row writes.  No reference
+ * counterpart: a measurement of what the memory fabric gives the restore's
+ * random-row reads (bench.py --only gather).  Rows must be whole 16-byte chunks
+ * (else VGO_EUNSUPPORTED).
+ */
+int vgo_top4_gather_probe(const void* table, int64_t table_row_stride, const int32_t* index,
+                          const float* weight, float* row_sums, int64_t n_rows, int64_t table_rows,
+                          int64_t dim, int dtype, void* stream);
+
 
 /*
  * Row gather + L2 normalisation: out[r] = x[rows[r]] / max(||x[rows[r]]||, eps),

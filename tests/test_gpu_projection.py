@@ -98,3 +98,60 @@ def test_ordered_projection_equals_plain(dtype, device, n, m, d):
     done[partial[n // 2:].long().cpu()] = True
     assert torch.equal(out[done.to(device)], plain[done.to(device)])
     assert bool((out[~done.to(device)] == 7.0).all())
+
+
+@pytest.mark.parametrize("dtype,n,m,d,strided", [
+    (torch.bfloat16, 40007, 3000, 1024, False), (torch.float32, 33001, 1500, 1024, False),
+    (torch.float16, 33000, 2500, 1024, True), (torch.bfloat16, 33000, 2500, 1024, True),
+    (torch.bfloat16, 32800, 1100, 2048, False)])
+def test_large_tables_bit_exact(vgo, device, dtype, n, m, d, strided):
+    """Tables larger than an XCD's L2 (4 MB) with tens of thousands of rows, the C2
+    regime at a size the oracle checks whole: bit-exact on a ragged row count, strided
+    table and output views, a poisoned row (out-of-range id with a non-zero weight), a
+    zero-weight out-of-range id that must not poison, and one-hot rows."""
+    print(f"[project] large table dtype={dtype} n={n} m={m} d={d} strided={strided}", flush=True)
+    table, index, weight = _case(n + m + d, n, m, d, dtype)
+    index[5, 1] = m + 17           # poisons row 5
+    index[11, 3] = -2              # zero weight: ignored
+    weight[11, 3] = 0.0
+    weight[13] = torch.tensor([0.0, 1.0, 0.0, 0.0])   # one-hot row
+    assert table.numel() * table.element_size() > 4 << 20
+    if strided:
+        wide = torch.zeros(m, d + 256, dtype=dtype)
+        wide[:, 128:128 + d] = table
+        table_d = wide.to(device)[:, 128:128 + d]
+        out_full = torch.full((n, d + 64), 3.0, dtype=dtype, device=device)
+        out = out_full[:, 64:]
+    else:
+        table_d = table.to(device)
+        out_full = out = torch.empty(n, d, dtype=dtype, device=device)
+    vgo.top4_project(table_d, index.to(device), weight.to(device), out=out)
+    torch.cuda.synchronize()
+    got = out.cpu()
+    ref = oracle.top4_project(table, index, weight)
+    assert torch.isnan(got[5]).all() and torch.isfinite(got[11]).all()
+    assert torch.equal(torch.nan_to_num(got), torch.nan_to_num(ref))
+    assert torch.equal(got[13], table[index[13, 1].long()])
+    if strided:
+        assert bool((out_full[:, :64] == 3.0).all())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_gather_probe_sums_the_projection_rows(vgo, device, dtype):
+    """vgo_top4_gather_probe reads what the projection reads and writes each row's sum:
+    the sums equal the projection's rows summed (fp32, within summation-order
+    rounding), a poisoned row gives NaN in both, and rows of odd width are refused."""
+    print(f"[project] gather probe dtype={dtype}", flush=True)
+    from tests.conftest import import_package
+    proj = import_package("projection")
+    table, index, weight = _case(21, 5000, 700, 1024, dtype)
+    index[7, 2] = 1 << 20
+    td, idd, wd = table.to(device), index.to(device), weight.to(device)
+    sums = proj.gather_probe(td, idd, wd)
+    rows = proj.top4_project(td, idd, wd).double().sum(1)
+    assert torch.isnan(sums[7]) and torch.isnan(rows[7])
+    ok = ~torch.isnan(rows)
+    assert torch.allclose(sums[ok].double(), rows[ok], rtol=1e-5, atol=1e-3)
+    small = table[:, :23].contiguous().to(device)
+    with pytest.raises(RuntimeError, match="16-byte"):
+        proj.gather_probe(small, idd, wd)
