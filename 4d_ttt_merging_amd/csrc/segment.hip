@@ -14,6 +14,8 @@
 // TokenPlan (FastVGGT) compaction is the one-segment case: the members of a
 // cluster in ascending token order, divided by their count
 // (token_merging.py:176-191).
+#include <algorithm>
+
 #include "vgo_common.h"
 
 namespace vgo {
@@ -296,6 +298,11 @@ __device__ __forceinline__ void v16_widen(const V16Raw<T>& r, float* v) {
     for (int j = 0; j < kPer; ++j) v[i * kPer + j] = to_f32(r.h[i][j]);
 }
 
+// Streaming (non-temporal) stores: a compact row is written once and not read
+// back by this launch.  On the C4 q/k/v compaction (a 202 MB read, 102 MB
+// written) launched back to back this takes the kernel from about 65 to 58 us;
+// inside the aggregator forward, right after the qkv projection, both forms run
+// at 70 us.  Non-temporal loads of the member rows made it slower (84 us).
 template <typename T>
 __device__ __forceinline__ void v16_store(T* p, const float* v) {
   typedef typename V16<T>::half V;
@@ -305,7 +312,7 @@ __device__ __forceinline__ void v16_store(T* p, const float* v) {
     V x;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) x[j] = from_f32<T>(v[i * kPer + j]);
-    *reinterpret_cast<V*>(p + i * kPer) = x;
+    __builtin_nontemporal_store(x, reinterpret_cast<V*>(p + i * kPer));
   }
 }
 
@@ -507,11 +514,6 @@ __global__ __launch_bounds__(256) void compact16_kernel(
     const uint32_t* __restrict__ items, int item_shift, const int64_t* __restrict__ item_rows,
     const float* __restrict__ weights, int n_weights, const float* __restrict__ norm, int rows,
     int dim, float ln_eps, CompactOuts<TO, G> o) {
-  // Wave-uniform row: its index loads (offsets, items, row ids) go through the
-  // scalar cache and are counted apart from the member rows' vector loads.
-  const int w = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const int k = w / G;
-  const int gs = w - k * G;
   __shared__ float ln_lds[G][2][64];
   for (int e = threadIdx.x; e < G * 128; e += blockDim.x) {
     const int g = e >> 7, h = (e >> 6) & 1, j = e & 63;
@@ -519,16 +521,26 @@ __global__ __launch_bounds__(256) void compact16_kernel(
     ln_lds[g][h][j] = src ? src[j] : 0.0f;
   }
   __syncthreads();
-  if (k >= rows) return;
-  // Output gs's fields, selected with compile-time indices (indexing the
-  // kernel-argument arrays at run time would copy them to scratch).
-  CompactOut<TO> o1{o.x_off[0], o.ln_w[0], o.ln_b[0], o.out[0], o.ots[0], o.ohs[0]};
+  // Persistent waves: wave w pools units w, w + W, ... (unit u = output u % G of
+  // compact row u / G), so the LayerNorm parameters are staged once per resident
+  // work-group.  The unit is wave-uniform: its index loads (offsets, items, row ids)
+  // go through the scalar cache, apart from the member rows' vector loads.
+  const int units = rows * G;
+  const int stride = gridDim.x * 4;
+  for (int w = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)); w < units;
+       w += stride) {
+    const int k = w / G;
+    const int gs = w - k * G;
+    // Output gs's fields, selected with compile-time indices (indexing the
+    // kernel-argument arrays at run time would copy them to scratch).
+    CompactOut<TO> o1{o.x_off[0], o.ln_w[0], o.ln_b[0], o.out[0], o.ots[0], o.ohs[0]};
 #pragma unroll
-  for (int g = 1; g < G; ++g)
-    if (gs == g) o1 = CompactOut<TO>{o.x_off[g], o.ln_w[g], o.ln_b[g], o.out[g], o.ots[g], o.ohs[g]};
-  compact16_row<TI, TO, kFold>(x, xts, xhs, x_rows, base_rows, offsets, segs_per_row, items, item_shift,
-                               item_rows, weights, n_weights, norm, k, dim, ln_eps, o1, ln_lds[gs][0],
-                               ln_lds[gs][1]);
+    for (int g = 1; g < G; ++g)
+      if (gs == g) o1 = CompactOut<TO>{o.x_off[g], o.ln_w[g], o.ln_b[g], o.out[g], o.ots[g], o.ohs[g]};
+    compact16_row<TI, TO, kFold>(x, xts, xhs, x_rows, base_rows, offsets, segs_per_row, items, item_shift,
+                                 item_rows, weights, n_weights, norm, k, dim, ln_eps, o1, ln_lds[gs][0],
+                                 ln_lds[gs][1]);
+  }
 }
 
 // Launch of compact16_kernel for `rows` compact rows of G outputs.
@@ -538,7 +550,19 @@ int launch_compact16(const TI* x, int64_t xts, int64_t xhs, int64_t x_rows, cons
                      const int64_t* item_rows, const float* weights, int nw, const float* normalizer,
                      int rows, int dim, float ln_eps, const CompactOuts<TO, G>& o, hipStream_t s,
                      const char* what) {
-  const dim3 grid(static_cast<unsigned>((static_cast<int64_t>(rows) * G + 3) / 4));
+  // Resident work-groups only (the kernel loops over its units).
+  int per_cu = 0, dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  const bool fold = sp == 1 && !base_rows;
+  if ((fold ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, compact16_kernel<TI, TO, G, true>, 256, 0)
+            : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, compact16_kernel<TI, TO, G, false>, 256, 0)) !=
+          hipSuccess ||
+      per_cu <= 0)
+    per_cu = 1;
+  const int64_t need = (static_cast<int64_t>(rows) * G + 3) / 4;
+  const dim3 grid(static_cast<unsigned>(std::min<int64_t>(need, static_cast<int64_t>(cus) * per_cu)));
   if (sp == 1 && !base_rows)
     hipLaunchKernelGGL((compact16_kernel<TI, TO, G, true>), grid, dim3(256), 0, s, x, xts, xhs, x_rows,
                        base_rows, offsets, sp, items, item_shift, item_rows, weights, nw, normalizer, rows,
