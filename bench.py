@@ -775,6 +775,21 @@ def only_workload(which: str) -> int:
         print(json.dumps({"workload": "gather", **gather_ceiling(device, 3)}), flush=True)
         return 0
     vgo = importlib.import_module("4d_ttt_merging_amd")
+    if which == "c3attention":
+        # Three launches of BASELINE config 3's mass-bias attention (16 heads, 16,464
+        # queries x 8,232 keys, the inputs of c3_attention), for counter passes.
+        nq, nk = 16 * 1029, 8232
+        g = torch.Generator().manual_seed(5)
+        q = (torch.randn(1, HEADS, nq, 64, generator=g) * 0.125).bfloat16().to(device)
+        k = (torch.randn(1, HEADS, nk, 64, generator=g) * 0.125).bfloat16().to(device)
+        v = (torch.randn(1, HEADS, nk, 64, generator=g) * 0.125).bfloat16().to(device)
+        mass = torch.randint(1, 9, (nk,), generator=g).float().log().to(device)
+        for _ in range(3):
+            vgo.mass_bias_attention(q, k, v, mass)
+        torch.cuda.synchronize()
+        print(json.dumps({"workload": "c3attention", "heads": HEADS, "n_query": nq, "n_key": nk,
+                          "launches": 3}), flush=True)
+        return 0
     if which == "similarity":
         # The C4 matcher problem (23,808 source rows x 8,960 dictionary rows x 1,024,
         # unit rows, top-1), then the plain bf16 GEMM of the same shape through
@@ -885,9 +900,11 @@ def main() -> int:
     ap.add_argument("--aggregator-only", action="store_true",
                     help="time the C4 aggregator and print its line without the other legs "
                          "(for kernel traces of the forward alone)")
-    ap.add_argument("--only", choices=("attention", "projection", "merge", "copy", "gather", "similarity"), default=None,
+    ap.add_argument("--only", choices=("attention", "c3attention", "projection", "merge", "copy", "gather",
+                                       "similarity"), default=None,
                     help="run one kernel workload for rocprofv3 counter passes, then exit: "
-                         "'attention' = 3 C4-size mass-bias attention launches, 'projection' = 3 "
+                         "'attention' = 3 C4-size mass-bias attention launches, 'c3attention' = 3 "
+                         "C3 ones (16,464 queries x 8,232 keys), 'projection' = 3 "
                          "C2 bf16 top-4 projections, 'merge' = 3 x (norm1 unit rows, FastVGGT plan, "
                          "q/k/v compaction) of a C4 global block, 'copy' = 3 plain 256 MiB device "
                          "copies (the FETCH_SIZE / WRITE_SIZE calibration), 'gather' = the random-row "
