@@ -298,11 +298,6 @@ __device__ __forceinline__ void v16_widen(const V16Raw<T>& r, float* v) {
     for (int j = 0; j < kPer; ++j) v[i * kPer + j] = to_f32(r.h[i][j]);
 }
 
-// Streaming (non-temporal) stores: a compact row is written once and not read
-// back by this launch.  On the C4 q/k/v compaction (a 202 MB read, 102 MB
-// written) launched back to back this takes the kernel from about 65 to 58 us;
-// inside the aggregator forward, right after the qkv projection, both forms run
-// at 70 us.  Non-temporal loads of the member rows made it slower (84 us).
 template <typename T>
 __device__ __forceinline__ void v16_store(T* p, const float* v) {
   typedef typename V16<T>::half V;
@@ -312,7 +307,7 @@ __device__ __forceinline__ void v16_store(T* p, const float* v) {
     V x;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) x[j] = from_f32<T>(v[i * kPer + j]);
-    __builtin_nontemporal_store(x, reinterpret_cast<V*>(p + i * kPer));
+    *reinterpret_cast<V*>(p + i * kPer) = x;
   }
 }
 
