@@ -164,12 +164,12 @@ def _pair(vgo, main, special):
 def test_pair_launch_matches_oracle(vgo, device, dtype, shapes):
     """Merged attention and the dense special-query pass in one launch."""
     (b0, h0, nq0, nk0), (b1, h1, nq1, nk1) = shapes
-    if dtype == torch.float32:
-        # Over 20,000 unit-variance values the outputs average to ~1e-2, and the
-        # RMS floor of the relative error then meets fp32 summation error
-        # (1.3e-5 measured); the fp32 path keeps its 1e-5 bar at 4,096 keys.
-        nk0 = min(nk0, 4096)
-    print(f"[attn pair] dtype={dtype} shapes={shapes} nk0={nk0}", flush=True)
+    # fp32: each output averages nk unit-variance values to ~1/sqrt(nk) of their
+    # scale, so the fp32 rounding of the running sums, which grows as sqrt(nk)
+    # relative to that scale, sets the error (1.3e-5 measured at 20,000 keys).
+    # The bar is 1e-5 up to 4,096 keys and grows as sqrt(nk / 4,096) beyond.
+    rtol0 = 1e-5 * max(1.0, (nk0 / 4096) ** 0.5) if dtype == torch.float32 else None
+    print(f"[attn pair] dtype={dtype} shapes={shapes} rtol_main={rtol0}", flush=True)
     std = 1.0 if dtype == torch.float32 else 0.125
     q, k, v, mass = _inputs(7 + nq0 + nk1, b0, h0, nq0, nk0, dtype, std=std)
     sq, sk, sv, _ = _inputs(9 + nq1, b1, h1, nq1, nk1, dtype, std=std)
@@ -178,7 +178,9 @@ def test_pair_launch_matches_oracle(vgo, device, dtype, shapes):
     special = (sq.to(device), sk.to(device), sv.to(device))
     out0, out1 = _pair(vgo, main, special)
     torch.cuda.synchronize()
-    assert_close(out0, oracle.mass_bias_attention(q, k, v, bias.float()), dtype, what=f"pair main {shapes}")
+    err = assert_close(out0, oracle.mass_bias_attention(q, k, v, bias.float()), dtype, rtol=rtol0,
+                       what=f"pair main {shapes}")
+    print(f"[attn pair] main error {err:.3e}", flush=True)
     ref1 = oracle.mass_bias_attention(sq, sk, sv, torch.zeros(nk1))
     assert_close(out1, ref1, dtype, what=f"pair special {shapes}")
 
