@@ -8,11 +8,13 @@ register_token) and merge setters (`set_fastvggt`, `set_sparse_convex`,
 
 * global blocks run `build_fastvggt_plan` or `build_sparse_convex_plan`
   ("fixed_topology") and `SelfAttentionBlock.forward_compacted` on the HIP
-  library; register blocks and frame blocks (RoPE) are stock PyTorch as in the
-  reference;
-* the DINOv3 patch encoder is not part of this path: forward() consumes the
+  library; frame blocks (RoPE) and register blocks run the same block class
+  (fused row passes, QKV epilogue and attention kernels under autocast);
+* the DINOv3 patch encoder is not part of the merged path: forward() consumes the
   patch tokens installed with `set_input_patch_tokens_cache` (the reference's
-  own bypass, aggregator.py:233-241, 735-743);
+  own bypass, aggregator.py:233-241, 735-743), or, when built with
+  `patch_encoder`, runs `patch_encoder.PatchEncoder` on the normalised images
+  (aggregator.py:725-739) while no cache is installed;
 * the other planners (k-means, hash, TTT, temporal, reference-anchor, affine)
   are out of scope and rejected by the setters; plans they built can still
   run here through `set_sparse_convex_plans` (e.g. TTT trace records rebuilt
@@ -29,10 +31,14 @@ import torch.nn as nn
 
 from . import profiling
 from .layers import Mlp, SelfAttentionBlock, init_weights_vit, rope_sincos
+from .patch_encoder import PatchEncoder
 from .sparse_convex import build_sparse_convex_plan, start_sparse_convex_plan
 from .token_merging import build_fastvggt_plan
 
 _DEFAULT_SPARSE_CONVEX_QKV_LAYERS = tuple(layer for layer in range(19) if layer not in {8, 10, 11, 12})
+# Image normalisation in front of the patch encoder (aggregator.py:39-40, 729).
+_RESNET_MEAN = (0.485, 0.456, 0.406)
+_RESNET_STD = (0.229, 0.224, 0.225)
 
 
 class Aggregator(nn.Module):
@@ -40,7 +46,10 @@ class Aggregator(nn.Module):
                  num_heads: int = 16, mlp_ratio: float = 4.0, num_register_tokens: int = 16,
                  register_attention_block_indices: tuple[int, ...] = (2, 6, 9, 14, 20),
                  cached_layer_indices: tuple[int, ...] = (4, 11, 17, 23),
-                 device=None) -> None:
+                 patch_encoder: bool | PatchEncoder = False, device=None) -> None:
+        """`patch_encoder`: True builds the DINOv3 ViT-L/16 encoder of
+        aggregator.py:66-68, 1296-1320 (random init); a PatchEncoder instance is used
+        as given; False (the default) leaves forward() to cached patch tokens."""
         super().__init__()
 
         def block():
@@ -82,6 +91,11 @@ class Aggregator(nn.Module):
         self._sparse_convex_replay: list | None = None
         self._input_patch_tokens_cache: torch.Tensor | None = None
         self.init_weights()
+        if patch_encoder is True:
+            patch_encoder = PatchEncoder(patch_size=patch_size, embed_dim=embed_dim, device=device)
+        self.patch_embed = patch_encoder if isinstance(patch_encoder, PatchEncoder) else None
+        for name, value in (("_resnet_mean", _RESNET_MEAN), ("_resnet_std", _RESNET_STD)):
+            self.register_buffer(name, torch.tensor(value, device=device).view(1, 1, 3, 1, 1), persistent=False)
 
     # ---------------------------------------------------------- setters ----
     def set_fastvggt(self, enabled: bool = True, merge_ratio: float = 0.9,
@@ -170,8 +184,13 @@ class Aggregator(nn.Module):
             raise ValueError(f"Expected 3 input channels, got {num_channels}")
         patch_tokens = self._input_patch_tokens_cache
         if patch_tokens is None:
-            raise RuntimeError("the DINOv3 patch encoder is not part of this build: install patch "
-                               "tokens with set_input_patch_tokens_cache()")
+            if self.patch_embed is None:
+                raise RuntimeError("no patch tokens: install them with set_input_patch_tokens_cache() or "
+                                   "build the aggregator with patch_encoder=True")
+            normalized = (images - self._resnet_mean) / self._resnet_std
+            with profiling.span("patch_embed"):
+                patch_tokens = self.patch_embed(normalized.view(batch_size * num_frames, num_channels, height,
+                                                                width))["x_norm_patchtokens"]
         grid = (height // self.patch_size, width // self.patch_size)
         if (patch_tokens.shape[0] != batch_size * num_frames
                 or patch_tokens.shape[1] != grid[0] * grid[1]

@@ -9,7 +9,9 @@ FastVGGT bipartite planner merges at ratio 0.5 (protect_ratio 0, integer
 cluster masses as log-mass attention bias), attention runs on the compacted
 tokens, and the plan's top-4 restore (fused into the block's next residual row
 pass) brings all tokens back.  Patch tokens are a
-seeded N(0,1) cache (the DINOv3 encoder is not part of this path).
+seeded N(0,1) cache (the DINOv3 encoder is not part of the merged path); the
+`with_patch_encoder` field times the same forward with a random-init encoder
+in front instead.
 
 One JSON line: value = frames/s of the aggregator forward (whole job, one
 GPU), plus
@@ -874,6 +876,44 @@ def only_workload(which: str) -> int:
     return 0
 
 
+def with_patch_encoder(model, prof, device, steps: int) -> dict:
+    """The C4 forward with its DINOv3 patch encoder in place of the cached patch tokens
+    (BASELINE C4: "report both"): a random-init ViT-L/16 (24 blocks, dim 1,024, 16 heads,
+    4 storage tokens; aggregator.py:1296-1320) built from this package's blocks, on
+    seeded U(0,1) 512x512 images normalised as the reference does.  One warm-up, then
+    `steps` timed forwards; `patch_embed_ms` is the encoder's label time in one more."""
+    pe = importlib.import_module("4d_ttt_merging_amd.patch_encoder")
+    torch.manual_seed(1)
+    cache = model._input_patch_tokens_cache
+    model.patch_embed = pe.PatchEncoder(patch_size=16, embed_dim=DIM).to(device).eval()
+    model.set_input_patch_tokens_cache(None)
+    g = torch.Generator().manual_seed(2)
+    images = torch.rand(1, FRAMES, 3, GRID[0] * 16, GRID[1] * 16, generator=g).to(device)
+
+    def step():
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            return model(images)
+
+    try:
+        sec = timed(step, steps, 1)
+        prof.reset()
+        prof.enable(True, only=("patch_embed",))
+        step()
+        prof.enable(False)
+        total, calls = prof.summary()["patch_embed"]
+        prof.reset()
+    finally:
+        model.patch_embed = None
+        model.set_input_patch_tokens_cache(cache)
+        torch.cuda.empty_cache()
+    return {"frames_per_s": round(FRAMES / sec, 3), "ms_per_step": round(sec * 1e3, 3),
+            "patch_embed_ms": round(total / calls, 3),
+            "encoder": "DINOv3 ViT-L/16, 24 blocks, dim 1024, 16 heads, 4 storage tokens, random init "
+                       "(this package's SelfAttentionBlock: fused row passes, QKV epilogue with RoPE, "
+                       "attention kernel under bf16 autocast)",
+            "images": "seeded U(0,1) 32 x 3 x 512 x 512, mean/std-normalised as aggregator.py:729"}
+
+
 def clock_adjusted(achieved_tflops: float) -> dict | None:
     """The attention kernel's fraction of the bf16 peak at the clock the chip actually
     holds under it (from the committed counter profile), beside the nominal 2.4 GHz one:
@@ -1024,6 +1064,8 @@ def main() -> int:
     if args.aggregator_only:
         print(json.dumps(result), flush=True)
         return 0
+    log("C4 with the patch encoder")
+    result["with_patch_encoder"] = with_patch_encoder(model, prof, device, args.steps)
     log("C3 global block")
     result["c3_block"] = c3_block(vgo, device, 20)
     log("C5 long sequence")

@@ -100,5 +100,27 @@ def aggregator_state(seed: int, keys_and_shapes: list[tuple[str, tuple[int, ...]
     return out
 
 
+def encoder_state(seed: int, keys_and_shapes: list[tuple[str, tuple[int, ...]]]) -> dict[str, torch.Tensor]:
+    """Seeded values for the patch encoder's parameters (names as in the reference's
+    DinoVisionTransformer: patch_embed.proj.*, cls_token, storage_tokens, mask_token,
+    blocks.i.*, norm.*).  Block entries follow `aggregator_state`; the class and
+    storage tokens are N(0,1), the mask token zero (the reference adds 0 times it to
+    the class token), and the patch projection is scaled by its fan-in."""
+    out, blocks = {}, []
+    for key, shape in sorted(keys_and_shapes):
+        g = torch.Generator().manual_seed(seed * 1_000_003 + int(hashlib.sha256(key.encode()).hexdigest()[:8], 16))
+        if key in ("cls_token", "storage_tokens"):
+            out[key] = torch.randn(shape, generator=g)
+        elif key == "mask_token":
+            out[key] = torch.zeros(shape)
+        elif key == "patch_embed.proj.weight":
+            fan_in = shape[1] * shape[2] * shape[3]
+            out[key] = torch.randn(shape, generator=g) * fan_in ** -0.5
+        else:
+            blocks.append((key, shape))
+    out.update(aggregator_state(seed, blocks, 0))
+    return out
+
+
 def sha256(tensor: torch.Tensor) -> str:
     return hashlib.sha256(tensor.detach().cpu().contiguous().numpy().tobytes()).hexdigest()

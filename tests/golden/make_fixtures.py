@@ -23,7 +23,10 @@ __init__ (the whole VGGT-Omega model) never runs.
 A third file, tests/golden/fixtures_c1w.npz (+ .json), holds the C1 merged layer at its
 stated width (dim 1024, 16 heads): see `wide_layer_fixture`.
 
-Usage:  PYTHONDONTWRITEBYTECODE=1 python tests/golden/make_fixtures.py [c1|agg|c1w|all]
+A fourth file, tests/golden/fixtures_enc.npz (+ .json), holds the reference's DINOv3 patch
+encoder at reduced width: see `encoder_fixture`.
+
+Usage:  PYTHONDONTWRITEBYTECODE=1 python tests/golden/make_fixtures.py [c1|agg|c1w|enc|all]
 """
 from __future__ import annotations
 
@@ -41,6 +44,7 @@ sys.path.insert(0, str(HERE.parents[1]))
 from tests.golden.inputs import (  # noqa: E402
     aggregator_state,
     attention_weights,
+    encoder_state,
     seeded_values,
     sha256,
     structured_tokens,
@@ -343,6 +347,51 @@ def wide_layer_fixture() -> None:
     print(f"wrote {len(out)} wide-layer arrays")
 
 
+# A reduced DINOv3 patch encoder: the arguments of aggregator.py:1296-1320 at dim 128,
+# 2 heads, depth 2, on two 64x64 images (4x4 patches after the 16x16 projection).
+ENC = dict(embed_dim=128, depth=2, num_heads=2)
+ENC_IMAGES = (2, 3, 64, 64)
+ENC_WEIGHT_SEED, ENC_IMAGE_SEED = 23, 24
+
+
+def encoder_fixture() -> None:
+    """forward_features of the reference DinoVisionTransformer built as the aggregator's
+    _build_patch_embed builds it (reduced width), fp32 on CPU, seeded parameters
+    (tests/golden/inputs.py `encoder_state`), on seeded already-normalised images."""
+    load_reference_aggregator()
+    import importlib
+    vit = importlib.import_module("vggt_omega.models.layers.vision_transformer")
+    torch.manual_seed(0)
+    model = vit.DinoVisionTransformer(
+        img_size=224, patch_size=16, in_chans=3, pos_embed_rope_base=100,
+        pos_embed_rope_normalize_coords="max", pos_embed_rope_dtype="fp32", ffn_ratio=4,
+        qkv_bias=True, drop_path_rate=0.0, layerscale_init=1.0e-5, norm_layer="layernormbf16",
+        ffn_layer="mlp", ffn_bias=True, proj_bias=True, n_storage_tokens=4, mask_k_bias=True, **ENC)
+    model.init_weights()
+    model.eval()
+    # every parameter and the qkv bias masks; the RoPE periods keep their init
+    names = [(k, tuple(v.shape)) for k, v in model.state_dict().items() if not k.startswith("rope_embed.")]
+    state = encoder_state(ENC_WEIGHT_SEED, names)
+    missing, unexpected = model.load_state_dict(state, strict=False)
+    assert not unexpected and all(m.startswith("rope_embed.") for m in missing), missing
+    images = seeded_values(ENC_IMAGE_SEED, ENC_IMAGES)
+    with torch.no_grad():
+        feats = model.forward_features(images)
+    out = {k: feats[k].numpy() for k in ("x_norm_clstoken", "x_storage_tokens", "x_norm_patchtokens")}
+    manifest = {
+        "config": dict(ENC, images=list(ENC_IMAGES), weight_seed=ENC_WEIGHT_SEED, image_seed=ENC_IMAGE_SEED,
+                       patch_size=16, n_storage_tokens=4, rope_base=100, normalize_coords="max"),
+        "images_sha256": sha256(images),
+        "state_sha256": sha256(torch.cat([state[k].flatten() for k in sorted(state)])),
+        "state_keys": [[k, list(shape)] for k, shape in names],
+        "arrays": {k: [list(v.shape), str(v.dtype)] for k, v in out.items()},
+        "arrays_sha256": {k: sha256(torch.from_numpy(v)) for k, v in out.items()},
+    }
+    np.savez_compressed(HERE / "fixtures_enc.npz", **out)
+    (HERE / "fixtures_enc.json").write_text(json.dumps(manifest, indent=1, default=str) + "\n")
+    print(f"wrote {len(out)} encoder arrays")
+
+
 if __name__ == "__main__":
     which = sys.argv[1] if len(sys.argv) > 1 else "all"
     if which in ("c1", "all"):
@@ -351,3 +400,5 @@ if __name__ == "__main__":
         aggregator_fixture()
     if which in ("c1w", "all"):
         wide_layer_fixture()
+    if which in ("enc", "all"):
+        encoder_fixture()
