@@ -186,7 +186,7 @@ class Aggregator(nn.Module):
         if patch_tokens is None:
             if self.patch_embed is None:
                 raise RuntimeError("no patch tokens: install them with set_input_patch_tokens_cache() or "
-                                   "build the aggregator with patch_encoder=True")
+                                   "build the aggregator with its patch encoder (patch_encoder=True)")
             normalized = (images - self._resnet_mean) / self._resnet_std
             with profiling.span("patch_embed"):
                 patch_tokens = self.patch_embed(normalized.view(batch_size * num_frames, num_channels, height,

@@ -27,6 +27,15 @@
 namespace vgo {
 namespace {
 
+// Stream-K partition: work-group w of `groups` runs units [sk_begin(w), sk_begin(w + 1)).
+__host__ __device__ __forceinline__ int64_t sk_begin(int64_t w, int64_t units, int64_t groups) {
+  return w * units / groups;
+}
+// Work-group whose range holds unit u.
+__host__ __device__ __forceinline__ int64_t sk_owner(int64_t u, int64_t units, int64_t groups) {
+  return ((u + 1) * groups - 1) / units;
+}
+
 constexpr int kTile = 128;       // dictionary rows and source rows per work-group step
 constexpr int kKc = 64;          // K chunk staged in LDS
 
@@ -375,6 +384,17 @@ __global__ __launch_bounds__(256, 2) void sim_topk_kernel(
 // one logical chunk per quarter-wave) are conflict-free.  Requires
 // dim % 32 == 0.  Invalid source row ids read row 0 through the DMA and score
 // 0 in the epilogue, as in the staged kernel.
+//
+// Two schedules.  kStreamK = false: work-group task t runs dictionary part
+// t % parts (tiles_per_part tiles) of source tile t / parts and merges its four
+// lists per source row through LDS into one.  kStreamK = true (top-1 without
+// the score matrix): the `units` (source tile, dictionary tile) pairs, source
+// tile major, are split evenly over the grid (stream-K: work-group w runs
+// [sk_begin(w), sk_begin(w + 1))), so no round of the grid runs part-empty;
+// the DMA ring runs on across source tiles, and at the end of its share of a
+// source tile a work-group writes each lane's best key (four lists per source
+// row) to slot w - (the tile's first owner) of `parts` slots, which
+// topk_finalize_kernel merges.
 constexpr int kRTile = 256;
 constexpr int kRWaves = 8;
 constexpr int kRKc = 32;
@@ -384,25 +404,43 @@ constexpr int kRTileElems = kRTile * kRKc;
 constexpr int kRDmaPerStep = 4;  // per wave: two 16-row blocks of each operand
 __device__ __forceinline__ int sw4(int row) { return (row >> 2) & 3; }
 
-template <int K>
+template <int K, bool kStreamK>
 __global__ __launch_bounds__(kRWaves * 64, 1) void sim_topk_ring_kernel(
     const bf16_t* __restrict__ src, int64_t src_stride, int64_t src_capacity,
     const int64_t* __restrict__ src_rows, const int* __restrict__ n_src_dev, int n_src,
     const bf16_t* __restrict__ dict,
     int64_t dict_stride, int n0, int off1, int n_dict, int dim, int tiles_per_part,
     uint64_t* __restrict__ partial, int parts, bf16_t* __restrict__ scores,
-    int64_t scores_stride) {
+    int64_t scores_stride, int units) {
+  static_assert(!kStreamK || K == 1, "the stream-K schedule is the top-1 kernel's");
   __shared__ __attribute__((aligned(16))) bf16_t a_lds[kRStages * kRTileElems];
   __shared__ __attribute__((aligned(16))) bf16_t b_lds[kRStages * kRTileElems];
 
   int ns = n_src;
   if (n_src_dev) ns = min(ns, *n_src_dev);
   const int task = xcd_remap(blockIdx.x, gridDim.x);
-  const int s0 = (task / parts) * kRTile;
-  if (s0 >= ns) return;
-  const int part = task % parts;
-  const int d_begin = part * tiles_per_part * kRTile;
-  const int d_end = min(n_dict, d_begin + tiles_per_part * kRTile);
+  // kStreamK: tiles_per_part is the dictionary's tile count; st_begin / dt_begin
+  // are the first unit's tiles, slot_begin the first segment's slot (a later
+  // segment starts its source tile, whose first owner is then this work-group).
+  int s0, part, d_begin, d_end, st_begin = 0, dt_begin = 0, slot_begin = 0, n_units = 0;
+  if constexpr (kStreamK) {
+    const int u_begin = static_cast<int>(sk_begin(task, units, gridDim.x));
+    n_units = static_cast<int>(sk_begin(task + 1, units, gridDim.x)) - u_begin;
+    st_begin = u_begin / tiles_per_part;
+    dt_begin = u_begin - st_begin * tiles_per_part;
+    slot_begin = task - static_cast<int>(sk_owner(static_cast<int64_t>(st_begin) * tiles_per_part, units,
+                                                   gridDim.x));
+    s0 = st_begin * kRTile;
+    part = 0;
+    d_begin = 0;
+    d_end = n_dict;
+  } else {
+    s0 = (task / parts) * kRTile;
+    if (s0 >= ns) return;
+    part = task % parts;
+    d_begin = part * tiles_per_part * kRTile;
+    d_end = min(n_dict, d_begin + tiles_per_part * kRTile);
+  }
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -418,26 +456,33 @@ __global__ __launch_bounds__(kRWaves * 64, 1) void sim_topk_ring_kernel(
   const int dr = lane >> 2;
   const int dpc = lane & 3;
   const bf16_t* src_p[2];
+  auto set_stile = [&](int stile) {  // this wave's DMA rows of source tile stile
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int r = 32 * wave + 16 * j + dr;
-    const int i = s0 + r;
-    const int64_t row = i < ns ? (src_rows ? src_rows[i] : i) : 0;
-    const bool ok = row >= 0 && row < src_capacity;
-    src_p[j] = src + (ok ? row : 0) * src_stride + 8 * (dpc ^ sw4(r));
-  }
+    for (int j = 0; j < 2; ++j) {
+      const int r = 32 * wave + 16 * j + dr;
+      const int i = stile * kRTile + r;
+      const int64_t row = i < ns ? (src_rows ? src_rows[i] : i) : 0;
+      const bool ok = row >= 0 && row < src_capacity;
+      src_p[j] = src + (ok ? row : 0) * src_stride + 8 * (dpc ^ sw4(r));
+    }
+  };
+  set_stile(s0 / kRTile);
   // Epilogue sources of this lane (lane = source row): an invalid row id scores 0.
   bool src_ok[2];
+  bool all_src_ok;
+  auto set_epilogue_stile = [&](int stile) {
 #pragma unroll
-  for (int sb = 0; sb < 2; ++sb) {
-    const int i = s0 + 64 * ws + 32 * sb + l32;
-    const int64_t row = i < ns ? (src_rows ? src_rows[i] : i) : 0;
-    src_ok[sb] = row >= 0 && row < src_capacity;
-  }
-  const bool all_src_ok = __ballot(!(src_ok[0] & src_ok[1])) == 0;
+    for (int sb = 0; sb < 2; ++sb) {
+      const int i = stile * kRTile + 64 * ws + 32 * sb + l32;
+      const int64_t row = i < ns ? (src_rows ? src_rows[i] : i) : 0;
+      src_ok[sb] = row >= 0 && row < src_capacity;
+    }
+    all_src_ok = __ballot(!(src_ok[0] & src_ok[1])) == 0;
+  };
+  set_epilogue_stile(s0 / kRTile);
 
   const int n_chunks = dim / kRKc;
-  const int n_dtiles = d_end > d_begin ? (d_end - d_begin + kRTile - 1) / kRTile : 0;
+  const int n_dtiles = kStreamK ? n_units : d_end > d_begin ? (d_end - d_begin + kRTile - 1) / kRTile : 0;
   const int n_steps = n_dtiles * n_chunks;
 
   const bf16_t* dict_p[2] = {dict, dict};
@@ -457,11 +502,14 @@ __global__ __launch_bounds__(kRWaves * 64, 1) void sim_topk_ring_kernel(
   // reads again): every call issues the same number of DMAs, which the
   // vmcnt waits below count on -- with fewer in flight, "at most N
   // outstanding" would no longer mean that the oldest step has landed.
-  int iss_step = 0, iss_dt = 0, iss_kc = 0, iss_stage = 0;
+  int iss_step = 0, iss_dt = dt_begin, iss_kc = 0, iss_stage = 0;
+  int iss_st = st_begin;  // kStreamK: the issued step's source tile
   // DMA q (0..3) of the next step: block q >> 1 of the dictionary (q even) or
   // source (q odd) operand; the last one moves on to the following step.
   auto issue_one = [&](int q) {
     if (q == 0 && iss_dt != cur_dt) set_dtile(iss_dt);
+    if constexpr (kStreamK)
+      if (q == 0 && iss_dt == 0 && iss_kc == 0 && iss_step > 0) set_stile(iss_st);
     const int blk = (32 * wave + 16 * (q >> 1)) * kRKc;
     if ((q & 1) == 0)
       lds_dma16_addr(dict_p[q >> 1] + iss_kc, lds_offset(a_lds + iss_stage * kRTileElems + blk));
@@ -474,6 +522,12 @@ __global__ __launch_bounds__(kRWaves * 64, 1) void sim_topk_ring_kernel(
         if (iss_kc == dim) {
           iss_kc = 0;
           ++iss_dt;
+          if constexpr (kStreamK) {
+            if (iss_dt == tiles_per_part) {
+              iss_dt = 0;
+              ++iss_st;
+            }
+          }
         }
       }
     }
@@ -530,7 +584,8 @@ __global__ __launch_bounds__(kRWaves * 64, 1) void sim_topk_ring_kernel(
     asm volatile("" ::: "memory");
     read_half(0, 0, a0, b0);
   }
-  int dt = 0, kcs = 0, stage = 0;
+  int dt = dt_begin, kcs = 0, stage = 0;
+  int st = st_begin;  // kStreamK: the computed unit's source tile
   for (int step = 0; step < n_steps; ++step) {
     const int next = stage == kRStages - 1 ? 0 : stage + 1;
     // Before the barrier: k-step 0's MFMAs (operands read in the previous
@@ -610,8 +665,9 @@ __global__ __launch_bounds__(kRWaves * 64, 1) void sim_topk_ring_kernel(
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[db][sb][r] = src_ok[sb] ? acc[db][sb][r] : 0.0f;
       }
+      if constexpr (kStreamK) s0 = st * kRTile;
       const int d0 = d_begin + dt * kRTile;
-      if (scores) {
+      if (!kStreamK && scores) {  // the stream-K kernel never writes scores
 #pragma unroll
         for (int sb = 0; sb < 2; ++sb) {
           const int i = s0 + 64 * ws + 32 * sb + l32;
@@ -760,12 +816,36 @@ __global__ __launch_bounds__(kRWaves * 64, 1) void sim_topk_ring_kernel(
         for (int db = 0; db < 4; ++db) acc[db][sb] = f32x16{};
       kcs = 0;
       ++dt;
+      if constexpr (kStreamK) {
+        const bool tile_done = dt == tiles_per_part;
+        const bool last = step == n_steps - 1;
+        if (tile_done || last) {
+          // End of this work-group's share of source tile st: every lane writes
+          // its two sources' best keys (list wd * 2 + hh) to the share's slot.
+          const int slot = st == st_begin ? slot_begin : 0;
+#pragma unroll
+          for (int sb = 0; sb < 2; ++sb) {
+            const int i = s0 + 64 * ws + 32 * sb + l32;
+            if (i < ns)
+              partial[static_cast<int64_t>(i) * parts + slot * 4 + wd * 2 + hh] =
+                  top_j[sb] >= 0 ? make_key(top_v[sb], top_j[sb]) : 0ull;
+            top_v[sb] = -__builtin_inff();
+            top_j[sb] = -1;
+          }
+        }
+        if (tile_done) {
+          dt = 0;
+          ++st;
+          if (!last) set_epilogue_stile(st);
+        }
+      }
     } else {
       ++kcs;
     }
   }
   // The look-ahead DMAs land before the ring's LDS is reused for the merge.
   wait_vmem<0>();
+  if constexpr (kStreamK) return;
   __syncthreads();
 
   if (K == 1) {
@@ -800,19 +880,29 @@ __global__ __launch_bounds__(kRWaves * 64, 1) void sim_topk_ring_kernel(
 
 // Merge `parts` partial lists per source row; decode keys into the bf16 score
 // (as fp32) and the dictionary row (optionally mapped through index_map).
+// With sk_groups > 0 the lists come from the stream-K top-1 ring kernel: row i's
+// source tile was split over work-groups first..last of the schedule, which
+// wrote four lists each into slots 0 .. last - first of the row's `parts`.
 template <int K>
 __global__ __launch_bounds__(256) void topk_finalize_kernel(
     const uint64_t* __restrict__ partial, int n_src, const int* __restrict__ n_src_dev, int parts,
     int n0, int off1, float* __restrict__ values, int64_t* __restrict__ index64,
-    int32_t* __restrict__ index32, const int64_t* __restrict__ index_map) {
+    int32_t* __restrict__ index32, const int64_t* __restrict__ index_map, int sk_units, int sk_groups,
+    int sk_dict_tiles) {
   const int i = blockIdx.x * 256 + threadIdx.x;
   int ns = n_src;
   if (n_src_dev) ns = min(ns, *n_src_dev);
   if (i >= ns) return;
+  int used = parts;
+  if (sk_groups > 0) {
+    const int64_t u0 = static_cast<int64_t>(i / kRTile) * sk_dict_tiles;
+    const int64_t u1 = u0 + sk_dict_tiles - 1;
+    used = 4 * static_cast<int>(sk_owner(u1, sk_units, sk_groups) - sk_owner(u0, sk_units, sk_groups) + 1);
+  }
   TopK<K> m;
   m.init();
   const uint64_t* p = partial + static_cast<int64_t>(i) * parts * K;
-  for (int q = 0; q < parts * K; ++q) m.insert(p[q]);
+  for (int q = 0; q < used * K; ++q) m.insert(p[q]);
 #pragma unroll
   for (int t = 0; t < K; ++t) {
     const uint64_t key = m.k[t];
@@ -841,7 +931,7 @@ int64_t resident_groups(bool ring) {
   if (cache[ring][dev] == 0) {
     int cus = 0, per_cu = 0;
     const hipError_t occ =
-        ring ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, sim_topk_ring_kernel<K>, kRWaves * 64, 0)
+        ring ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, sim_topk_ring_kernel<K, false>, kRWaves * 64, 0)
              : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, sim_topk_kernel<K>, 256, 0);
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         occ != hipSuccess)
@@ -877,6 +967,44 @@ int choose_parts(int64_t n_src, int64_t n_dict, int topk, bool ring) {
   return best;
 }
 
+// Stream-K schedule of the top-1 ring kernel over units = source tiles x
+// dictionary tiles on as many work-groups as are resident.  It removes the
+// split schedule's last-round waste but gives up its cache locality (the
+// resident tasks of a round read a few dictionary tiles and source tiles
+// together; a stream-K share walks its own), so it is taken only where that
+// waste is large and a share spans few source tiles: when the longest share,
+// ceil(units / groups) tiles, is at least 5% below the split's rounds x tiles
+// per part, and a share is at most two dictionaries long.  At C4 (93 x 35
+// units, 256 work-groups) 13 against 2 x 7 tiles: 431 -> 393 us in a same-box
+// A/B; at 372 x 140 units (1.9% waste) stream-K ran 19% slower, at 47 x 18 units
+// (4 tiles either way) no faster.  `lists` = 4 x the most work-groups one source
+// tile is split over; groups = 0 when the split schedule is kept.
+struct StreamK {
+  int units = 0, groups = 0, dict_tiles = 0, lists = 0;
+};
+StreamK stream_k_schedule(int64_t n_src, int64_t n_dict) {
+  StreamK r;
+  const int64_t src_tiles = (n_src + kRTile - 1) / kRTile;
+  const int64_t dict_tiles = (n_dict + kRTile - 1) / kRTile;
+  if (src_tiles <= 0 || dict_tiles <= 0 || src_tiles * dict_tiles >= (1LL << 31)) return r;
+  const int64_t slots = resident_groups<1>(true);
+  const int p = choose_parts(n_src, n_dict, 1, true);
+  const int64_t tpp = (dict_tiles + p - 1) / p;
+  const int64_t split = (src_tiles * p + slots - 1) / slots * tpp;
+  const int64_t units = src_tiles * dict_tiles;
+  const int64_t share = (units + slots - 1) / slots;
+  if (static_cast<double>(share) > 0.95 * static_cast<double>(split) || share > 2 * dict_tiles) return r;
+  r.units = static_cast<int>(units);
+  r.groups = static_cast<int>(std::min(slots, units));
+  r.dict_tiles = static_cast<int>(dict_tiles);
+  int64_t most = 1;
+  for (int64_t st = 0; st < src_tiles; ++st)
+    most = std::max(most, sk_owner((st + 1) * dict_tiles - 1, units, r.groups) -
+                              sk_owner(st * dict_tiles, units, r.groups) + 1);
+  r.lists = static_cast<int>(4 * most);
+  return r;
+}
+
 }  // namespace
 }  // namespace vgo
 
@@ -885,8 +1013,9 @@ extern "C" int vgo_similarity_topk_workspace(int64_t n_src, int64_t n_dict, int 
   using namespace vgo;
   VGO_REQUIRE(topk == 1 || topk == 4, "similarity_topk: topk must be 1 or 4");
   VGO_REQUIRE(n_src >= 0 && n_dict >= 0, "similarity_topk: negative size");
-  // Sized for whichever kernel the dimension selects.
-  const int p = std::max(choose_parts(n_src, n_dict, topk, true), choose_parts(n_src, n_dict, topk, false));
+  // Sized for whichever kernel and schedule the dimension selects.
+  int p = std::max(choose_parts(n_src, n_dict, topk, true), choose_parts(n_src, n_dict, topk, false));
+  if (topk == 1) p = std::max(p, stream_k_schedule(n_src, n_dict).lists);
   if (parts) *parts = p;
   if (bytes) *bytes = static_cast<size_t>(n_src) * p * topk * sizeof(uint64_t);
   return VGO_OK;
@@ -915,17 +1044,18 @@ extern "C" int vgo_similarity_topk(const void* src, int64_t src_row_stride, int6
               "similarity_topk: dictionary ranges exceed the dictionary");
   VGO_REQUIRE(src_rows || n_src <= src_capacity, "similarity_topk: more sources than rows");
   const bool ring = use_ring(dim);
-  const int parts = choose_parts(n_src, n_dict, topk, ring);
+  const StreamK sk = ring && topk == 1 && !scores ? stream_k_schedule(n_src, n_dict) : StreamK{};
+  const int parts = sk.groups > 0 ? sk.lists : choose_parts(n_src, n_dict, topk, ring);
   const size_t need = static_cast<size_t>(n_src) * parts * topk * sizeof(uint64_t);
   VGO_REQUIRE(workspace && workspace_bytes >= need, "similarity_topk: workspace too small");
   VGO_REQUIRE(aligned(workspace, 8), "similarity_topk: workspace must be 8-byte aligned");
   const int64_t tile = ring ? kRTile : kTile;
   const int64_t dict_tiles = (n_dict + tile - 1) / tile;
-  const int tiles_per_part = static_cast<int>((dict_tiles + parts - 1) / parts);
+  const int tiles_per_part = sk.groups > 0 ? sk.dict_tiles : static_cast<int>((dict_tiles + parts - 1) / parts);
   hipStream_t s = as_stream(stream);
   const int64_t src_tiles = (n_src + tile - 1) / tile;
   VGO_REQUIRE(src_tiles * parts < (1LL << 31), "similarity_topk: grid too large");
-  dim3 grid(static_cast<unsigned>(src_tiles * parts));
+  dim3 grid(static_cast<unsigned>(sk.groups > 0 ? sk.groups : src_tiles * parts));
   uint64_t* partial = static_cast<uint64_t*>(workspace);
   const bf16_t* sp = static_cast<const bf16_t*>(src);
   const bf16_t* dp = static_cast<const bf16_t*>(dict);
@@ -934,16 +1064,18 @@ extern "C" int vgo_similarity_topk(const void* src, int64_t src_row_stride, int6
   if (ring) {
     // 64-bit row addresses per lane; the DMA reads stay inside the buffers
     // (rows are clamped, dim is a multiple of the chunk).
-    if (topk == 1)
-      hipLaunchKernelGGL((sim_topk_ring_kernel<1>), grid, dim3(kRWaves * 64), 0, s, sp, src_row_stride, src_capacity,
-                         src_rows, n_src_device, static_cast<int>(n_src), dp, dict_row_stride,
-                         static_cast<int>(dict_n0), static_cast<int>(dict_off1), static_cast<int>(n_dict),
-                         static_cast<int>(dim), tiles_per_part, partial, parts, sc, scores_row_stride);
+    auto launch = [&](auto kernel) {
+      hipLaunchKernelGGL(kernel, grid, dim3(kRWaves * 64), 0, s, sp, src_row_stride, src_capacity, src_rows,
+                         n_src_device, static_cast<int>(n_src), dp, dict_row_stride, static_cast<int>(dict_n0),
+                         static_cast<int>(dict_off1), static_cast<int>(n_dict), static_cast<int>(dim),
+                         tiles_per_part, partial, parts, sc, scores_row_stride, sk.units);
+    };
+    if (sk.groups > 0)
+      launch(sim_topk_ring_kernel<1, true>);
+    else if (topk == 1)
+      launch(sim_topk_ring_kernel<1, false>);
     else
-      hipLaunchKernelGGL((sim_topk_ring_kernel<4>), grid, dim3(kRWaves * 64), 0, s, sp, src_row_stride, src_capacity,
-                         src_rows, n_src_device, static_cast<int>(n_src), dp, dict_row_stride,
-                         static_cast<int>(dict_n0), static_cast<int>(dict_off1), static_cast<int>(n_dict),
-                         static_cast<int>(dim), tiles_per_part, partial, parts, sc, scores_row_stride);
+      launch(sim_topk_ring_kernel<4, false>);
   } else if (topk == 1) {
     hipLaunchKernelGGL((sim_topk_kernel<1>), grid, dim3(256), 0, s, sp, src_row_stride, src_capacity, src_rows,
                        n_src_device, static_cast<int>(n_src), dp, dict_row_stride,
@@ -960,10 +1092,11 @@ extern "C" int vgo_similarity_topk(const void* src, int64_t src_row_stride, int6
   if (topk == 1)
     hipLaunchKernelGGL((topk_finalize_kernel<1>), dim3(blocks2), dim3(256), 0, s, partial,
                        static_cast<int>(n_src), n_src_device, parts, static_cast<int>(dict_n0),
-                       static_cast<int>(dict_off1), values, index64, index32, index_map);
+                       static_cast<int>(dict_off1), values, index64, index32, index_map, sk.units, sk.groups,
+                       sk.dict_tiles);
   else
     hipLaunchKernelGGL((topk_finalize_kernel<4>), dim3(blocks2), dim3(256), 0, s, partial,
                        static_cast<int>(n_src), n_src_device, parts, static_cast<int>(dict_n0),
-                       static_cast<int>(dict_off1), values, index64, index32, index_map);
+                       static_cast<int>(dict_off1), values, index64, index32, index_map, 0, 0, 0);
   return check_launch("similarity_topk");
 }
