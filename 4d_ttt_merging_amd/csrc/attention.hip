@@ -26,13 +26,14 @@
 //    multiply but adds a logit error of up to 2^-9 of each product, which
 //    grows with the logit scale: 7e-2 of the output at q, k of 3x unit scale
 //    in bf16.)  Sub-tile 0's multiplies run under sub-tile 1's MFMAs.  The
-//    per-key bias and the softmax offset ride in the MFMA: a fifth k-step
-//    multiplies the key-side column pair (hi, lo) = (log m, 0) with log m in
-//    the input dtype, and a column of ones, with the query-side (1, 1, -mref).
-//    It has three terms, so it runs as one 8-deep v_mfma_f32_32x32x8, which
-//    takes the matrix pipe for less time than a 16-deep one (same accumulator
-//    layout, same sums).  The reference rounds log(m) to the input dtype
-//    first (mass_bias_attention.py:109); so do we.
+//    per-key bias enters as the accumulator the score MFMAs start from: in
+//    S^T a register holds one key for all 32 queries of its lane half, so the
+//    tile's fp32 biases (log m in the input dtype, as the reference rounds it
+//    first, mass_bias_attention.py:109; -inf past n_key) are four 16-byte LDS
+//    broadcast reads per 32-key sub-tile, shared by both query blocks.  The
+//    softmax offset -mref joins the log2(e) multiply as the addend of an fma,
+//    so neither takes an MFMA k-step (an 8-deep v_mfma_f32_32x32x8 holds the
+//    matrix pipe as long as a 16-deep one).
 //  * Lazy online softmax: P = e^S straight from the accumulator while no
 //    logit exceeds the reference max mref by more than 15 ln 2 (checked through the
 //    per-lane sums); only then, and on a segment's first tile, are the tile's
@@ -74,12 +75,6 @@ struct Mma<bf16_t> {
   static __device__ __forceinline__ f32x16 mma(op8 a, op8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
-  // 8-deep product (lanes 0-31 hold k-slots 0-3, lanes 32-63 slots 4-7).
-  static __device__ __forceinline__ f32x16 mma8(op4 a, op4 b, f32x16 c) {
-    typedef short s4 __attribute__((ext_vector_type(4)));
-    return __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(__builtin_bit_cast(s4, a), __builtin_bit_cast(s4, b), c,
-                                                     0, 0, 0);
-  }
 };
 template <>
 struct Mma<f16_t> {
@@ -88,9 +83,6 @@ struct Mma<f16_t> {
   typedef f16x4 op4;
   static __device__ __forceinline__ f32x16 mma(op8 a, op8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ f32x16 mma8(op4 a, op4 b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x8f16(a, b, c, 0, 0, 0);
   }
 };
 
@@ -136,10 +128,10 @@ struct AttnArgs {
   int64_t qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn, osb, osh, osn;
   float c;  // 1/8, folded into Q (exact)
   // LDS-DMA kernel only: V^T packed per (batch*head) as [64][npad] in the MFMA
-  // key order, and per key the pair (hi, lo) = (bias, 0) ((-inf, 0) past
-  // n_key), 2*npad long.
+  // key order, and per key the bias as fp32 (the input dtype's value; -inf past
+  // n_key), npad long.
   const T* vt;
-  const T* bias2;
+  const float* kbias;
   int npad;
 };
 
@@ -171,18 +163,7 @@ __host__ __device__ __forceinline__ int64_t sk_owner(int64_t u, int64_t units, i
 }
 
 // LDS stages: 2 (register-staged kernel) or 4 (DMA kernel); a stage holds a
-// K tile, a V^T tile and the tile's 64 bias pairs (hi, lo), followed by 32
-// zero dwords: the bias k-step's A operand of lanes 32-63 is zero, and those
-// lanes read it from there, so the loaded dword is the operand as it stands
-// (no VALU step on it, hence no early wait for the read inside an MFMA run).
-constexpr int kBiasPairs = 2 * kBN;
-constexpr int kBiasSlot = kBiasPairs + kBN;
-// Every kernel zeroes the tail of its stages once, before its first barrier.
-template <typename T>
-__device__ __forceinline__ void zero_bias_tails(T* b_lds, int stages) {
-  for (int i = threadIdx.x; i < stages * (kBN / 2); i += blockDim.x)
-    reinterpret_cast<uint32_t*>(b_lds + (i / (kBN / 2)) * kBiasSlot + kBiasPairs)[i % (kBN / 2)] = 0u;
-}
+// K tile, a V^T tile and the tile's 64 key biases (fp32).
 // Largest per-lane sum of 32 probabilities the lazy softmax accepts without
 // moving its reference max.  It bounds every P by 2^15, below the largest
 // finite f16 (65,504), so the rounded P operands of either type stay finite;
@@ -203,14 +184,12 @@ struct WaveAttn {
   typedef typename Mma<T>::op4 op4;
 
   op8 qreg[kQB][4];  // Q' = Q / 8 (exact), B operands
-  uint32_t qneg[kQB];  // -mref as a T bit pattern (lanes 0-31; 0 elsewhere)
   // Reference max per query (a T value; -inf until a finite logit is seen);
-  // the running sum and O are relative to 2^mref.
-  float mref[kQB], lsum[kQB];
+  // the running sum and O are relative to e^mref.  nm = -mref log2(e), the
+  // offset of the exp2 argument (+inf while mref = -inf).
+  float mref[kQB], lsum[kQB], nm[kQB];
   f32x16 o[kQB][2];
   int off[4];  // LDS element offsets of logical chunk pair t of row l32
-  int boff[2];  // bias dword of sub-tile sub: key 32*sub + l32's pair, or a zero (lanes 32-63)
-  uint32_t low_lanes, one_bits;
   int l32, hh;
 
   // Q' = Q * c for the wave's rows qw0.. (rows past n_query read a valid row;
@@ -229,40 +208,38 @@ struct WaveAttn {
         for (int e = 0; e < 8; ++e) qreg[qb][t][e] = static_cast<T>(to_f32(raw[e]) * c);
       }
     }
-    low_lanes = hh == 0 ? 0xffffffffu : 0u;
-    one_bits = __builtin_bit_cast(uint16_t, static_cast<T>(1.0f));
     // Row l32 + 32 uses off[t ^ 2] (swz flips bit 2 of the chunk there).
     const int s0 = swz(l32);
 #pragma unroll
     for (int t = 0; t < 4; ++t) off[t] = l32 * kD + (((2 * t + hh) ^ s0) << 3);
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) boff[sub] = hh == 0 ? 2 * (sub * 32 + l32) : kBiasPairs + 2 * l32;
-#pragma unroll
     for (int qb = 0; qb < kQB; ++qb) {
       mref[qb] = -__builtin_inff();
-      qneg[qb] = neg_bits(mref[qb]);
+      nm[qb] = exp_offset(mref[qb]);
       lsum[qb] = 0.0f;
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt) o[qb][dt] = f32x16{};
     }
   }
 
-  // The bias k-step (8 deep).  A (keys; lanes 0-31 hold k-slots 0-3 of key
-  // l32, lanes 32-63 slots 4-7): {bias_hi, bias_lo, 1, 0}, the key's bias
-  // as a pair of T values (the second 0 for a T bias), and zeros.  B (queries):
-  // {1, 1, -offset, 0}, and zeros.
-  __device__ __forceinline__ uint32_t neg_bits(float offset) const {
-    return __builtin_bit_cast(uint16_t, static_cast<T>(-offset)) & low_lanes;
+  // Offset of the exp2 argument for reference max m: -m log2(e), +inf while
+  // m = -inf (every P then non-finite, which takes the rescaling path).
+  static __device__ __forceinline__ float exp_offset(float m) {
+    return m == -__builtin_inff() ? __builtin_inff() : -m * kLog2e;
   }
-  // Built where it is used (it is needed once per tile) rather than held.
-  __device__ __forceinline__ op4 offset_b(uint32_t neg) const {
-    const i32x2 w = {static_cast<int>((one_bits | (one_bits << 16)) & low_lanes), static_cast<int>(neg)};
-    return __builtin_bit_cast(op4, w);
-  }
-  __device__ __forceinline__ op4 bias_a(const T* bl, int sub) const {
-    const uint32_t bw = *reinterpret_cast<const uint32_t*>(bl + boff[sub]);
-    const i32x2 w = {static_cast<int>(bw), static_cast<int>(one_bits & low_lanes)};
-    return __builtin_bit_cast(op4, w);
+  // The key biases of sub-tile sub in the accumulator layout: register r of
+  // lane l holds key 32 sub + 8 (r / 4) + 4 (l / 32) + r % 4, so each group of
+  // four registers is one 16-byte LDS read (the same address in every lane of a
+  // half: a broadcast).  The score MFMAs start from it.
+  __device__ __forceinline__ f32x16 key_bias(const float* bl, int sub) const {
+    f32x16 c;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(bl + 32 * sub + 8 * g + 4 * hh);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) c[4 * g + e] = x[e];
+    }
+    return c;
   }
   // A operand of rows 32*half.. of a K or V^T tile, k-chunk pair t.
   __device__ __forceinline__ op8 tile_op(const T* tl, int half, int t) const {
@@ -273,18 +250,15 @@ struct WaveAttn {
   // the reads overlap each other rather than each MFMA waiting for its own).
   struct KOps {
     op8 k[2][4];  // K rows 32*sub.., k-chunk pair t
-    op4 b[2];     // bias k-step A operands
   };
   struct VOps {
     op8 v[4][2];  // V^T rows (dims) 32*dt.., key chunk pair t
   };
-  __device__ __forceinline__ void load_k(const T* kl, const T* bl, KOps& ops) const {
+  __device__ __forceinline__ void load_k(const T* kl, KOps& ops) const {
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
+    for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
       for (int t = 0; t < 4; ++t) ops.k[sub][t] = tile_op(kl, sub, t);
-      ops.b[sub] = bias_a(bl, sub);
-    }
   }
   __device__ __forceinline__ void load_v(const T* vl, VOps& ops) const {
 #pragma unroll
@@ -293,41 +267,40 @@ struct WaveAttn {
       for (int dt = 0; dt < 2; ++dt) ops.v[t][dt] = tile_op(vl, dt, t);
   }
 
-  // S^T = K Q'^T + bias - mref for the tile's two 32-key sub-tiles, times
-  // log2(e) (the exp2 domain the softmax takes them in).
-  __device__ __forceinline__ void scores(const KOps& ops, f32x16 (&s)[kQB][2]) const {
+  // S^T = K Q'^T + bias for the tile's two 32-key sub-tiles (the MFMAs start
+  // from the key biases); sub-tile 0 then leaves in the exp2 domain,
+  // S log2(e) - mref log2(e), as pv_scores leaves it.
+  __device__ __forceinline__ void scores(const KOps& ops, const float* bl, f32x16 (&s)[kQB][2]) const {
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
+      const f32x16 c = key_bias(bl, sub);
 #pragma unroll
-      for (int qb = 0; qb < kQB; ++qb) s[qb][sub] = f32x16{};
+      for (int qb = 0; qb < kQB; ++qb) s[qb][sub] = Mma<T>::mma(ops.k[sub][0], qreg[qb][0], c);
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+      for (int t = 1; t < 4; ++t)
 #pragma unroll
         for (int qb = 0; qb < kQB; ++qb) s[qb][sub] = Mma<T>::mma(ops.k[sub][t], qreg[qb][t], s[qb][sub]);
-#pragma unroll
-      for (int qb = 0; qb < kQB; ++qb) s[qb][sub] = Mma<T>::mma8(ops.b[sub], offset_b(qneg[qb]), s[qb][sub]);
     }
-    // Sub-tile 0 leaves in the exp2 domain, as pv_scores leaves it.
 #pragma unroll
     for (int qb = 0; qb < kQB; ++qb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[qb][0][r] *= kLog2e;
+      for (int r = 0; r < 16; ++r) s[qb][0][r] = fmaf(s[qb][0][r], kLog2e, nm[qb]);
   }
-  __device__ __forceinline__ void scores(const T* kl, const T* bl, f32x16 (&s)[kQB][2]) const {
+  __device__ __forceinline__ void scores(const T* kl, const float* bl, f32x16 (&s)[kQB][2]) const {
     KOps ops;
-    load_k(kl, bl, ops);
+    load_k(kl, ops);
     __builtin_amdgcn_sched_barrier(0);
-    scores(ops, s);
+    scores(ops, bl, s);
   }
 
-  // P = e^(x - shift) = exp2((x - shift) * log2(e)) for one 32-key sub-tile
-  // (x; kScaled: x is already (x - 0) * log2(e)), rounded to T and packed
-  // into B operands p[2*sub], p[2*sub+1] of O^T += V^T P^T.  The unrounded
-  // values are summed into part[4] (started by sub 0), as the reference sums
-  // its fp32 probabilities; the sum uses fp32 adds because dot instructions
-  // would share the matrix pipe with the other wave's MFMAs.
+  // P = e^(x - m) = exp2(x log2(e) + nmv) with nmv = -m log2(e), for one
+  // 32-key sub-tile (x; kScaled: x is already x log2(e) + nmv), rounded to T and
+  // packed into B operands p[2*sub], p[2*sub+1] of O^T += V^T P^T.  The
+  // unrounded values are summed into part[4] (started by sub 0), as the
+  // reference sums its fp32 probabilities; the sum uses fp32 adds because dot
+  // instructions would share the matrix pipe with the other wave's MFMAs.
   template <bool kScaled = false>
-  __device__ __forceinline__ void exp_pack(const f32x16& x, int sub, float shift, op8 (&p)[4],
+  __device__ __forceinline__ void exp_pack(const f32x16& x, int sub, float nmv, op8 (&p)[4],
                                            float (&part)[4]) const {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
@@ -335,8 +308,8 @@ struct WaveAttn {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int r = u * 8 + 2 * j;
-        const float e0 = __builtin_amdgcn_exp2f(kScaled ? x[r] : (x[r] - shift) * kLog2e);
-        const float e1 = __builtin_amdgcn_exp2f(kScaled ? x[r + 1] : (x[r + 1] - shift) * kLog2e);
+        const float e0 = __builtin_amdgcn_exp2f(kScaled ? x[r] : fmaf(x[r], kLog2e, nmv));
+        const float e1 = __builtin_amdgcn_exp2f(kScaled ? x[r + 1] : fmaf(x[r + 1], kLog2e, nmv));
         part[j] = sub == 0 && u == 0 ? e0 : part[j] + e0;
         part[j] += e1;
         const op2 pr = {static_cast<T>(e0), static_cast<T>(e1)};
@@ -349,12 +322,12 @@ struct WaveAttn {
     return (part[0] + part[1]) + (part[2] + part[3]);
   }
 
-  // Logits of query block qb against the sub-tile's 32 keys, no offset.
-  __device__ __forceinline__ f32x16 logits(const T* kl, const T* bl, int qb, int sub) const {
-    f32x16 x = {};
+  // Logits (with the key bias) of query block qb against the sub-tile's 32 keys.
+  __device__ __forceinline__ f32x16 logits(const T* kl, const float* bl, int qb, int sub) const {
+    f32x16 x = key_bias(bl, sub);
 #pragma unroll
     for (int t = 0; t < 4; ++t) x = Mma<T>::mma(tile_op(kl, sub, t), qreg[qb][t], x);
-    return Mma<T>::mma8(bias_a(bl, sub), offset_b(0u), x);
+    return x;
   }
 
   // Lazy online softmax of one tile's scores.  P = e^S directly while every
@@ -366,14 +339,14 @@ struct WaveAttn {
   // O and the sum are rescaled, and P is recomputed.  That path works one
   // 32-key sub-tile at a time (logits computed twice) to stay within the
   // registers the fast path leaves free.
-  __device__ __forceinline__ void softmax(const f32x16 (&s)[kQB][2], const T* kl, const T* bl,
+  __device__ __forceinline__ void softmax(const f32x16 (&s)[kQB][2], const T* kl, const float* bl,
                                           op8 (&p)[kQB][4]) {
     float part[kQB];
 #pragma unroll
     for (int qb = 0; qb < kQB; ++qb) {
       float acc[4];
       exp_pack<true>(s[qb][0], 0, 0.0f, p[qb], acc);
-      exp_pack(s[qb][1], 1, 0.0f, p[qb], acc);
+      exp_pack(s[qb][1], 1, nm[qb], p[qb], acc);
       part[qb] = sum4(acc);
     }
     if (__builtin_expect(__ballot(!(part[0] <= kLazyLimit) | !(part[1] <= kLazyLimit)) != 0, 0)) {
@@ -398,14 +371,14 @@ struct WaveAttn {
 #pragma unroll
             for (int r = 0; r < 16; ++r) o[qb][dt][r] *= corr;
           mref[qb] = mnew;
-          qneg[qb] = neg_bits(mnew);
+          nm[qb] = exp_offset(mnew);
         }
         // No finite logit yet: every P is 0 (x = -inf).
-        const float shift = mref[qb] == -__builtin_inff() ? 0.0f : mref[qb];
+        const float nmv = mref[qb] == -__builtin_inff() ? 0.0f : nm[qb];
         asm volatile("" ::: "memory");
         float acc[4];
-        exp_pack(logits(kl, bl, qb, 0), 0, shift, p[qb], acc);
-        exp_pack(logits(kl, bl, qb, 1), 1, shift, p[qb], acc);
+        exp_pack(logits(kl, bl, qb, 0), 0, nmv, p[qb], acc);
+        exp_pack(logits(kl, bl, qb, 1), 1, nmv, p[qb], acc);
         part[qb] = sum4(acc);
       }
     }
@@ -434,7 +407,7 @@ struct WaveAttn {
   // of the previous step run: their latency is hidden and at most about half
   // of the operands are held at once.
   __device__ __forceinline__ void pv_scores(const T* vl, const op8 (&p)[kQB][4], const T* kl,
-                                            const T* bl, f32x16 (&s)[kQB][2]) {
+                                            const float* bl, f32x16 (&s)[kQB][2]) {
     VOps vops;
     load_v(vl, vops);
     __builtin_amdgcn_sched_barrier(0);
@@ -442,7 +415,7 @@ struct WaveAttn {
   }
   // The same with the V^T operands already requested (vops).
   __device__ __forceinline__ void pv_scores(const VOps& vops, const op8 (&p)[kQB][4], const T* kl,
-                                            const T* bl, f32x16 (&s)[kQB][2]) {
+                                            const float* bl, f32x16 (&s)[kQB][2]) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -453,7 +426,7 @@ struct WaveAttn {
     op8 ka[4], kb[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) ka[t] = tile_op(kl, 0, t);
-    const op4 ba = bias_a(bl, 0);
+    const f32x16 ca = key_bias(bl, 0);
     __builtin_amdgcn_sched_barrier(0);
     // The second half's K reads go out between the last two P.V k-steps and
     // ahead of every score MFMA (left to itself the scheduler sinks them
@@ -467,7 +440,7 @@ struct WaveAttn {
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 0; t < 4; ++t) kb[t] = tile_op(kl, 1, t);
-    const op4 bb = bias_a(bl, 1);
+    const f32x16 cb = key_bias(bl, 1);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt)
@@ -476,26 +449,24 @@ struct WaveAttn {
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int qb = 0; qb < kQB; ++qb) {
-      s[qb][0] = f32x16{};
+      s[qb][0] = Mma<T>::mma(ka[0], qreg[qb][0], ca);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) s[qb][0] = Mma<T>::mma(ka[t], qreg[qb][t], s[qb][0]);
-      s[qb][0] = Mma<T>::mma8(ba, offset_b(qneg[qb]), s[qb][0]);
+      for (int t = 1; t < 4; ++t) s[qb][0] = Mma<T>::mma(ka[t], qreg[qb][t], s[qb][0]);
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int qb = 0; qb < kQB; ++qb) {
-      s[qb][1] = f32x16{};
+      s[qb][1] = Mma<T>::mma(kb[0], qreg[qb][0], cb);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) s[qb][1] = Mma<T>::mma(kb[t], qreg[qb][t], s[qb][1]);
-      s[qb][1] = Mma<T>::mma8(bb, offset_b(qneg[qb]), s[qb][1]);
+      for (int t = 1; t < 4; ++t) s[qb][1] = Mma<T>::mma(kb[t], qreg[qb][t], s[qb][1]);
     }
     // Sub-tile 0's scores into the exp2 domain under sub-tile 1's MFMAs.
 #pragma unroll
     for (int qb = 0; qb < kQB; ++qb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[qb][0][r] *= kLog2e;
+      for (int r = 0; r < 16; ++r) s[qb][0][r] = fmaf(s[qb][0][r], kLog2e, nm[qb]);
 #pragma unroll
-    for (int i = 0; i < 10; ++i) {
+    for (int i = 0; i < 8; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
       __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four VALU
     }
@@ -558,7 +529,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attn_reg_kernel(AttnArgs<T> a)
   typedef typename Mma<T>::op2 op2;
   __shared__ __attribute__((aligned(16))) T k_lds[2 * kTileElems];
   __shared__ __attribute__((aligned(16))) T vt_lds[2 * kTileElems];
-  __shared__ __attribute__((aligned(16))) T b_lds[2 * kBiasSlot];
+  __shared__ __attribute__((aligned(16))) float b_lds[2 * kBN];
   const int task = static_cast<int>(xcd_remap(blockIdx.x, gridDim.x));
   const int bh = task / a.n_qblocks;
   const int qblk = task - bh * a.n_qblocks;
@@ -573,7 +544,6 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attn_reg_kernel(AttnArgs<T> a)
 
   WaveAttn<T> w;
   w.init(a.q + b * a.qsb + h * a.qsh, a.qsn, qw0, a.nq, a.c);
-  zero_bias_tails(b_lds, 2);
 
   // K: rows st and st+32, chunk sc.  V: keys 2st, 2st+1, dims 8sc..8sc+7.
   // Row offsets fit in 32 bits (checked on the host).
@@ -600,7 +570,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attn_reg_kernel(AttnArgs<T> a)
     pv1 = *reinterpret_cast<const op8*>(vcol + min(kt + 2 * st + 1, last_key) * vsn);
     if (a.bias) pb = a.bias[min(kt + lane, last_key)];
   };
-  // Every wave writes the same 64 bias pairs (branch-free; identical data).
+  // Every wave writes the same 64 key biases (branch-free; identical data).
   auto stage_store = [&](int tile, int buf) {
     T* kl = k_lds + buf * kTileElems;
     T* vl = vt_lds + buf * kTileElems;
@@ -612,11 +582,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attn_reg_kernel(AttnArgs<T> a)
       *reinterpret_cast<op2*>(vl + vbase + i * kD + ((vphys ^ i) << 3)) = pr;
     }
     const bool valid = tile * kBN + lane < a.nk;
-    const float bv = valid ? (a.bias ? to_f32(pb) : 0.0f) : -__builtin_inff();
-    const T hi = static_cast<T>(bv);
-    const T lo = static_cast<T>(__builtin_isfinite(bv) ? bv - to_f32(hi) : 0.0f);
-    const op2 pair = {hi, lo};
-    *reinterpret_cast<op2*>(b_lds + buf * kBiasSlot + 2 * lane) = pair;
+    b_lds[buf * kBN + lane] = valid ? (a.bias ? to_f32(pb) : 0.0f) : -__builtin_inff();
   };
 
   stage_load(0);
@@ -627,7 +593,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attn_reg_kernel(AttnArgs<T> a)
     const bool more = tile + 1 < a.ntiles;
     if (more) stage_load(tile + 1);
     const T* kl = k_lds + buf * kTileElems;
-    const T* bl = b_lds + buf * kBiasSlot;
+    const float* bl = b_lds + buf * kBN;
     // A wave whose 64 queries all lie past n_query (the short last block of a
     // problem) only stages tiles and meets the barriers; its SIMD is then free
     // for the other work-group resident on the CU.
@@ -709,7 +675,7 @@ __device__ __forceinline__ void ring_barrier_reads_in_flight() {
 }
 
 template <typename T>
-__device__ __forceinline__ void attn_pp_segment(const AttnArgs<T>& a, T* k_lds, T* vt_lds, T* b_lds,
+__device__ __forceinline__ void attn_pp_segment(const AttnArgs<T>& a, T* k_lds, T* vt_lds, float* b_lds,
                                                 int bh, int qblk, int tile0, int tile1, float* partial) {
   typedef typename Mma<T>::op8 op8;
   const int b = bh / a.heads;
@@ -732,7 +698,7 @@ __device__ __forceinline__ void attn_pp_segment(const AttnArgs<T>& a, T* k_lds, 
 
   // Per tile each group-0 wave issues rows 16*wave.. 16*wave+15 of K and of
   // V^T as two 8-row blocks (lane i: row i/8, physical chunk i%8, i.e. the
-  // global chunk (i%8) ^ swz(row)) and the tile's 64 bias pairs (every wave
+  // global chunk (i%8) ^ swz(row)) and the tile's 64 key biases (every wave
   // the same, so the count is uniform).
   const int dr = lane >> 3;
   const int dc = lane & 7;
@@ -752,11 +718,11 @@ __device__ __forceinline__ void attn_pp_segment(const AttnArgs<T>& a, T* k_lds, 
               lds_offset(kst + 8 * kD));
     lds_dma16(vt_head, v_off0 + kt * sizeof(T), lds_offset(vst));
     lds_dma16(vt_head, v_off1 + kt * sizeof(T), lds_offset(vst + 8 * kD));
-    lds_dma4(a.bias2, (lane + kt) * 2 * sizeof(T), lds_offset(b_lds + stage * kBiasSlot));
+    lds_dma4(a.kbias, (lane + kt) * sizeof(float), lds_offset(b_lds + stage * kBN));
   };
   auto kl = [&](int tile) { return k_lds + (tile & (kPPStages - 1)) * kTileElems; };
   auto vl = [&](int tile) { return vt_lds + (tile & (kPPStages - 1)) * kTileElems; };
-  auto bl = [&](int tile) { return b_lds + (tile & (kPPStages - 1)) * kBiasSlot; };
+  auto bl = [&](int tile) { return b_lds + (tile & (kPPStages - 1)) * kBN; };
 
   f32x16 s[kQB][2];
   op8 p[kQB][4];
@@ -866,10 +832,9 @@ template <typename T>
 __global__ __launch_bounds__(kPPWaves * 64, 1) void attn_pp_kernel(PPLaunch<T> L) {
   __shared__ __attribute__((aligned(16))) T k_lds[kPPStages * kTileElems];
   __shared__ __attribute__((aligned(16))) T vt_lds[kPPStages * kTileElems];
-  __shared__ __attribute__((aligned(16))) T b_lds[kPPStages * kBiasSlot];
+  __shared__ __attribute__((aligned(16))) float b_lds[kPPStages * kBN];
   const PPSchedule& sc = L.s;
   const int64_t w = xcd_remap(blockIdx.x, gridDim.x);
-  zero_bias_tails(b_lds, kPPStages);  // ordered before any read by the segment's first barrier
   // Whole tasks first: consecutive work-groups (one XCD's, after the remap)
   // take consecutive tasks of a round, so they stream one head's K/V in step
   // and share it in that XCD's L2.  Then the stream-K range.  One call site
@@ -1067,14 +1032,13 @@ __global__ __launch_bounds__(64) void attn_f32_kernel(
 // Packs V of every (batch, head) into V^T tiles for the DMA kernel:
 // vt[bh][d][j'] = V[bh][key j][d] with j' = vt_pos(j) inside each 16-key group
 // (the key order of the P operand), zeros past n_key, npad = ntiles * 64
-// columns; and bias2[2j], bias2[2j+1] = hi, lo of bias[j] (0, 0
-// without a bias) for j < n_key, (-inf, 0) up to npad.  One block per
-// (64-key tile, bh).
+// columns; and kbias[j] = bias[j] as fp32 (0 without a bias) for j < n_key,
+// -inf up to npad.  One block per (64-key tile, bh).
 template <typename T>
 __global__ __launch_bounds__(256) void vt_pack_kernel(const T* __restrict__ v, int heads, int nk,
                                                       int ntiles, int npad, int64_t vsb, int64_t vsh,
                                                       int64_t vsn, const T* __restrict__ bias,
-                                                      T* __restrict__ vt, T* __restrict__ bias2) {
+                                                      T* __restrict__ vt, float* __restrict__ kbias) {
   typedef typename Mma<T>::op8 op8;
   constexpr int kRow = kD + 2;  // padded LDS row
   __shared__ T tile[kBN * kRow];
@@ -1110,10 +1074,7 @@ __global__ __launch_bounds__(256) void vt_pack_kernel(const T* __restrict__ v, i
   }
   if (bh == 0 && tid < kBN) {
     const int j = kt + tid;
-    const float bv = j < nk ? (bias ? to_f32(bias[j]) : 0.0f) : -__builtin_inff();
-    const T hi = static_cast<T>(bv);
-    bias2[2 * j] = hi;
-    bias2[2 * j + 1] = static_cast<T>(__builtin_isfinite(bv) ? bv - to_f32(hi) : 0.0f);
+    kbias[j] = j < nk ? (bias ? to_f32(bias[j]) : 0.0f) : -__builtin_inff();
   }
 }
 
@@ -1191,10 +1152,10 @@ PPPlan pp_plan(const Problem* pr, int count) {
   return plan;
 }
 
-// Workspace of the DMA path: per problem V^T and the bias pairs, then the
+// Workspace of the DMA path: per problem V^T and the fp32 key biases, then the
 // partial states (each part 256-byte aligned).
 struct AttnWorkspace {
-  size_t vt[2], bias2[2], partial, total;
+  size_t vt[2], kbias[2], partial, total;
 };
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 inline AttnWorkspace attn_workspace(const PPPlan& plan, const Problem* pr, size_t elem) {
@@ -1204,8 +1165,8 @@ inline AttnWorkspace attn_workspace(const PPPlan& plan, const Problem* pr, size_
     const int64_t npad = plan.ntiles[i] * kBN;
     w.vt[i] = at;
     at += align256(static_cast<size_t>(pr[i].batch * pr[i].heads) * kD * npad * elem);
-    w.bias2[i] = at;
-    at += align256(static_cast<size_t>(2 * npad) * elem);
+    w.kbias[i] = at;
+    at += align256(static_cast<size_t>(npad) * sizeof(float));
   }
   w.partial = at;
   w.total = at + (plan.s.units > 0 ? static_cast<size_t>(plan.s.groups) * 2 * kPartialFloats * sizeof(float) : 0);
@@ -1231,7 +1192,7 @@ AttnArgs<T> make_args(const Problem& pr, int64_t qblock) {
   a.osb = pr.os[0], a.osh = pr.os[1], a.osn = pr.os[2];
   a.c = 0.125f;
   a.vt = nullptr;
-  a.bias2 = nullptr;
+  a.kbias = nullptr;
   a.npad = a.ntiles * kBN;
   return a;
 }
@@ -1316,11 +1277,11 @@ int launch_pp(const Problem* pr, int count, void* workspace, size_t workspace_by
     AttnArgs<T>& a = L.p[i];
     a = make_args<T>(pr[i], kPPQBlock);
     a.vt = reinterpret_cast<T*>(base + ws.vt[i]);
-    a.bias2 = reinterpret_cast<T*>(base + ws.bias2[i]);
+    a.kbias = reinterpret_cast<float*>(base + ws.kbias[i]);
     hipLaunchKernelGGL((vt_pack_kernel<T>),
                        dim3(static_cast<unsigned>(a.ntiles), static_cast<unsigned>(pr[i].batch * pr[i].heads)),
                        dim3(256), 0, stream, a.v, a.heads, a.nk, a.ntiles, a.npad, a.vsb, a.vsh, a.vsn,
-                       a.bias, const_cast<T*>(a.vt), const_cast<T*>(a.bias2));
+                       a.bias, const_cast<T*>(a.vt), const_cast<float*>(a.kbias));
     const int status = check_launch("mass_bias_attention(pack)");
     if (status != VGO_OK) return status;
   }
