@@ -223,6 +223,20 @@ class Aggregator(nn.Module):
                 outputs.append(None)
         return outputs, self.patch_token_start
 
+    def _side_qkv(self, block, x: torch.Tensor) -> "_SideQkv | None":
+        """The side-stream projection of a FastVGGT block's qkv (see `_SideQkv`), or None
+        to project in the block: off the GPU, or while a graph is being captured before
+        the side stream exists (a stream is created outside capture only)."""
+        if not x.is_cuda:
+            return None
+        streams = self.__dict__.setdefault("_qkv_streams", {})
+        stream = streams.get(x.device)
+        if stream is None:
+            if torch.cuda.is_current_stream_capturing():
+                return None
+            stream = streams[x.device] = torch.cuda.Stream(device=x.device)
+        return _SideQkv(stream, block, x)
+
     def _run_inter_frame_attention_block(self, tokens, batch_size, num_frames, num_tokens,
                                          embed_dim, block_idx, patch_hw,
                                          reuse_input: bool = False) -> torch.Tensor:
@@ -313,10 +327,13 @@ class Aggregator(nn.Module):
                                                       else plan.original_tokens),
                         **plan.metadata})
                 else:
+                    side = self._side_qkv(block, attn_input)
                     plan = build_fastvggt_plan(
                         normalized if unit_rows is None else unit_rows,
                         merge_ratio=self.fastvggt_merge_ratio, protect_ratio=self.fastvggt_protect_ratio,
-                        mass_bias=self.fastvggt_mass_bias, prenormalized=unit_rows is not None, **layout)
+                        mass_bias=self.fastvggt_mass_bias, prenormalized=unit_rows is not None,
+                        after_match=None if side is None else side.launch, **layout)
+                    precomputed_qkv = None if side is None else side.join()
                     self.fastvggt_last_plan_stats.append({
                         "block_index": block_idx, "original_tokens": plan.original_tokens,
                         "kept_tokens": plan.kept_tokens,
@@ -333,6 +350,43 @@ class Aggregator(nn.Module):
                 finally:
                     plan.precomputed_qkv = None
         return tokens.view(batch_size, num_frames, num_tokens, embed_dim)
+
+
+class _SideQkv:
+    """A global block's qkv projection on a side stream.
+
+    `launch` (the FastVGGT builder's `after_match` hook) makes the side stream wait
+    for the current stream's work so far -- the norm1 rows and the matcher -- and
+    enqueues the projection there, so the GEMM runs beside the plan's short
+    rank-and-select and cluster kernels, which occupy few CUs, and never beside the
+    matcher, whose work-groups hold every CU.  `join` makes the current stream wait
+    for the projection and returns it (None if `launch` was not called: plans that
+    need no matching).  The projection is the same call the block makes itself, so
+    the outputs are unchanged.
+    """
+
+    def __init__(self, stream: torch.cuda.Stream, block: SelfAttentionBlock, x: torch.Tensor) -> None:
+        self.stream, self.block, self.x = stream, block, x
+        self.qkv = None
+        self.done = None
+
+    def launch(self) -> None:
+        ready = torch.cuda.Event()
+        ready.record(torch.cuda.current_stream(self.x.device))
+        with torch.cuda.stream(self.stream):
+            self.stream.wait_event(ready)
+            self.x.record_stream(self.stream)
+            self.qkv = self.block.attn.qkv(self.x)
+            self.done = torch.cuda.Event()
+            self.done.record(self.stream)
+
+    def join(self) -> torch.Tensor | None:
+        if self.qkv is None:
+            return None
+        main = torch.cuda.current_stream(self.x.device)
+        main.wait_event(self.done)
+        self.qkv.record_stream(main)
+        return self.qkv
 
 
 def _slice_expand_and_flatten(token_tensor: torch.Tensor, batch_size: int, num_frames: int) -> torch.Tensor:

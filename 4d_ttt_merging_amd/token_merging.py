@@ -25,6 +25,7 @@ import ctypes
 import functools
 import math
 from dataclasses import dataclass, field
+from typing import Callable
 
 import torch
 
@@ -494,6 +495,7 @@ def build_fastvggt_plan(
     match_chunk_size: int = FAST_MATCH_SOURCE_CHUNK,
     mass_bias: bool = False,
     prenormalized: bool = False,
+    after_match: Callable[[], None] | None = None,
 ) -> TokenPlan:
     """FastVGGT bipartite plan on Omega's interleaved token layout (reference :1044-1122).
 
@@ -508,6 +510,13 @@ def build_fastvggt_plan(
     `match_chunk_size` is accepted for signature compatibility; the HIP matcher
     streams the whole score matrix without materialising it.  With
     `mass_bias=True` the plan carries key_log_mass = log(cluster size).
+
+    `after_match` (not in the reference) is called once, right after the
+    matcher's kernels are enqueued on the current stream and before the
+    rank-and-select: a caller can start plan-independent work on another stream
+    there (the aggregator enqueues the block's qkv projection), which then runs
+    beside the plan's short selection and cluster kernels instead of after them
+    and never beside the matcher, whose work-groups hold every CU.
     """
     del match_chunk_size
     if not (0.0 <= merge_ratio <= 1.0 and 0.0 <= protect_ratio <= 1.0):
@@ -546,6 +555,8 @@ def build_fastvggt_plan(
             dst = _kernels.normalize_rows(x, destinations, 1e-12)
         _kernels.similarity_topk(src, dst, 1, src_rows=src_rows, index_dtype=torch.int32,
                                  out=(best[b].view(-1, 1), target[b].view(-1, 1)))
+    if after_match is not None:
+        after_match()
     keep = torch.empty((batch, total - removed), device=device, dtype=torch.int64)
     inverse = torch.empty((batch, total), device=device, dtype=torch.int64)
     flags = torch.empty((batch, sources.numel()), device=device, dtype=torch.uint8)
