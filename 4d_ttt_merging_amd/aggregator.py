@@ -275,6 +275,7 @@ class Aggregator(nn.Module):
             layout = dict(frames=num_frames, tokens_per_frame=num_tokens,
                           patch_token_start=self.patch_token_start, patch_hw=patch_hw)
             precomputed_qkv = None
+            side = None
             unit_rows = None if self.sparse_convex_enabled else block.norm1_unit_rows(tokens)
             if unit_rows is not None:
                 normalized = None
@@ -311,7 +312,8 @@ class Aggregator(nn.Module):
                                 normalized, threshold=self.sparse_convex_threshold,
                                 preserve_queries=preserve_queries,
                                 preserve_destination_keys=preserve_keys, **layout)
-                            precomputed_qkv = block.attn.qkv(attn_input)
+                            with profiling.span("global.qkv_projection"):
+                                precomputed_qkv = block.attn.qkv(attn_input)
                             plan = pending.result()
                         if reuse_plan:
                             self._sparse_convex_reuse_plan = plan
@@ -333,12 +335,16 @@ class Aggregator(nn.Module):
                         merge_ratio=self.fastvggt_merge_ratio, protect_ratio=self.fastvggt_protect_ratio,
                         mass_bias=self.fastvggt_mass_bias, prenormalized=unit_rows is not None,
                         after_match=None if side is None else side.launch, **layout)
-                    precomputed_qkv = None if side is None else side.join()
                     self.fastvggt_last_plan_stats.append({
                         "block_index": block_idx, "original_tokens": plan.original_tokens,
                         "kept_tokens": plan.kept_tokens,
                         "merged_tokens": plan.original_tokens - plan.kept_tokens,
                         "merge_ratio": 1.0 - plan.keep_ratio, **plan.metadata})
+            if side is not None:
+                # The wait for the side-stream projection: the part of the GEMM the plan's
+                # kernels did not cover.
+                with profiling.span("global.qkv_projection"):
+                    precomputed_qkv = side.join()
             if precomputed_qkv is None:
                 tokens = block.forward_compacted(tokens, plan, normalized=attn_input)
             else:

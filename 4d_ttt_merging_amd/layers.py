@@ -209,9 +209,10 @@ class SelfAttention(nn.Module):
     def _forward_merged(self, x: Tensor, attn_bias, rope, token_plan) -> Tensor:
         """The merged forward up to the output projection: attention.py:284-303 without
         the final `token_plan.restore`, which the caller applies (or fuses)."""
-        with profiling.span("global.qkv_projection"):
-            qkv = (token_plan.precomputed_qkv
-                   if getattr(token_plan, "precomputed_qkv", None) is not None else self.qkv(x))
+        qkv = getattr(token_plan, "precomputed_qkv", None)
+        if qkv is None:  # a precomputed projection was timed where its caller made it
+            with profiling.span("global.qkv_projection"):
+                qkv = self.qkv(x)
         attn_v = self.compute_attention(qkv=qkv, attn_bias=attn_bias, rope=rope, token_plan=token_plan)
         with profiling.span("global.output_projection"):
             x = self.proj_drop(self.proj(attn_v))
