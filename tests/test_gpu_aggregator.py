@@ -324,3 +324,27 @@ def test_aggregator_fastvggt_forward_replays_from_a_hip_graph(manifest, device):
         assert all(torch.equal(a, b) for a, b in zip(static, eager))
         step()
         torch.cuda.synchronize()
+
+
+@pytest.mark.gpu
+def test_aggregator_side_stream_qkv_matches_in_block_projection(manifest, device, monkeypatch):
+    """FastVGGT blocks project qkv on a side stream once the matcher is enqueued
+    (`build_fastvggt_plan(after_match=...)`); the outputs equal, bit for bit, those of
+    the same forward with the projection made inside the block."""
+    print("[aggregator] side-stream qkv projection", flush=True)
+    agg = import_package("aggregator")
+    model, images = _model(manifest, device)
+    _configure(model, "fv")
+    model.set_fastvggt(True, merge_ratio=0.5, protect_ratio=0.0, mass_bias=True)
+
+    def step():
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            return [o for o in model(images)[0] if o is not None]
+
+    side = step()
+    assert model.__dict__.get("_qkv_streams"), "the side stream was not used"
+    monkeypatch.setattr(agg.Aggregator, "_side_qkv", lambda self, block, x: None)
+    inline = step()
+    torch.cuda.synchronize()
+    assert len(side) == len(inline) > 0
+    assert all(torch.equal(a, b) for a, b in zip(side, inline))
