@@ -158,18 +158,18 @@ def _pair(vgo, main, special):
 @pytest.mark.parametrize("shapes", [
     ((1, 16, 1044, 522), (1, 16, 20, 1044)),     # C1: merged pass + 4 frames x 5 specials
     ((1, 2, 100, 20000), (1, 2, 7, 3000)),       # both problems cut over many work-groups
+    ((1, 2, 64, 52968), (1, 1, 5, 100)),         # C5's key count (fp32: 1e-5 at 52,968 keys)
     ((2, 3, 700, 1333), (1, 3, 513, 2100)),      # different batch; special tasks > 512 queries
     ((1, 1, 1, 1), (1, 1, 1, 65)),               # single rows
 ])
 def test_pair_launch_matches_oracle(vgo, device, dtype, shapes):
     """Merged attention and the dense special-query pass in one launch."""
     (b0, h0, nq0, nk0), (b1, h1, nq1, nk1) = shapes
-    # fp32: each output averages nk unit-variance values to ~1/sqrt(nk) of their
-    # scale, so the fp32 rounding of the running sums, which grows as sqrt(nk)
-    # relative to that scale, sets the error (1.3e-5 measured at 20,000 keys).
-    # The bar is 1e-5 up to 4,096 keys and grows as sqrt(nk / 4,096) beyond.
-    rtol0 = 1e-5 * max(1.0, (nk0 / 4096) ** 0.5) if dtype == torch.float32 else None
-    print(f"[attn pair] dtype={dtype} shapes={shapes} rtol_main={rtol0}", flush=True)
+    # fp32: each output averages nk unit-variance values to ~1/sqrt(nk) of their scale,
+    # so the rounding of the running sums sets the error; the kernel sums 32 keys at a
+    # time before adding them to the totals, which keeps it under the 1e-5 bar at
+    # 20,000 keys (1.3e-5 with one running sum).
+    print(f"[attn pair] dtype={dtype} shapes={shapes}", flush=True)
     std = 1.0 if dtype == torch.float32 else 0.125
     q, k, v, mass = _inputs(7 + nq0 + nk1, b0, h0, nq0, nk0, dtype, std=std)
     sq, sk, sv, _ = _inputs(9 + nq1, b1, h1, nq1, nk1, dtype, std=std)
@@ -178,7 +178,7 @@ def test_pair_launch_matches_oracle(vgo, device, dtype, shapes):
     special = (sq.to(device), sk.to(device), sv.to(device))
     out0, out1 = _pair(vgo, main, special)
     torch.cuda.synchronize()
-    err = assert_close(out0, oracle.mass_bias_attention(q, k, v, bias.float()), dtype, rtol=rtol0,
+    err = assert_close(out0, oracle.mass_bias_attention(q, k, v, bias.float()), dtype,
                        what=f"pair main {shapes}")
     print(f"[attn pair] main error {err:.3e}", flush=True)
     ref1 = oracle.mass_bias_attention(sq, sk, sv, torch.zeros(nk1))
