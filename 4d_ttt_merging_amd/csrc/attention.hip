@@ -756,6 +756,31 @@ __device__ __forceinline__ void attn_pp_segment(const AttnArgs<T>& a, T* k_lds, 
       for (int t = 0; t < 4; ++t) pin_out(p[qb][t]);
   };
 
+  // A wave whose 64 queries all lie past the problem's end (the last task of
+  // a problem whose query count is not a multiple of 512, e.g. the special
+  // queries' 160) computes nothing: it issues its share of the DMAs (group 0)
+  // and meets the same 2 n + 3 barriers, and its SIMD's other wave runs its
+  // phases alone.  Its rows are never stored or merged.
+  if (qw0 >= a.nq) {
+    const int n = tile1 - tile0;
+    if (group == 0) {
+      issue(tile0);
+      issue(tile0 + 1);
+      issue(tile0 + 2);
+      ring_barrier<2 * kPPDmaPerTile>();
+      ring_barrier<2 * kPPDmaPerTile>();
+      for (int tile = tile0; tile < tile1; ++tile) {
+        ring_barrier_reads_in_flight<kPPDmaPerTile>();
+        issue(tile + 3);
+        ring_barrier<2 * kPPDmaPerTile>();
+      }
+      ring_barrier<0>();
+    } else {
+      for (int i = 0; i < 2 * n + 3; ++i) ring_barrier<-1>();
+    }
+    return;
+  }
+
   if (group == 0) {
     issue(tile0);
     issue(tile0 + 1);
