@@ -228,6 +228,23 @@ def c3_attention(vgo, device, steps):
             "frac": flops / sec / 1e12 / PEAK_BF16_TFLOPS, "torch_sdpa_ms": sdpa * 1e3}
 
 
+def vendor_flash_attention(device, n):
+    """torch's flash SDPA kernel on the C4 attention shape (16 heads, n x n, head_dim 64, bf16),
+    with no mask, since it takes no per-key bias: the stack's own attention kernel, timed beside
+    the roofline's kernel on the same inputs' shape."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    g = torch.Generator().manual_seed(6)
+    q, k, v = (torch.randn(1, HEADS, n, 64, generator=g).bfloat16().to(device) for _ in range(3))
+    try:
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+            sec = event_time(lambda: F.scaled_dot_product_attention(q, k, v), 4, 2)
+    except RuntimeError as exc:  # backend not built into this torch
+        return {"backend": "torch SDPA flash", "unavailable": str(exc)[:200]}
+    flops = 4 * HEADS * n * n * 64
+    return {"backend": "torch SDPA flash, no bias", "ms": round(sec * 1e3, 4),
+            "frac": round(flops / sec / 1e12 / PEAK_BF16_TFLOPS, 4)}
+
+
 def _global_block_step(vgo, prof, block, x, layout, ratio):
     """One merged global block as the aggregator's global arm runs it
     (aggregator.py:1002-1052, 1215): fused norm1 + unit rows, FastVGGT plan with
@@ -1042,7 +1059,8 @@ def main() -> int:
                      "at_measured_clock": clock_adjusted(attn_flops / (attn_ms / 1e3) / 1e12),
                      "with_pack_and_merge": {
                          "ms": round(label_ms, 4),
-                         "frac": round(attn_flops / (label_ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4)}},
+                         "frac": round(attn_flops / (label_ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4)},
+                     "vendor_flash_same_shape": vendor_flash_attention(device, kept)},
         "gemm_selection": "TunableOp table 4d_ttt_merging_amd/tuning/gemm_gfx950.csv" if tuned_gemms
                           else "hipBLASLt default heuristic",
         "global_block_ms": round(block_ms, 3),
