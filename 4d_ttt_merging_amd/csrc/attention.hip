@@ -704,21 +704,33 @@ __device__ __forceinline__ void attn_pp_segment(const AttnArgs<T>& a, T* k_lds, 
   const int dc = lane & 7;
   const int row0 = 16 * wave + dr;
   const int lc0 = dc ^ swz(row0), lc1 = dc ^ swz(row0 + 8);
-  // Byte offsets from the (scalar) bases; they fit in 32 bits (checked on the host).
+  // Byte offsets of the lane's rows from the tile's first key; the tile's base
+  // moves in scalar registers, so a full tile's DMAs take no VALU work (which
+  // would run between the MFMAs, waiting for the VALU issue that the other
+  // group's softmax holds).  The offsets fit in 32 bits (checked on the host).
+  const uint32_t k_off0 = (static_cast<uint32_t>(row0) * ksn + lc0 * 8) * sizeof(T);
+  const uint32_t k_off1 = (static_cast<uint32_t>(row0 + 8) * ksn + lc1 * 8) * sizeof(T);
   const uint32_t v_off0 = (static_cast<uint32_t>(row0) * a.npad + lc0 * 8) * sizeof(T);
   const uint32_t v_off1 = (static_cast<uint32_t>(row0 + 8) * a.npad + lc1 * 8) * sizeof(T);
+  const uint32_t b_off = lane * sizeof(float);
   auto issue = [&](int tile) {
     const int stage = tile & (kPPStages - 1);
     const int kt = min(tile, a.ntiles - 1) * kBN;
     T* kst = k_lds + stage * kTileElems + 16 * wave * kD;
     T* vst = vt_lds + stage * kTileElems + 16 * wave * kD;
-    lds_dma16(kb_ptr, (static_cast<uint32_t>(min(kt + row0, last_key) * ksn) + lc0 * 8) * sizeof(T),
-              lds_offset(kst));
-    lds_dma16(kb_ptr, (static_cast<uint32_t>(min(kt + row0 + 8, last_key) * ksn) + lc1 * 8) * sizeof(T),
-              lds_offset(kst + 8 * kD));
-    lds_dma16(vt_head, v_off0 + kt * sizeof(T), lds_offset(vst));
-    lds_dma16(vt_head, v_off1 + kt * sizeof(T), lds_offset(vst + 8 * kD));
-    lds_dma4(a.kbias, (lane + kt) * sizeof(float), lds_offset(b_lds + stage * kBN));
+    if (kt + kBN <= a.nk) {
+      const T* kbase = kb_ptr + static_cast<int64_t>(kt) * ksn;
+      lds_dma16(kbase, k_off0, lds_offset(kst));
+      lds_dma16(kbase, k_off1, lds_offset(kst + 8 * kD));
+    } else {  // the last tile: rows past n_key read the last key (their bias is -inf)
+      lds_dma16(kb_ptr, (static_cast<uint32_t>(min(kt + row0, last_key) * ksn) + lc0 * 8) * sizeof(T),
+                lds_offset(kst));
+      lds_dma16(kb_ptr, (static_cast<uint32_t>(min(kt + row0 + 8, last_key) * ksn) + lc1 * 8) * sizeof(T),
+                lds_offset(kst + 8 * kD));
+    }
+    lds_dma16(vt_head + kt, v_off0, lds_offset(vst));
+    lds_dma16(vt_head + kt, v_off1, lds_offset(vst + 8 * kD));
+    lds_dma4(a.kbias + kt, b_off, lds_offset(b_lds + stage * kBN));
   };
   auto kl = [&](int tile) { return k_lds + (tile & (kPPStages - 1)) * kTileElems; };
   auto vl = [&](int tile) { return vt_lds + (tile & (kPPStages - 1)) * kTileElems; };
