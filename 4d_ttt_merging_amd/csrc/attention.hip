@@ -174,21 +174,22 @@ __host__ __device__ __forceinline__ int64_t sk_owner(int64_t u, int64_t units, i
 // results are the same bit for bit).
 constexpr float kLazyLimit = 32768.0f;
 
-// Per-wave state of the bf16/f16 kernels: 64 queries as two 32-column MFMA
-// blocks -- their scaled Q operands, the online-softmax state and the O^T
+// Per-wave state of the bf16/f16 kernels: QB 32-column MFMA blocks of queries
+// (two, 64 queries; one where the wave's second block would hold only rows past
+// n_query) -- their scaled Q operands, the online-softmax state and the O^T
 // accumulators -- and the tile-level steps on LDS-resident K / V^T / bias.
-template <typename T>
+template <typename T, int QB = kQB>
 struct WaveAttn {
   typedef typename Mma<T>::op8 op8;
   typedef typename Mma<T>::op2 op2;
   typedef typename Mma<T>::op4 op4;
 
-  op8 qreg[kQB][4];  // Q' = Q / 8 (exact), B operands
+  op8 qreg[QB][4];  // Q' = Q / 8 (exact), B operands
   // Reference max per query (a T value; -inf until a finite logit is seen);
   // the running sum and O are relative to e^mref.  nm = -mref log2(e), the
   // offset of the exp2 argument (+inf while mref = -inf).
-  float mref[kQB], lsum[kQB], nm[kQB];
-  f32x16 o[kQB][2];
+  float mref[QB], lsum[QB], nm[QB];
+  f32x16 o[QB][2];
   int off[4];  // LDS element offsets of logical chunk pair t of row l32
   int l32, hh;
 
@@ -199,7 +200,7 @@ struct WaveAttn {
     l32 = lane & 31;
     hh = lane >> 5;
 #pragma unroll
-    for (int qb = 0; qb < kQB; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
       const int row = min(qw0 + qb * 32 + l32, nq - 1);
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
@@ -213,7 +214,7 @@ struct WaveAttn {
 #pragma unroll
     for (int t = 0; t < 4; ++t) off[t] = l32 * kD + (((2 * t + hh) ^ s0) << 3);
 #pragma unroll
-    for (int qb = 0; qb < kQB; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
       mref[qb] = -__builtin_inff();
       nm[qb] = exp_offset(mref[qb]);
       lsum[qb] = 0.0f;
@@ -270,23 +271,23 @@ struct WaveAttn {
   // S^T = K Q'^T + bias for the tile's two 32-key sub-tiles (the MFMAs start
   // from the key biases); sub-tile 0 then leaves in the exp2 domain,
   // S log2(e) - mref log2(e), as pv_scores leaves it.
-  __device__ __forceinline__ void scores(const KOps& ops, const float* bl, f32x16 (&s)[kQB][2]) const {
+  __device__ __forceinline__ void scores(const KOps& ops, const float* bl, f32x16 (&s)[QB][2]) const {
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
       const f32x16 c = key_bias(bl, sub);
 #pragma unroll
-      for (int qb = 0; qb < kQB; ++qb) s[qb][sub] = Mma<T>::mma(ops.k[sub][0], qreg[qb][0], c);
+      for (int qb = 0; qb < QB; ++qb) s[qb][sub] = Mma<T>::mma(ops.k[sub][0], qreg[qb][0], c);
 #pragma unroll
       for (int t = 1; t < 4; ++t)
 #pragma unroll
-        for (int qb = 0; qb < kQB; ++qb) s[qb][sub] = Mma<T>::mma(ops.k[sub][t], qreg[qb][t], s[qb][sub]);
+        for (int qb = 0; qb < QB; ++qb) s[qb][sub] = Mma<T>::mma(ops.k[sub][t], qreg[qb][t], s[qb][sub]);
     }
 #pragma unroll
-    for (int qb = 0; qb < kQB; ++qb)
+    for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[qb][0][r] = fmaf(s[qb][0][r], kLog2e, nm[qb]);
   }
-  __device__ __forceinline__ void scores(const T* kl, const float* bl, f32x16 (&s)[kQB][2]) const {
+  __device__ __forceinline__ void scores(const T* kl, const float* bl, f32x16 (&s)[QB][2]) const {
     KOps ops;
     load_k(kl, ops);
     __builtin_amdgcn_sched_barrier(0);
@@ -339,21 +340,24 @@ struct WaveAttn {
   // O and the sum are rescaled, and P is recomputed.  That path works one
   // 32-key sub-tile at a time (logits computed twice) to stay within the
   // registers the fast path leaves free.
-  __device__ __forceinline__ void softmax(const f32x16 (&s)[kQB][2], const T* kl, const float* bl,
-                                          op8 (&p)[kQB][4]) {
-    float part[kQB];
+  __device__ __forceinline__ void softmax(const f32x16 (&s)[QB][2], const T* kl, const float* bl,
+                                          op8 (&p)[QB][4]) {
+    float part[QB];
 #pragma unroll
-    for (int qb = 0; qb < kQB; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
       float acc[4];
       exp_pack<true>(s[qb][0], 0, 0.0f, p[qb], acc);
       exp_pack(s[qb][1], 1, nm[qb], p[qb], acc);
       part[qb] = sum4(acc);
     }
-    if (__builtin_expect(__ballot(!(part[0] <= kLazyLimit) | !(part[1] <= kLazyLimit)) != 0, 0)) {
+    bool over = false;
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) over |= !(part[qb] <= kLazyLimit);
+    if (__builtin_expect(__ballot(over) != 0, 0)) {
       // Reload K here rather than keep the score operands alive.
       asm volatile("" ::: "memory");
 #pragma unroll
-      for (int qb = 0; qb < kQB; ++qb) {
+      for (int qb = 0; qb < QB; ++qb) {
         float mx = -__builtin_inff();
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub) {
@@ -383,19 +387,19 @@ struct WaveAttn {
       }
     }
 #pragma unroll
-    for (int qb = 0; qb < kQB; ++qb) lsum[qb] += part[qb];
+    for (int qb = 0; qb < QB; ++qb) lsum[qb] += part[qb];
   }
 
   // O^T += V^T P^T.
-  __device__ __forceinline__ void pv(const VOps& ops, const op8 (&p)[kQB][4]) {
+  __device__ __forceinline__ void pv(const VOps& ops, const op8 (&p)[QB][4]) {
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-        for (int qb = 0; qb < kQB; ++qb) o[qb][dt] = Mma<T>::mma(ops.v[t][dt], p[qb][t], o[qb][dt]);
+        for (int qb = 0; qb < QB; ++qb) o[qb][dt] = Mma<T>::mma(ops.v[t][dt], p[qb][t], o[qb][dt]);
   }
-  __device__ __forceinline__ void pv(const T* vl, const op8 (&p)[kQB][4]) {
+  __device__ __forceinline__ void pv(const T* vl, const op8 (&p)[QB][4]) {
     VOps ops;
     load_v(vl, ops);
     __builtin_amdgcn_sched_barrier(0);
@@ -406,22 +410,22 @@ struct WaveAttn {
   // K reads go out in two halves (one per 32-key sub-tile), each while MFMAs
   // of the previous step run: their latency is hidden and at most about half
   // of the operands are held at once.
-  __device__ __forceinline__ void pv_scores(const T* vl, const op8 (&p)[kQB][4], const T* kl,
-                                            const float* bl, f32x16 (&s)[kQB][2]) {
+  __device__ __forceinline__ void pv_scores(const T* vl, const op8 (&p)[QB][4], const T* kl,
+                                            const float* bl, f32x16 (&s)[QB][2]) {
     VOps vops;
     load_v(vl, vops);
     __builtin_amdgcn_sched_barrier(0);
     pv_scores(vops, p, kl, bl, s);
   }
   // The same with the V^T operands already requested (vops).
-  __device__ __forceinline__ void pv_scores(const VOps& vops, const op8 (&p)[kQB][4], const T* kl,
-                                            const float* bl, f32x16 (&s)[kQB][2]) {
+  __device__ __forceinline__ void pv_scores(const VOps& vops, const op8 (&p)[QB][4], const T* kl,
+                                            const float* bl, f32x16 (&s)[QB][2]) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-        for (int qb = 0; qb < kQB; ++qb) o[qb][dt] = Mma<T>::mma(vops.v[t][dt], p[qb][t], o[qb][dt]);
+        for (int qb = 0; qb < QB; ++qb) o[qb][dt] = Mma<T>::mma(vops.v[t][dt], p[qb][t], o[qb][dt]);
     __builtin_amdgcn_sched_barrier(0);
     op8 ka[4], kb[4];
 #pragma unroll
@@ -436,7 +440,7 @@ struct WaveAttn {
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-      for (int qb = 0; qb < kQB; ++qb) o[qb][dt] = Mma<T>::mma(vops.v[2][dt], p[qb][2], o[qb][dt]);
+      for (int qb = 0; qb < QB; ++qb) o[qb][dt] = Mma<T>::mma(vops.v[2][dt], p[qb][2], o[qb][dt]);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 0; t < 4; ++t) kb[t] = tile_op(kl, 1, t);
@@ -445,24 +449,24 @@ struct WaveAttn {
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-      for (int qb = 0; qb < kQB; ++qb) o[qb][dt] = Mma<T>::mma(vops.v[3][dt], p[qb][3], o[qb][dt]);
+      for (int qb = 0; qb < QB; ++qb) o[qb][dt] = Mma<T>::mma(vops.v[3][dt], p[qb][3], o[qb][dt]);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int qb = 0; qb < kQB; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
       s[qb][0] = Mma<T>::mma(ka[0], qreg[qb][0], ca);
 #pragma unroll
       for (int t = 1; t < 4; ++t) s[qb][0] = Mma<T>::mma(ka[t], qreg[qb][t], s[qb][0]);
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int qb = 0; qb < kQB; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
       s[qb][1] = Mma<T>::mma(kb[0], qreg[qb][0], cb);
 #pragma unroll
       for (int t = 1; t < 4; ++t) s[qb][1] = Mma<T>::mma(kb[t], qreg[qb][t], s[qb][1]);
     }
     // Sub-tile 0's scores into the exp2 domain under sub-tile 1's MFMAs.
 #pragma unroll
-    for (int qb = 0; qb < kQB; ++qb)
+    for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[qb][0][r] = fmaf(s[qb][0][r], kLog2e, nm[qb]);
 #pragma unroll
@@ -475,7 +479,7 @@ struct WaveAttn {
   // Normalised output rows qw0.. (rows past n_query are not stored).
   __device__ __forceinline__ void store_out(T* ob_ptr, int64_t osn, int qw0, int nq) const {
 #pragma unroll
-    for (int qb = 0; qb < kQB; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
       const float ltot = half_sum(lsum[qb]);
       const int row = qw0 + qb * 32 + l32;
       if (row < nq) {
@@ -497,7 +501,7 @@ struct WaveAttn {
   // then the sum of every query); this wave's queries start at ql0.
   __device__ __forceinline__ void store_partial(float* partial, int qblock, int ql0) const {
 #pragma unroll
-    for (int qb = 0; qb < kQB; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
       const int ql = ql0 + qb * 32 + l32;
       float* po = partial + ql * kD;
 #pragma unroll
@@ -537,13 +541,12 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attn_reg_kernel(AttnArgs<T> a)
   const int h = bh - b * a.heads;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // Wave-uniform (scalar): the loop variants below hold barriers, so the
+  // branch between them must be a plain branch that each wave takes one way.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qw0 = qblk * kQBlock + wave * kQPerWave;
   const T* kb_ptr = a.k + b * a.ksb + h * a.ksh;
   const T* vb_ptr = a.v + b * a.vsb + h * a.vsh;
-
-  WaveAttn<T> w;
-  w.init(a.q + b * a.qsb + h * a.qsh, a.qsn, qw0, a.nq, a.c);
 
   // K: rows st and st+32, chunk sc.  V: keys 2st, 2st+1, dims 8sc..8sc+7.
   // Row offsets fit in 32 bits (checked on the host).
@@ -585,29 +588,42 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attn_reg_kernel(AttnArgs<T> a)
     b_lds[buf * kBN + lane] = valid ? (a.bias ? to_f32(pb) : 0.0f) : -__builtin_inff();
   };
 
-  stage_load(0);
-  stage_store(0, 0);
-  __syncthreads();
-  for (int tile = 0; tile < a.ntiles; ++tile) {
-    const int buf = tile & 1;
-    const bool more = tile + 1 < a.ntiles;
-    if (more) stage_load(tile + 1);
-    const T* kl = k_lds + buf * kTileElems;
-    const float* bl = b_lds + buf * kBN;
-    // A wave whose 64 queries all lie past n_query (the short last block of a
-    // problem) only stages tiles and meets the barriers; its SIMD is then free
-    // for the other work-group resident on the CU.
-    if (qw0 < a.nq) {
-      f32x16 s[kQB][2];
-      w.scores(kl, bl, s);
-      op8 p[kQB][4];
-      w.softmax(s, kl, bl, p);
-      w.pv(vt_lds + buf * kTileElems, p);
-    }
-    if (more) stage_store(tile + 1, buf ^ 1);
+  // The tile loop with qbs::value query blocks per wave; every variant meets
+  // the same ntiles + 1 barriers.
+  auto run = [&](auto qbs) {
+    constexpr int QB = decltype(qbs)::value;
+    WaveAttn<T, QB> w;
+    w.init(a.q + b * a.qsb + h * a.qsh, a.qsn, qw0, a.nq, a.c);
+    stage_load(0);
+    stage_store(0, 0);
     __syncthreads();
-  }
-  w.store_out(a.out + b * a.osb + h * a.osh, a.osn, qw0, a.nq);
+    for (int tile = 0; tile < a.ntiles; ++tile) {
+      const int buf = tile & 1;
+      const bool more = tile + 1 < a.ntiles;
+      if (more) stage_load(tile + 1);
+      const T* kl = k_lds + buf * kTileElems;
+      const float* bl = b_lds + buf * kBN;
+      // A wave whose 64 queries all lie past n_query (the short last block of
+      // a problem) only stages tiles and meets the barriers; its SIMD is then
+      // free for the other work-group resident on the CU.
+      if (qw0 < a.nq) {
+        f32x16 s[QB][2];
+        w.scores(kl, bl, s);
+        op8 p[QB][4];
+        w.softmax(s, kl, bl, p);
+        w.pv(vt_lds + buf * kTileElems, p);
+      }
+      if (more) stage_store(tile + 1, buf ^ 1);
+      __syncthreads();
+    }
+    w.store_out(a.out + b * a.osb + h * a.osh, a.osn, qw0, a.nq);
+  };
+  // A wave whose second 32-query block lies wholly past n_query (the 5 queries
+  // past 4 x 256 of a frame's 1,029) computes its first block only.
+  if (qw0 < a.nq && qw0 + 32 >= a.nq)
+    run(std::integral_constant<int, 1>{});
+  else
+    run(std::integral_constant<int, kQB>{});
 }
 
 // ------------------------------------------------- ping-pong kernel -------

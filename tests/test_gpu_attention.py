@@ -260,9 +260,11 @@ def test_wide_logits_match_oracle(vgo, device, dtype, std, nk):
     q and k) and at 2-3x unit scale (logits of tens in the exp2 domain, which take
     the lazy softmax's rescaling path on many tiles); both kernels (1,500 keys:
     register-staged, 3,000: ping-pong) stay within the tolerance of the oracle.
-    The measured error is printed beside the bar."""
+    657 queries leave a wave with 17 (past 2 x 256 + 128), which the
+    register-staged kernel runs as one 32-query block.  The measured error is
+    printed beside the bar."""
     print(f"[attn] wide logits dtype={dtype} std={std} nk={nk}", flush=True)
-    q, k, v, mass = _inputs(int(std * 10) + nk, 1, 4, 700, nk, dtype, mass_max=16, std=std)
+    q, k, v, mass = _inputs(int(std * 10) + nk, 1, 4, 657, nk, dtype, mass_max=16, std=std)
     out = vgo.mass_bias_attention(q.to(device), k.to(device), v.to(device), mass.log().to(device))
     torch.cuda.synchronize()
     ref = oracle.mass_bias_attention(q, k, v, mass.log())
