@@ -271,6 +271,9 @@ struct WaveAttn {
   // S^T = K Q'^T + bias for the tile's two 32-key sub-tiles (the MFMAs start
   // from the key biases); sub-tile 0 then leaves in the exp2 domain,
   // S log2(e) - mref log2(e), as pv_scores leaves it.
+  // kRaw: both sub-tiles stay raw logits (a segment's first tile, whose
+  // softmax_first takes their maximum before any offset exists).
+  template <bool kRaw = false>
   __device__ __forceinline__ void scores(const KOps& ops, const float* bl, f32x16 (&s)[QB][2]) const {
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
@@ -282,16 +285,19 @@ struct WaveAttn {
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) s[qb][sub] = Mma<T>::mma(ops.k[sub][t], qreg[qb][t], s[qb][sub]);
     }
+    if constexpr (!kRaw) {
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb)
+      for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[qb][0][r] = fmaf(s[qb][0][r], kLog2e, nm[qb]);
+        for (int r = 0; r < 16; ++r) s[qb][0][r] = fmaf(s[qb][0][r], kLog2e, nm[qb]);
+    }
   }
+  template <bool kRaw = false>
   __device__ __forceinline__ void scores(const T* kl, const float* bl, f32x16 (&s)[QB][2]) const {
     KOps ops;
     load_k(kl, ops);
     __builtin_amdgcn_sched_barrier(0);
-    scores(ops, bl, s);
+    scores<kRaw>(ops, bl, s);
   }
 
   // P = e^(x - m) = exp2(x log2(e) + nmv) with nmv = -m log2(e), for one
@@ -388,6 +394,30 @@ struct WaveAttn {
     }
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) lsum[qb] += part[qb];
+  }
+
+  // The softmax of a segment's first tile from its raw logits (scores<true>):
+  // the reference max moves from -inf to the T value nearest the tile's
+  // maximum and P is computed once with that offset -- the values the
+  // rescaling path would give, without recomputing the logits from K.  The
+  // state is the one init leaves (O and the sums zero), so nothing rescales.
+  __device__ __forceinline__ void softmax_first(const f32x16 (&s)[QB][2], op8 (&p)[QB][4]) {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      float mx = -__builtin_inff();
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[qb][sub][r]);
+      mref[qb] = to_f32(static_cast<T>(fmaxf(mref[qb], half_max(mx))));
+      nm[qb] = exp_offset(mref[qb]);
+      // No finite logit yet: every P is 0 (x = -inf).
+      const float nmv = mref[qb] == -__builtin_inff() ? 0.0f : nm[qb];
+      float acc[4];
+      exp_pack(s[qb][0], 0, nmv, p[qb], acc);
+      exp_pack(s[qb][1], 1, nmv, p[qb], acc);
+      lsum[qb] += sum4(acc);
+    }
   }
 
   // O^T += V^T P^T.
@@ -597,7 +627,8 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attn_reg_kernel(AttnArgs<T> a)
     stage_load(0);
     stage_store(0, 0);
     __syncthreads();
-    for (int tile = 0; tile < a.ntiles; ++tile) {
+    // Tile `tile` (first: tile 0, whose softmax starts from its raw logits).
+    auto step = [&](auto first, int tile) {
       const int buf = tile & 1;
       const bool more = tile + 1 < a.ntiles;
       if (more) stage_load(tile + 1);
@@ -608,14 +639,21 @@ __global__ __launch_bounds__(kWaves * 64, 2) void attn_reg_kernel(AttnArgs<T> a)
       // free for the other work-group resident on the CU.
       if (qw0 < a.nq) {
         f32x16 s[QB][2];
-        w.scores(kl, bl, s);
         op8 p[QB][4];
-        w.softmax(s, kl, bl, p);
+        if constexpr (decltype(first)::value) {
+          w.template scores<true>(kl, bl, s);
+          w.softmax_first(s, p);
+        } else {
+          w.scores(kl, bl, s);
+          w.softmax(s, kl, bl, p);
+        }
         w.pv(vt_lds + buf * kTileElems, p);
       }
       if (more) stage_store(tile + 1, buf ^ 1);
       __syncthreads();
-    }
+    };
+    step(std::true_type{}, 0);
+    for (int tile = 1; tile < a.ntiles; ++tile) step(std::false_type{}, tile);
     w.store_out(a.out + b * a.osb + h * a.osh, a.osn, qw0, a.nq);
   };
   // A wave whose second 32-query block lies wholly past n_query (the 5 queries
