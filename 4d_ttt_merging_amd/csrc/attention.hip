@@ -271,8 +271,8 @@ struct WaveAttn {
   // S^T = K Q'^T + bias for the tile's two 32-key sub-tiles (the MFMAs start
   // from the key biases); sub-tile 0 then leaves in the exp2 domain,
   // S log2(e) - mref log2(e), as pv_scores leaves it.
-  // kRaw: both sub-tiles stay raw logits (a segment's first tile, whose
-  // softmax_first takes their maximum before any offset exists).
+  // kRaw: both sub-tiles stay raw logits (tile 0 of a register-staged task,
+  // whose softmax_first takes their maximum before any offset exists).
   template <bool kRaw = false>
   __device__ __forceinline__ void scores(const KOps& ops, const float* bl, f32x16 (&s)[QB][2]) const {
 #pragma unroll
@@ -396,7 +396,7 @@ struct WaveAttn {
     for (int qb = 0; qb < QB; ++qb) lsum[qb] += part[qb];
   }
 
-  // The softmax of a segment's first tile from its raw logits (scores<true>):
+  // The softmax of a task's first tile from its raw logits (scores<true>):
   // the reference max moves from -inf to the T value nearest the tile's
   // maximum and P is computed once with that offset -- the values the
   // rescaling path would give, without recomputing the logits from K.  The
