@@ -1107,13 +1107,16 @@ __global__ __launch_bounds__(64) void attn_f32_kernel(
         mx = fmaxf(mx, logit[j]);
       }
       const float mnew = fmaxf(m, mx);
-      const float corr = exp2f(m - mnew);
+      // No finite logit yet (every key so far of mass 0): every P is 0 and the
+      // sums stay 0, where -inf - -inf would make them NaN.
+      const float base = mnew == -__builtin_inff() ? 0.0f : mnew;
+      const float corr = exp2f(m - base);
       float lc = 0.0f, accc[kD];
 #pragma unroll
       for (int d = 0; d < kD; ++d) accc[d] = 0.0f;
 #pragma unroll
       for (int j = 0; j < kF32Chunk; ++j) {
-        const float p = exp2f(logit[j] - mnew);
+        const float p = exp2f(logit[j] - base);
         lc += p;
 #pragma unroll
         for (int d = 0; d < kD; ++d) accc[d] = fmaf(p, v_lds[j0 + j][d], accc[d]);

@@ -293,3 +293,26 @@ def test_c4_unit_scale_rows_match_oracle(vgo, device, dtype):
     err = assert_close(out[:, :, rows.to(device)].cpu(), ref, dtype, what=f"C4 unit-scale rows {dtype}")
     print(f"[attn] C4 unit-scale rows dtype={dtype}: rel err {err:.3e} over {rows.numel()} rows x 16 heads "
           f"(bar {RTOL[dtype]:.0e})", flush=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("nk", [1029, 3000])
+def test_zero_mass_leading_keys_match_oracle(vgo, device, dtype, nk):
+    """Keys of mass 0 (log-mass bias -inf) take no weight.  With the first 80 keys
+    and a scattered tenth of the rest at mass 0, the first key tile of every task
+    holds no finite logit: the register-staged kernel (1,029 keys) starts its
+    first-tile softmax with the reference max still at -inf, the ping-pong kernel
+    (3,000 keys) its rescaling path, and both must leave those keys out."""
+    print(f"[attn] zero-mass leading keys dtype={dtype} nk={nk}", flush=True)
+    q, k, v, mass = _inputs(97 + nk, 1, 3, 657, nk, dtype, mass_max=8, std=1.0 if dtype == torch.float32 else 0.5)
+    g = torch.Generator().manual_seed(98)
+    mass[:80] = 0.0
+    mass[torch.randperm(nk, generator=g)[: nk // 10]] = 0.0
+    bias = mass.log()  # -inf where the mass is 0
+    out = vgo.mass_bias_attention(q.to(device), k.to(device), v.to(device), bias.to(device))
+    torch.cuda.synchronize()
+    ref = oracle.mass_bias_attention(q, k, v, bias)
+    assert torch.isfinite(out).all()
+    err = assert_close(out.cpu(), ref, dtype, what=f"zero-mass nk={nk}")
+    print(f"[attn] zero-mass leading keys dtype={dtype} nk={nk}: rel err {err:.3e} (bar {RTOL[dtype]:.0e})",
+          flush=True)
