@@ -25,6 +25,7 @@ SHAPES = [
     (1, 16, 1044, 522),  # C1 shape (S=4, 16x16 patches + 5 specials, ratio 0.5)
     (2, 3, 300, 257),    # batch > 1, tile remainders on both axes
     (1, 4, 129, 64),     # exactly one key tile, query remainder of 1
+    (1, 2, 1, 2600),     # ping-pong kernel, one query: seven idle waves, all stream-K pieces
 ]
 
 
