@@ -346,9 +346,13 @@ struct WaveAttn {
   // O and the sum are rescaled, and P is recomputed.  That path works one
   // 32-key sub-tile at a time (logits computed twice) to stay within the
   // registers the fast path leaves free.
-  __device__ __forceinline__ void softmax(const f32x16 (&s)[QB][2], const T* kl, const float* bl,
-                                          op8 (&p)[QB][4]) {
-    float part[QB];
+  //
+  // In three steps, so that a caller can take the rare branch away from the
+  // work that feeds it: softmax_fast computes P and the per-lane sums and
+  // returns whether any lane of the wave failed the check, rescale redoes
+  // the tile, and commit adds the sums.
+  __device__ __forceinline__ bool softmax_fast(const f32x16 (&s)[QB][2], op8 (&p)[QB][4],
+                                               float (&part)[QB]) const {
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
       float acc[4];
@@ -359,41 +363,50 @@ struct WaveAttn {
     bool over = false;
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) over |= !(part[qb] <= kLazyLimit);
-    if (__builtin_expect(__ballot(over) != 0, 0)) {
-      // Reload K here rather than keep the score operands alive.
-      asm volatile("" ::: "memory");
+    return __ballot(over) != 0;
+  }
+  __device__ __forceinline__ void rescale(const T* kl, const float* bl, op8 (&p)[QB][4], float (&part)[QB]) {
+    // Reload K here rather than keep the score operands alive.
+    asm volatile("" ::: "memory");
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
-        float mx = -__builtin_inff();
+    for (int qb = 0; qb < QB; ++qb) {
+      float mx = -__builtin_inff();
 #pragma unroll
-        for (int sub = 0; sub < 2; ++sub) {
-          const f32x16 x = logits(kl, bl, qb, sub);
+      for (int sub = 0; sub < 2; ++sub) {
+        const f32x16 x = logits(kl, bl, qb, sub);
 #pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, x[r]);
-        }
-        // Rounding is monotone and mref is a T value, so mnew >= mref.
-        const float mnew = to_f32(static_cast<T>(fmaxf(mref[qb], half_max(mx))));
-        if (__ballot(mnew != mref[qb])) {
-          const float corr = mnew == -__builtin_inff() ? 1.0f : __builtin_amdgcn_exp2f((mref[qb] - mnew) * kLog2e);
-          lsum[qb] *= corr;
-#pragma unroll
-          for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) o[qb][dt][r] *= corr;
-          mref[qb] = mnew;
-          nm[qb] = exp_offset(mnew);
-        }
-        // No finite logit yet: every P is 0 (x = -inf).
-        const float nmv = mref[qb] == -__builtin_inff() ? 0.0f : nm[qb];
-        asm volatile("" ::: "memory");
-        float acc[4];
-        exp_pack(logits(kl, bl, qb, 0), 0, nmv, p[qb], acc);
-        exp_pack(logits(kl, bl, qb, 1), 1, nmv, p[qb], acc);
-        part[qb] = sum4(acc);
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, x[r]);
       }
+      // Rounding is monotone and mref is a T value, so mnew >= mref.
+      const float mnew = to_f32(static_cast<T>(fmaxf(mref[qb], half_max(mx))));
+      if (__ballot(mnew != mref[qb])) {
+        const float corr = mnew == -__builtin_inff() ? 1.0f : __builtin_amdgcn_exp2f((mref[qb] - mnew) * kLog2e);
+        lsum[qb] *= corr;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[qb][dt][r] *= corr;
+        mref[qb] = mnew;
+        nm[qb] = exp_offset(mnew);
+      }
+      // No finite logit yet: every P is 0 (x = -inf).
+      const float nmv = mref[qb] == -__builtin_inff() ? 0.0f : nm[qb];
+      asm volatile("" ::: "memory");
+      float acc[4];
+      exp_pack(logits(kl, bl, qb, 0), 0, nmv, p[qb], acc);
+      exp_pack(logits(kl, bl, qb, 1), 1, nmv, p[qb], acc);
+      part[qb] = sum4(acc);
     }
+  }
+  __device__ __forceinline__ void commit(const float (&part)[QB]) {
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) lsum[qb] += part[qb];
+  }
+  __device__ __forceinline__ void softmax(const f32x16 (&s)[QB][2], const T* kl, const float* bl,
+                                          op8 (&p)[QB][4]) {
+    float part[QB];
+    if (__builtin_expect(softmax_fast(s, p, part), 0)) rescale(kl, bl, p, part);
+    commit(part);
   }
 
   // The softmax of a task's first tile from its raw logits (scores<true>):
@@ -809,6 +822,20 @@ __device__ __forceinline__ void attn_pp_segment(const AttnArgs<T>& a, T* k_lds, 
       pin_in(w.lsum[qb]);
     }
   };
+  auto pin_sums = [&](const float (&part)[kQB]) {
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb) pin_in(part[qb]);
+  };
+  // The rescaling path of the lazy softmax for tile `tile`, taken at the
+  // start of the MFMA phase after the softmax phase that found the tile's
+  // probabilities out of range (a branch at the end of that phase would
+  // hold the wave until the check's whole dependency chain has drained).
+  // The tile's V^T operands in flight are dropped and read again, so their
+  // registers are free meanwhile.
+  auto redo = [&](int tile, float (&part)[kQB], typename WaveAttn<T>::VOps& vops) {
+    w.rescale(kl(tile), bl(tile), p, part);
+    w.load_v(vl(tile), vops);
+  };
   auto renew_scores = [&]() {
 #pragma unroll
     for (int qb = 0; qb < kQB; ++qb)
@@ -857,14 +884,20 @@ __device__ __forceinline__ void attn_pp_segment(const AttnArgs<T>& a, T* k_lds, 
     ring_barrier<2 * kPPDmaPerTile>();
     renew_scores();
     for (int tile = tile0; tile < tile1; ++tile) {
-      w.softmax(s, kl(tile), bl(tile), p);  // A_j
+      float part[kQB];
+      const bool over = w.softmax_fast(s, p, part);  // A_j
       pin_probs();
+      pin_sums(part);
       __builtin_amdgcn_sched_barrier(0);
       typename WaveAttn<T>::VOps vops;
       w.load_v(vl(tile), vops);  // B_j's first operands, in flight across the barrier
       ring_barrier_reads_in_flight<kPPDmaPerTile>();  // tile + 1 has landed
       renew_probs();
-      // B_j.  Tile j + 3 refills the stage of tile j - 1, whose last reads
+      // B_j.  A tile that failed the lazy check is redone first (its stage
+      // stays valid until A_{j+1}).
+      if (__builtin_expect(over, 0)) redo(tile, part, vops);
+      w.commit(part);
+      // Tile j + 3 refills the stage of tile j - 1, whose last reads
       // (group 1's, in A_j) completed before the barrier just passed; the
       // DMA issue runs under this phase's MFMAs rather than the softmax.
       // After the last tile the scores of the look-ahead tile go unused.
@@ -882,25 +915,33 @@ __device__ __forceinline__ void attn_pp_segment(const AttnArgs<T>& a, T* k_lds, 
     pin_scores();
     ring_barrier<-1>();
     renew_scores();
-    w.softmax(s, kl(tile0), bl(tile0), p);  // B_0
+    float part[kQB];
+    bool over = w.softmax_fast(s, p, part);  // B_0
     pin_probs();
+    pin_sums(part);
     __builtin_amdgcn_sched_barrier(0);
     typename WaveAttn<T>::VOps vops;
     w.load_v(vl(tile0), vops);
     ring_barrier_reads_in_flight<-1>();
     for (int tile = tile0 + 1; tile < tile1; ++tile) {
       renew_probs();
-      w.pv_scores(vops, p, kl(tile), bl(tile), s);  // A_j
+      // A_j: tile j - 1 redone if it failed the lazy check, its P.V, S(j).
+      if (__builtin_expect(over, 0)) redo(tile - 1, part, vops);
+      w.commit(part);
+      w.pv_scores(vops, p, kl(tile), bl(tile), s);
       pin_scores();
       ring_barrier<-1>();
       renew_scores();
-      w.softmax(s, kl(tile), bl(tile), p);  // B_j
+      over = w.softmax_fast(s, p, part);  // B_j
       pin_probs();
+      pin_sums(part);
       __builtin_amdgcn_sched_barrier(0);
       w.load_v(vl(tile), vops);
       ring_barrier_reads_in_flight<-1>();
     }
     renew_probs();
+    if (__builtin_expect(over, 0)) redo(tile1 - 1, part, vops);
+    w.commit(part);
     w.pv(vops, p);  // H_n
     pin_scores();
     ring_barrier<-1>();
