@@ -317,3 +317,38 @@ def test_zero_mass_leading_keys_match_oracle(vgo, device, dtype, nk):
     err = assert_close(out.cpu(), ref, dtype, what=f"zero-mass nk={nk}")
     print(f"[attn] zero-mass leading keys dtype={dtype} nk={nk}: rel err {err:.3e} (bar {RTOL[dtype]:.0e})",
           flush=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("split", [True, False])
+@pytest.mark.parametrize("case", [
+    (8, 1100, 3000),   # split: 24 tasks, every segment a stream-K piece of 4-5 key tiles
+    (64, 2100, 700),   # split: 320 tasks, a round of whole tasks, then stream-K pieces
+])
+def test_late_heavy_keys_rescale_mid_segment(vgo, device, dtype, split, case):
+    """Keys whose log-mass bias steps up by 11 (more than the lazy softmax's 15 ln 2
+    headroom) several tiles into the key sequence: every query's probabilities leave
+    the fast path's range on those tiles, which are not the first tile of their
+    segment, so the rescaling path runs mid-segment (in the ping-pong kernel, split,
+    at the start of the following MFMA phase for both wave groups; in the
+    register-staged kernel before its P.V) and must rescale O and the sums that
+    earlier tiles left.  fp32 runs its own kernel either way."""
+    h, nq, nk = case
+    if dtype == torch.float32 and not split:
+        pytest.skip("fp32 takes the same kernel for both entries")
+    print(f"[attn] late heavy keys dtype={dtype} split={split} heads={h} nq={nq} nk={nk}", flush=True)
+    q, k, v, mass = _inputs(311 + nk, 1, h, nq, nk, dtype, mass_max=4, std=0.5)
+    bias = mass.log()
+    steps = {nk // 7: 11.0, nk // 3: 22.0, (2 * nk) // 3: 33.0, nk - 40: 33.0}
+    for pos, b in steps.items():
+        bias[pos] = b
+    bias = bias.to(dtype).float()  # the entry takes the bias in the query dtype; the oracle gets the same values
+    out = _attention_split(vgo, q.to(device), k.to(device), v.to(device), bias.to(dtype).to(device), split)
+    torch.cuda.synchronize()
+    out = out.cpu()
+    assert torch.isfinite(out).all()
+    ref = torch.cat([oracle.mass_bias_attention(q[:, i:i + 1], k[:, i:i + 1], v[:, i:i + 1], bias)
+                     for i in range(h)], dim=1)
+    err = assert_close(out, ref, dtype, what=f"late heavy keys split={split} heads={h} nq={nq} nk={nk}")
+    print(f"[attn] late heavy keys dtype={dtype} split={split} heads={h} nq={nq} nk={nk}: rel err {err:.3e} "
+          f"(bar {RTOL[dtype]:.0e})", flush=True)
