@@ -72,6 +72,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "vgo_attn_kernel_timing_read": (_c_int, [
         ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64),
     ]),
+    "vgo_attn_kernel_clock_read": (_c_int, [
+        ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
+        ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_c_i64),
+    ]),
     "vgo_top4_project": (_c_int, [
         _c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_p,
     ]),

@@ -49,7 +49,9 @@
 // fp32 path: exact fp32 arithmetic, one query row per lane, K/V tiles in LDS.
 #include <algorithm>
 #include <mutex>
+#include <string>
 #include <type_traits>
+#include <vector>
 
 #include "vgo_common.h"
 
@@ -145,6 +147,10 @@ struct AttnArgs {
 // the last round only.
 struct PPSchedule {
   float* partial;  // stream-K partial states, 2 per work-group (may be null)
+  // Clock samples of the kernel-timing record (null unless sampled): work-group
+  // b's wave 0 stores its shader-clock and constant-clock counters at its start
+  // (stamps[4b], stamps[4b + 1]) and end (stamps[4b + 2], stamps[4b + 3]).
+  unsigned long long* stamps;
   int64_t groups, full_rounds, tail_task0, tail_tasks0, units0, units, tail_groups;
 };
 template <typename T>
@@ -966,6 +972,10 @@ __global__ __launch_bounds__(kPPWaves * 64, 1) void attn_pp_kernel(PPLaunch<T> L
   __shared__ __attribute__((aligned(16))) T vt_lds[kPPStages * kTileElems];
   __shared__ __attribute__((aligned(16))) float b_lds[kPPStages * kBN];
   const PPSchedule& sc = L.s;
+  // Clock samples: read here, stored after the last segment (a store before the
+  // segments would have to be assumed to alias the kernel arguments they read).
+  const unsigned long long clock0 = sc.stamps != nullptr ? __builtin_amdgcn_s_memtime() : 0;
+  const unsigned long long const0 = sc.stamps != nullptr ? __builtin_amdgcn_s_memrealtime() : 0;
   const int64_t w = xcd_remap(blockIdx.x, gridDim.x);
   // Whole tasks first: consecutive work-groups (one XCD's, after the remap)
   // take consecutive tasks of a round, so they stream one head's K/V in step
@@ -1009,6 +1019,14 @@ __global__ __launch_bounds__(kPPWaves * 64, 1) void attn_pp_kernel(PPLaunch<T> L
       break;
     }
     attn_pp_segment<T>(L.p[second], k_lds, vt_lds, b_lds, bh, qblk, tile0, tile1, partial);
+  }
+  if (sc.stamps != nullptr && threadIdx.x == 0) {
+    const unsigned long long clock1 = __builtin_amdgcn_s_memtime();
+    const unsigned long long const1 = __builtin_amdgcn_s_memrealtime();
+    sc.stamps[4 * blockIdx.x] = clock0;
+    sc.stamps[4 * blockIdx.x + 1] = const0;
+    sc.stamps[4 * blockIdx.x + 2] = clock1;
+    sc.stamps[4 * blockIdx.x + 3] = const1;
   }
 }
 
@@ -1360,7 +1378,12 @@ int launch_reg(const Problem& pr, hipStream_t stream) {
 // launch made outside stream capture on the device it was switched on for is
 // bracketed by a pair of HIP events from a fixed pool, so the kernel's own
 // duration can be read without the V^T pack and the merge around it.
+// The first kClockSlots timed launches of up to kClockGroups work-groups also
+// carry clock samples (PPSchedule::stamps), in a buffer allocated on the device
+// when timing is switched on there.
 constexpr int kTimingSlots = 4096;
+constexpr int kClockSlots = 512;
+constexpr int64_t kClockGroups = 1024;
 struct KernelTiming {
   std::mutex mutex;
   bool on = false;
@@ -1369,15 +1392,21 @@ struct KernelTiming {
   int64_t dropped = 0;
   hipEvent_t start[kTimingSlots] = {};
   hipEvent_t stop[kTimingSlots] = {};
+  unsigned long long* stamps = nullptr;  // kClockSlots x kClockGroups x 4, on `device`
+  int64_t clock_groups[kClockSlots] = {};  // work-groups of each sampled launch (0: none)
 };
 KernelTiming& kernel_timing() {
   static KernelTiming t;
   return t;
 }
 
-// The event pair for the next launch on `stream`, or false when timing is off,
-// the stream is being captured or belongs to another device, or the pool is full.
-bool timing_slot(hipStream_t stream, hipEvent_t* start, hipEvent_t* stop) {
+// The event pair for the next launch on `stream` (and, for one of the first
+// kClockSlots launches with at most kClockGroups work-groups, its clock-sample
+// slice in *stamps, else null), or false when timing is off, the stream is being
+// captured or belongs to another device, or the pool is full.
+bool timing_slot(hipStream_t stream, int64_t groups, hipEvent_t* start, hipEvent_t* stop,
+                 unsigned long long** stamps) {
+  *stamps = nullptr;
   KernelTiming& t = kernel_timing();
   std::lock_guard<std::mutex> lock(t.mutex);
   if (!t.on) return false;
@@ -1396,6 +1425,13 @@ bool timing_slot(hipStream_t stream, hipEvent_t* start, hipEvent_t* stop) {
   ++t.used;
   *start = t.start[i];
   *stop = t.stop[i];
+  if (i < kClockSlots) {
+    t.clock_groups[i] = 0;
+    if (t.stamps != nullptr && groups <= kClockGroups) {
+      t.clock_groups[i] = groups;
+      *stamps = t.stamps + static_cast<int64_t>(i) * kClockGroups * 4;
+    }
+  }
   return true;
 }
 
@@ -1435,7 +1471,7 @@ int launch_pp(const Problem* pr, int count, void* workspace, size_t workspace_by
   L.s = plan.s;
   if (plan.s.units > 0) L.s.partial = reinterpret_cast<float*>(base + ws.partial);
   hipEvent_t t_start = nullptr, t_stop = nullptr;
-  const bool timed = timing_slot(stream, &t_start, &t_stop);
+  const bool timed = timing_slot(stream, plan.s.groups, &t_start, &t_stop, &L.s.stamps);
   if (timed) (void)hipEventRecord(t_start, stream);
   hipLaunchKernelGGL((attn_pp_kernel<T>), dim3(static_cast<unsigned>(plan.s.groups)),
                      dim3(kPPWaves * 64), 0, stream, L);
@@ -1670,14 +1706,64 @@ extern "C" int vgo_attn_kernel_timing(int enable) {
           if (t.start[i]) (void)hipEventDestroy(t.start[i]);
           if (t.stop[i]) (void)hipEventDestroy(t.stop[i]);
         }
+        if (t.stamps) (void)hipFree(t.stamps);
       }
       if (hipSetDevice(dev) != hipSuccess)
         return fail(VGO_ELAUNCH, "vgo_attn_kernel_timing: cannot return to the current device");
     }
     for (int i = 0; i < kTimingSlots; ++i) t.start[i] = t.stop[i] = nullptr;
+    t.stamps = nullptr;
+  }
+  if (t.stamps == nullptr) {
+    void* buf = nullptr;
+    const hipError_t err = hipMalloc(&buf, sizeof(unsigned long long) * kClockSlots * kClockGroups * 4);
+    if (err != hipSuccess)
+      return fail(VGO_ELAUNCH, std::string("vgo_attn_kernel_timing: ") + hipGetErrorString(err));
+    t.stamps = static_cast<unsigned long long*>(buf);
   }
   t.device = dev;
   t.on = true;
+  return VGO_OK;
+}
+
+extern "C" int vgo_attn_kernel_clock_read(double* shader_cycles, double* const_ticks,
+                                          double* span_ticks, double* span_ms, int64_t* launches) {
+  using namespace vgo;
+  VGO_REQUIRE(shader_cycles && const_ticks && span_ticks && span_ms && launches,
+              "vgo_attn_kernel_clock_read: null output");
+  KernelTiming& t = kernel_timing();
+  std::lock_guard<std::mutex> lock(t.mutex);
+  *shader_cycles = *const_ticks = *span_ticks = *span_ms = 0.0;
+  *launches = 0;
+  const int n = std::min(t.used, kClockSlots);
+  if (n == 0 || t.stamps == nullptr) return VGO_OK;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev != t.device)
+    return fail(VGO_EINVAL, "vgo_attn_kernel_clock_read: call it on the device the launches ran on");
+  std::vector<unsigned long long> host(static_cast<size_t>(kClockGroups) * 4);
+  for (int i = 0; i < n; ++i) {
+    hipError_t err = hipEventSynchronize(t.stop[i]);
+    float ms = 0.0f;
+    if (err == hipSuccess) err = hipEventElapsedTime(&ms, t.start[i], t.stop[i]);
+    const int64_t groups = t.clock_groups[i];
+    if (err == hipSuccess && groups > 0)
+      err = hipMemcpy(host.data(), t.stamps + static_cast<int64_t>(i) * kClockGroups * 4,
+                      sizeof(unsigned long long) * 4 * groups, hipMemcpyDeviceToHost);
+    if (err != hipSuccess)
+      return fail(VGO_ELAUNCH, std::string("vgo_attn_kernel_clock_read: ") + hipGetErrorString(err));
+    if (groups == 0) continue;
+    unsigned long long first = ~0ull, last = 0;
+    for (int64_t b = 0; b < groups; ++b) {
+      const unsigned long long* g = host.data() + 4 * b;
+      *shader_cycles += static_cast<double>(g[2] - g[0]);
+      *const_ticks += static_cast<double>(g[3] - g[1]);
+      first = std::min(first, g[1]);
+      last = std::max(last, g[3]);
+    }
+    *span_ticks += static_cast<double>(last - first);
+    *span_ms += ms;
+    ++*launches;
+  }
   return VGO_OK;
 }
 

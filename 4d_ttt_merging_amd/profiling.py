@@ -86,6 +86,32 @@ def attention_kernel_timing(flag: bool = True) -> None:
     _lib.check(lib.vgo_attn_kernel_timing(1 if flag else 0))
 
 
+def attention_kernel_clock() -> dict | None:
+    """Mean shader clock of the attention launches timed since the last
+    `attention_kernel_summary` (the first 512 of them), from the counters each
+    work-group's wave 0 reads at its start and end; None when none were sampled.
+    Call it before `attention_kernel_summary`, which empties the record.
+
+    `clock_ghz` takes the constant counter at its 100 MHz rate; `const_mhz` is that
+    rate as the launches' constant-clock spans over their HIP-event durations
+    show it (a little low: the events also hold the launch's start-up and drain)."""
+    import ctypes
+
+    from . import _lib
+
+    lib = _lib.load()
+    cycles, ticks, span_ticks, span_ms = (ctypes.c_double(0.0) for _ in range(4))
+    launches = ctypes.c_int64(0)
+    _lib.check(lib.vgo_attn_kernel_clock_read(ctypes.byref(cycles), ctypes.byref(ticks),
+                                              ctypes.byref(span_ticks), ctypes.byref(span_ms),
+                                              ctypes.byref(launches)))
+    if launches.value == 0 or ticks.value <= 0 or span_ms.value <= 0:
+        return None
+    return {"clock_ghz": cycles.value / ticks.value * 0.1,
+            "const_mhz": span_ticks.value / span_ms.value / 1e3,
+            "launches": int(launches.value)}
+
+
 def attention_kernel_summary() -> tuple[float, int]:
     """(total ms, launches) of the attention kernel launches timed since the last
     call; waits for them, then empties the record."""

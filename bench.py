@@ -931,19 +931,32 @@ def with_patch_encoder(model, prof, device, steps: int) -> dict:
             "images": "seeded U(0,1) 32 x 3 x 512 x 512, mean/std-normalised as aggregator.py:729"}
 
 
-def clock_adjusted(achieved_tflops: float) -> dict | None:
+def clock_adjusted(achieved_tflops: float, live: dict | None) -> dict | None:
     """The attention kernel's fraction of the bf16 peak at the clock the chip actually
-    holds under it (from the committed counter profile), beside the nominal 2.4 GHz one:
-    the part of the gap that is clock, not schedule."""
-    clock = attention_clock_ghz()
+    held under it, beside the nominal 2.4 GHz one: the part of the gap that is clock,
+    not schedule.  The clock is measured live, over the timed launches themselves
+    (`live`: each work-group's shader-clock cycles over its 100 MHz constant-clock
+    ticks); the committed counter profile's figure is printed beside it, and is used
+    only when no live sample exists."""
+    profiled = attention_clock_ghz()
+    clock = live["clock_ghz"] if live else profiled
     if clock is None:
         return None
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     peak = peak_bf16_tflops(clock, cus)
-    return {"clock_ghz": clock, "cus": cus, "peak": round(peak, 1),
-            "frac": round(achieved_tflops / peak, 4),
-            "clock_source": "GRBM_GUI_ACTIVE per XCD / duration, steady-state launches of "
-                            "profiles/c4_attention_mfma_utilisation.md"}
+    out = {"clock_ghz": round(clock, 3), "cus": cus, "peak": round(peak, 1),
+           "frac": round(achieved_tflops / peak, 4)}
+    if live:
+        out["clock_source"] = ("live: shader-clock cycles / 100 MHz constant-clock ticks that each "
+                               "work-group of the timed attention launches reads at its start and "
+                               "end (vgo_attn_kernel_clock_read)")
+        out["sampled_launches"] = live["launches"]
+        out["const_clock_mhz_check"] = round(live["const_mhz"], 2)
+    else:
+        out["clock_source"] = ("GRBM_GUI_ACTIVE per XCD / duration, steady-state launches of "
+                               "profiles/c4_attention_mfma_utilisation.md")
+    out["profile_clock_ghz"] = profiled
+    return out
 
 
 # --------------------------------------------------------------------- main ----
@@ -1012,6 +1025,7 @@ def main() -> int:
     prof.attention_kernel_timing(False)
     prof.enable(False)
     attn_span = prof.summary()["global.main_attention"]
+    live_clock = prof.attention_kernel_clock()  # before the summary, which empties the record
     kernel_total_ms, kernel_launches = prof.attention_kernel_summary()
     prof.reset()
     prof.enable(True)
@@ -1056,7 +1070,8 @@ def main() -> int:
                      "traffic": attention_traffic(), "mfma_busy": attention_mfma_busy(),
                      "flops_per_launch": attn_flops,
                      "avg_launch_ms": round(attn_ms, 4), "launches": kernel_launches,
-                     "at_measured_clock": clock_adjusted(attn_flops / (attn_ms / 1e3) / 1e12),
+                     "at_measured_clock": clock_adjusted(attn_flops / (attn_ms / 1e3) / 1e12,
+                                                         live_clock),
                      "with_pack_and_merge": {
                          "ms": round(label_ms, 4),
                          "frac": round(attn_flops / (label_ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4)},

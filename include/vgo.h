@@ -160,6 +160,25 @@ int vgo_attn_kernel_timing(int enable);
 int vgo_attn_kernel_timing_read(double* total_ms, int64_t* launches, int64_t* dropped);
 
 /*
+ * Clock of the timed attention launches.  No counterpart in the reference; it
+ * serves callers that state the kernel's fraction of the MFMA peak at the
+ * clock the chip held under it.  Of the launches timed since the last
+ * vgo_attn_kernel_timing_read, the first 512 with at most 1,024 work-groups
+ * also record, per work-group, the shader-clock counter and the constant
+ * 100 MHz counter at its start and end (wave 0).  This call returns, summed
+ * over those launches, the work-groups' shader-clock cycles, their
+ * constant-clock ticks, each launch's constant-clock span (its last
+ * work-group's end less its first one's start), the HIP-event duration of
+ * the same launches in milliseconds, and their count.  Mean clock =
+ * shader_cycles / const_ticks x the constant clock's rate; span_ticks /
+ * span_ms checks that rate.  Call it before vgo_attn_kernel_timing_read,
+ * which empties the record; it waits for the launches and leaves the
+ * record as it is.
+ */
+int vgo_attn_kernel_clock_read(double* shader_cycles, double* const_ticks, double* span_ticks,
+                               double* span_ms, int64_t* launches);
+
+/*
  * Top-4 convex projection (unmerge): out[i,:] = sum_c w[i,c] * table[index[i,c],:].
  *
  * Replaces the restore of WeightedBilinearTokenPlan / TokenPlan

@@ -233,7 +233,10 @@ def test_pair_launch_empty_problems_and_errors(vgo, device):
 
 def test_kernel_timing_records_each_workspace_launch(vgo, device):
     """vgo_attn_kernel_timing brackets each attention-kernel launch with an event
-    pair while it is on, records nothing while it is off, and leaves results alone."""
+    pair while it is on, records nothing while it is off, and leaves results alone;
+    vgo_attn_kernel_clock_read reports the clock of the same launches from their
+    work-groups' counters (a shader clock within the chip's range, and a constant
+    counter whose ticks over the launch spans do not run ahead of the events' 100 MHz)."""
     prof = __import__("4d_ttt_merging_amd.profiling", fromlist=["profiling"])
     print("[attn] kernel timing, 1x2x600x3000 bf16", flush=True)
     q, k, v, mass = _inputs(11, 1, 2, 600, 3000, torch.bfloat16)
@@ -245,8 +248,14 @@ def test_kernel_timing_records_each_workspace_launch(vgo, device):
         timed = [vgo.mass_bias_attention(q, k, v, bias) for _ in range(3)]
     finally:
         prof.attention_kernel_timing(False)
+    clock = prof.attention_kernel_clock()
+    print(f"[attn] kernel clock {clock}", flush=True)
+    assert clock is not None and clock["launches"] == 3
+    assert 0.3 < clock["clock_ghz"] < 3.0
+    assert 0.0 < clock["const_mhz"] <= 101.0
     total_ms, launches = prof.attention_kernel_summary()
     assert launches == 3 and total_ms > 0.0
+    assert prof.attention_kernel_clock() is None
     for out in timed:
         assert torch.equal(out, untimed)
     vgo.mass_bias_attention(q, k, v, bias)
